@@ -1,0 +1,143 @@
+"""Decode and matvec on the MI355X against the oracle, through the C ABI.
+
+Decoded weights must be bit-identical to the reference decoders; matvec rows must stay within
+1e-5 * |w_row| * |x| of the oracle's float64-accumulated result (the tolerance the path is
+specified with). Shapes cover the reference's KAT blocks, ragged row counts, fp16 subnormal and
+extreme scales, and the full DeepSeek/OLMoE expert matrix shapes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.oracle import IQ1_S, IQ2_XXS, IQ3_XXS, Q8_0
+from tests.kat_blocks import KAT, fnv_f32, kat_input
+from vastloom_amd.workloads import random_matrix
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def ops():
+    assert torch.cuda.is_available(), "GPU tests need a visible HIP device"
+    from vastloom_amd import ops as _ops
+
+    return _ops
+
+
+def row_bound(w: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """Per-row tolerance TOL * |w_row| * |x| for every token row of x."""
+    wn = np.linalg.norm(w.astype(np.float64), axis=1)
+    xn = np.linalg.norm(np.atleast_2d(x).astype(np.float64), axis=1)
+    return TOL * xn[:, None] * wn[None, :]
+
+
+@pytest.mark.parametrize("name", sorted(KAT))
+def test_kat_blocks_decode_bit_exact(ops, oracle, name):
+    k = KAT[name]
+    enc = k["blocks"]()
+    rows, cols = 3, k["cols"]
+    print(f"[decode KAT] {name} {rows}x{cols}", flush=True)
+    m = ops.DeviceMatrix(k["qtype"], rows, cols, enc)
+    got = m.dequantize().cpu().numpy().reshape(-1)
+    want = oracle.dequantize(k["qtype"], enc, rows * cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert fnv_f32(got) == k["fnv"]
+    y = m.matvec(torch.from_numpy(kat_input(cols)).cuda()).cpu().numpy()
+    for got_v, (want_v, tol) in zip(y, k["outputs"]):
+        assert abs(float(got_v) - want_v) <= max(tol, 1e-5 * abs(want_v) + 1e-6)
+
+
+SHAPES = [
+    (Q8_0, 3, 64), (Q8_0, 45, 512), (Q8_0, 1024, 2048), (Q8_0, 2048, 1024),
+    (IQ2_XXS, 3, 512), (IQ2_XXS, 100, 1024), (IQ2_XXS, 2048, 7168), (IQ2_XXS, 7168, 2048),
+    (IQ3_XXS, 33, 512), (IQ3_XXS, 7168, 2048),
+    (IQ1_S, 31, 768), (IQ1_S, 2048, 7168),
+]
+
+
+@pytest.mark.parametrize("qtype,rows,cols", SHAPES)
+def test_random_decode_bit_exact(ops, oracle, qtype, rows, cols):
+    print(f"[decode] type={qtype} {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows * 7 + cols + qtype)
+    enc = random_matrix(rng, qtype, rows, cols, 0.01)
+    m = ops.DeviceMatrix(qtype, rows, cols, enc)
+    got = m.dequantize().cpu().numpy().reshape(-1)
+    want = oracle.dequantize(qtype, enc, rows * cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_extreme_scales_decode_bit_exact(ops, oracle):
+    rng = np.random.default_rng(3)
+    special = np.array([0x0001, 0x03FF, 0x0400, 0x7BFF, 0x8001, 0xFBFF, 0x0000], np.uint16)
+    for qtype, rows, cols in ((Q8_0, 40, 256), (IQ2_XXS, 40, 512), (IQ3_XXS, 40, 512),
+                              (IQ1_S, 40, 512)):
+        print(f"[decode extreme] type={qtype}", flush=True)
+        enc = random_matrix(rng, qtype, rows, cols, 0.01)
+        be = 32 if qtype == Q8_0 else 256
+        blocks = enc.reshape(rows * cols // be, -1)
+        s = special[np.arange(blocks.shape[0]) % special.size]
+        blocks[:, 0], blocks[:, 1] = s & 0xFF, s >> 8
+        m = ops.DeviceMatrix(qtype, rows, cols, enc)
+        got = m.dequantize().cpu().numpy().reshape(-1)
+        want = oracle.dequantize(qtype, enc, rows * cols)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype,rows,cols", SHAPES)
+@pytest.mark.parametrize("tokens", [1, 3, 8])
+def test_matvec_within_tolerance(ops, oracle, qtype, rows, cols, tokens):
+    print(f"[matvec] type={qtype} {rows}x{cols} tokens={tokens}", flush=True)
+    rng = np.random.default_rng(rows + cols * 3 + qtype + tokens)
+    enc = random_matrix(rng, qtype, rows, cols, 0.01)
+    x = rng.standard_normal((tokens, cols)).astype(np.float32)
+    m = ops.DeviceMatrix(qtype, rows, cols, enc)
+    y = m.matvec(torch.from_numpy(x).cuda()).cpu().numpy()
+    w = oracle.dequantize(qtype, enc, rows * cols).reshape(rows, cols)
+    bound = row_bound(w, x)
+    for t in range(tokens):
+        want = oracle.matvec(qtype, enc, rows, cols, x[t], threads=8)
+        err = np.abs(y[t].astype(np.float64) - want)
+        assert np.all(err <= bound[t]), (t, float((err / bound[t]).max()))
+
+
+def test_matvec_scaled_and_sparse_inputs(ops, oracle):
+    # Wide dynamic range within a token, an all-zero token and a tiny-magnitude token.
+    rng = np.random.default_rng(99)
+    rows, cols = 256, 2048
+    enc = random_matrix(rng, IQ2_XXS, rows, cols, 0.01)
+    x = rng.standard_normal((4, cols)).astype(np.float32)
+    x[0, ::7] *= 1e4
+    x[1] = 0.0
+    x[2] *= 1e-30
+    x[3, 100:] = 0.0
+    m = ops.DeviceMatrix(IQ2_XXS, rows, cols, enc)
+    y = m.matvec(torch.from_numpy(x).cuda()).cpu().numpy()
+    w = oracle.dequantize(IQ2_XXS, enc, rows * cols).reshape(rows, cols)
+    bound = row_bound(w, x)
+    for t in range(4):
+        want = oracle.matvec(IQ2_XXS, enc, rows, cols, x[t])
+        assert np.all(np.abs(y[t].astype(np.float64) - want) <= bound[t] + 1e-37)
+    assert np.all(y[1] == 0.0)
+
+
+def test_matvec_refuses_non_finite(ops):
+    rng = np.random.default_rng(5)
+    rows, cols = 64, 512
+    enc = random_matrix(rng, IQ2_XXS, rows, cols, 0.01)
+    m = ops.DeviceMatrix(IQ2_XXS, rows, cols, enc)
+    x = rng.standard_normal(cols).astype(np.float32)
+    x[3] = np.nan
+    with pytest.raises(ops.VlError) as err:
+        m.matvec(torch.from_numpy(x).cuda())
+    assert err.value.name == "invalid_argument"
+    bad = enc.copy()
+    bad[0], bad[1] = 0x00, 0x7C  # +inf block scale
+    m2 = ops.DeviceMatrix(IQ2_XXS, rows, cols, bad)
+    with pytest.raises(ops.VlError) as err:
+        m2.matvec(torch.from_numpy(np.ones(cols, np.float32)).cuda())
+    assert err.value.name == "invalid_format"

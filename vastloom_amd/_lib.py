@@ -1,0 +1,77 @@
+"""Loader for the in-tree HIP library (libvastloom_hip.so) and its C ABI.
+
+There is no CPU fallback: if the library is missing or a device call fails, the error is raised.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libvastloom_hip.so"
+
+VL_OK, VL_DECLINED = 0, 100
+STATUS_NAMES = {
+    1: "invalid_argument", 2: "invalid_format", 3: "not_found", 4: "permission_denied",
+    5: "io_error", 6: "integrity_error", 7: "unsafe_path", 8: "unsupported",
+    9: "resource_exhausted", 10: "internal_error", 100: "declined",
+}
+STATUS_NONFINITE_INPUT, STATUS_NONFINITE_OUTPUT, STATUS_BAD_ROUTE = 1, 2, 4
+
+_lib: C.CDLL | None = None
+
+
+class VlError(RuntimeError):
+    def __init__(self, code: int, what: str, message: str):
+        super().__init__(f"{what}: {STATUS_NAMES.get(code, code)}: {message}")
+        self.code = code
+        self.name = STATUS_NAMES.get(code, str(code))
+
+
+_U32, _U64, _I32, _P = C.c_uint32, C.c_uint64, C.c_int, C.c_void_p
+
+# name -> argument types (all return int status unless listed in _RESTYPES)
+_SIGNATURES = {
+    "vl_last_error": [],
+    "vl_device_count": [C.POINTER(C.c_int)],
+    "vl_matrix_layout": [_U32, _U64, _U64, C.POINTER(_U64), C.POINTER(_U64)],
+    "vl_pack_matrix": [_U32, _U64, _U64, _P, _P, _P],
+    "vl_dequantize": [_U32, _U64, _U64, _P, _P, _P],
+    "vl_matvec_workspace": [_U32, _U64, _U64, _U32, C.POINTER(_U64)],
+    "vl_matvec": [_U32, _U64, _U64, _P, _P, _U32, _P, _P, _U64, _P],
+    "vl_read_status": [_P, _P, C.POINTER(_U32)],
+}
+_RESTYPES = {"vl_last_error": C.c_char_p}
+
+
+def lib() -> C.CDLL:
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m vastloom_amd.build` "
+                "(there is no CPU fallback)")
+        handle = C.CDLL(str(LIB_PATH))
+        for name, args in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, C.c_int)
+        _lib = handle
+    return _lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def check(code: int, what: str) -> int:
+    """Raise VlError for a failure; return the code (0 or VL_DECLINED) otherwise."""
+    if code not in (VL_OK, VL_DECLINED):
+        msg = lib().vl_last_error()
+        raise VlError(code, what, msg.decode() if msg else "")
+    return code
+
+
+def call(name: str, *args) -> int:
+    return check(getattr(lib(), name)(*args), name)

@@ -1,0 +1,138 @@
+// C ABI entry points (include/vastloom_hip.h) over the HIP kernels.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/vastloom_hip.h"
+#include "vl_kernels.h"
+#include "vl_layout.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(VL_INTERNAL_ERROR, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool make_layout(uint32_t type, uint64_t rows, uint64_t cols, vl_tiled_layout* L) {
+    if (rows == 0 || cols == 0 || rows > 0x7fffffffu || cols > 0x7fffffffu) return false;
+    return vl_make_layout(type, (uint32_t)rows, (uint32_t)cols, L) != 0;
+}
+
+// Workspace of one matvec call: status word, per-token exponents, input limbs.
+constexpr uint64_t kStatusOffset = 0;
+constexpr uint64_t kExpOffset = 64;
+constexpr uint64_t kLimbOffset = 256;
+
+}  // namespace
+
+extern "C" {
+
+const char* vl_last_error(void) { return g_last_error.c_str(); }
+
+int vl_device_count(int* count) {
+    if (!count) return fail(VL_INVALID_ARGUMENT, "count is null");
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice) n = 0;
+    else if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    *count = n;
+    return VL_OK;
+}
+
+int vl_matrix_layout(uint32_t type, uint64_t rows, uint64_t cols, uint64_t* gguf_bytes,
+                     uint64_t* device_bytes) {
+    vl_tiled_layout L;
+    if (!make_layout(type, rows, cols, &L))
+        return fail(VL_UNSUPPORTED, "no device layout for type %u with %llu x %llu", type,
+                    (unsigned long long)rows, (unsigned long long)cols);
+    if (gguf_bytes) *gguf_bytes = L.gguf_bytes;
+    if (device_bytes) *device_bytes = L.bytes;
+    return VL_OK;
+}
+
+int vl_pack_matrix(uint32_t type, uint64_t rows, uint64_t cols, const void* gguf_device,
+                   void* tiled_device, void* stream) {
+    vl_tiled_layout L;
+    if (!make_layout(type, rows, cols, &L)) return fail(VL_UNSUPPORTED, "unsupported matrix");
+    if (!gguf_device || !tiled_device) return fail(VL_INVALID_ARGUMENT, "null device pointer");
+    const hipError_t e = vl::launch_pack(L, static_cast<const uint8_t*>(gguf_device),
+                                         static_cast<uint8_t*>(tiled_device),
+                                         static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? VL_OK : hip_fail(e, "pack launch");
+}
+
+int vl_dequantize(uint32_t type, uint64_t rows, uint64_t cols, const void* tiled_device,
+                  float* out_device, void* stream) {
+    vl_tiled_layout L;
+    if (!make_layout(type, rows, cols, &L)) return fail(VL_UNSUPPORTED, "unsupported matrix");
+    if (!tiled_device || !out_device) return fail(VL_INVALID_ARGUMENT, "null device pointer");
+    const hipError_t e = vl::launch_dequant(L, static_cast<const uint8_t*>(tiled_device),
+                                            out_device, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? VL_OK : hip_fail(e, "dequantize launch");
+}
+
+int vl_matvec_workspace(uint32_t type, uint64_t rows, uint64_t cols, uint32_t tokens,
+                        uint64_t* bytes) {
+    vl_tiled_layout L;
+    if (!make_layout(type, rows, cols, &L)) return fail(VL_UNSUPPORTED, "unsupported matrix");
+    if (tokens == 0 || tokens > 8) return fail(VL_INVALID_ARGUMENT, "tokens must be 1..8");
+    if (!bytes) return fail(VL_INVALID_ARGUMENT, "bytes is null");
+    *bytes = kLimbOffset + vl::limb_bytes((uint32_t)cols, tokens);
+    return VL_OK;
+}
+
+int vl_matvec(uint32_t type, uint64_t rows, uint64_t cols, const void* tiled_device,
+              const float* x_device, uint32_t tokens, float* y_device, void* workspace,
+              uint64_t workspace_bytes, void* stream) {
+    uint64_t need = 0;
+    int st = vl_matvec_workspace(type, rows, cols, tokens, &need);
+    if (st) return st;
+    if (!tiled_device || !x_device || !y_device || !workspace)
+        return fail(VL_INVALID_ARGUMENT, "null device pointer");
+    if (workspace_bytes < need)
+        return fail(VL_INVALID_ARGUMENT, "workspace of %llu bytes is below the %llu needed",
+                    (unsigned long long)workspace_bytes, (unsigned long long)need);
+    vl_tiled_layout L;
+    make_layout(type, rows, cols, &L);
+    auto* ws = static_cast<uint8_t*>(workspace);
+    auto* status = reinterpret_cast<uint32_t*>(ws + kStatusOffset);
+    auto* xe = reinterpret_cast<int*>(ws + kExpOffset);
+    auto* xl = reinterpret_cast<int8_t*>(ws + kLimbOffset);
+    const auto s = static_cast<hipStream_t>(stream);
+    hipError_t e = vl::launch_fill_u32(status, 1, 0, s);
+    if (e == hipSuccess)
+        e = vl::launch_prep_limbs(x_device, 1, tokens, (uint32_t)cols, cols, 0, xl, xe, status, s);
+    if (e != hipSuccess) return hip_fail(e, "prep launch");
+    vl::QmvBatch batch{};
+    batch.inline_jobs[0] = vl::QmvJob{static_cast<const uint8_t*>(tiled_device), xl, xe, y_device,
+                                      (uint32_t)rows, (uint32_t)cols, tokens, (uint32_t)rows};
+    e = vl::launch_qmv(type, vl::limb_slots(tokens), batch, 1, L.tiles, status, s);
+    return e == hipSuccess ? VL_OK : hip_fail(e, "matvec launch");
+}
+
+int vl_read_status(const void* workspace, void* stream, uint32_t* bits) {
+    if (!workspace || !bits) return fail(VL_INVALID_ARGUMENT, "null pointer");
+    const auto s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipStreamSynchronize(s);
+    if (e == hipSuccess)
+        e = hipMemcpy(bits, static_cast<const uint8_t*>(workspace) + kStatusOffset, sizeof(uint32_t),
+                      hipMemcpyDeviceToHost);
+    return e == hipSuccess ? VL_OK : hip_fail(e, "status read");
+}
+
+}  // extern "C"

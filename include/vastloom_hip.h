@@ -94,6 +94,93 @@ int vl_matvec(uint32_t ggml_type, uint64_t rows, uint64_t cols, const void* tile
  * issued on it since the workspace was last handed to an entry point. */
 int vl_read_status(const void* workspace, void* stream, uint32_t* bits);
 
+/* ---- Expert FFN and MoE layer ------------------------------------------------------------ */
+
+/* Tiled device weights of one expert: gate (w1), up (w3), down (w2). */
+typedef struct vl_expert_weights {
+    const void* gate;
+    const void* up;
+    const void* down;
+} vl_expert_weights;
+
+/* SwiGLU and combine conventions.
+ * VL_SEM_DEEPSEEK: execute_expert + moe_forward (src/inference/deepseek_v4_graph.cpp:1826-1894,
+ *   :2129-2266): float64 SwiGLU, gate capped and up clamped at the limit when it is > 0, route
+ *   weight applied before the down projection, outputs added in ascending expert id, then the
+ *   shared expert (no route weight).
+ * VL_SEM_QWEN: qwen38_expert_mlp_q8 + qwen38_moe_block
+ *   (src/inference/qwen3_8_flash_next_reference.cpp:1317-1421): silu_f(g) * u in float, expert
+ *   outputs scaled by the route weight and added in route-slot order, then the shared expert.
+ * VL_SEM_PLAIN: routed_expert_iq1_s_iq3_xxs_f32 (src/inference/ggml_quantization.cpp:1678-1745):
+ *   g / (1 + expf(-g)) * u in float, no clamp, no route weight. */
+#define VL_SEM_DEEPSEEK 0u
+#define VL_SEM_QWEN 1u
+#define VL_SEM_PLAIN 2u
+
+/* Routing.
+ * VL_ROUTE_LEARNED: top-k of score(logit) + bias, ties to the lower id; weights = selected
+ *   scores / their float64 sum * route_scale (deepseek_v4_route_learned_logits,
+ *   src/inference/deepseek_v4_reference.cpp:223-255; route_from_indices :80-121).
+ * VL_ROUTE_TABLE: expert ids from table_ids[token][slot], weights as above
+ *   (deepseek_v4_route_hash_logits, :275-307).
+ * VL_ROUTE_SOFTMAX: float64 softmax over the logits, top-k by probability, optional
+ *   renormalisation (qwen38_moe_route, src/inference/qwen3_8_flash_next_reference.cpp:1186-1240).
+ * VL_ROUTE_GIVEN: ids and weights supplied in given_ids / given_weights (null ids = expert 0,
+ *   null weights = 1). */
+#define VL_ROUTE_LEARNED 0u
+#define VL_ROUTE_TABLE 1u
+#define VL_ROUTE_SOFTMAX 2u
+#define VL_ROUTE_GIVEN 3u
+
+/* Score of a gate logit: sqrt(softplus(x)) (deepseek_v4_reference.cpp:65-69) or the float64
+ * logistic (:71-78). */
+#define VL_SCORE_SQRT_SOFTPLUS 0u
+#define VL_SCORE_SIGMOID 1u
+
+typedef struct vl_moe_config {
+    uint32_t tokens;        /* 1..8 */
+    uint32_t width;         /* model width H (multiple of 256) */
+    uint32_t intermediate;  /* expert width F */
+    uint32_t experts;       /* routed experts E (<= 1024) */
+    uint32_t top_k;         /* 1..16 */
+    uint32_t gate_type;     /* storage type of gate and up */
+    uint32_t down_type;     /* storage type of down */
+    uint32_t semantics;
+    uint32_t routing;
+    uint32_t score_fn;
+    uint32_t has_shared;    /* the shared expert is entry E of the expert array */
+    uint32_t renormalize;   /* softmax routing only */
+    float route_scale;
+    float routed_limit;     /* SwiGLU clamp of routed experts, 0 = none */
+    float shared_limit;     /* SwiGLU clamp of the shared expert, 0 = none */
+} vl_moe_config;
+
+typedef struct vl_moe_inputs {
+    const vl_expert_weights* experts;  /* DEVICE array of E (+1 shared) entries */
+    const float* router;               /* [E][width] float32, device */
+    const float* bias;                 /* [E] selection bias or null (learned routing) */
+    const uint32_t* table_ids;         /* [tokens][top_k] (table routing) */
+    const uint32_t* given_ids;         /* [tokens][top_k] (given routing) or null */
+    const float* given_weights;        /* [tokens][top_k] (given routing) or null */
+    const float* x;                    /* [tokens][width] float32, device */
+    float* out;                        /* [tokens][width] float32, device */
+} vl_moe_inputs;
+
+int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes);
+
+/* One MoE layer: router logits (float64 accumulation), routing, the selected experts' SwiGLU
+ * FFNs and the combine, all on the stream with no host synchronisation. The status word of the
+ * workspace (vl_read_status) reports non-finite values and invalid routes (an out-of-range or
+ * repeated expert id); the output is then not meaningful, as the reference would have refused
+ * the layer. Replaces the per-matvec device calls of moe_forward / qwen38_moe_block. */
+int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
+                 uint64_t workspace_bytes, void* stream);
+
+/* Routing chosen by the last vl_moe_layer on this workspace: ids and weights [tokens][top_k]
+ * copied to host memory (synchronizes the stream). */
+int vl_moe_read_routes(const vl_moe_config* config, const void* workspace, void* stream,
+                       uint32_t* ids_host, float* weights_host);
+
 #ifdef __cplusplus
 }
 #endif

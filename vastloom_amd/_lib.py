@@ -40,7 +40,35 @@ _SIGNATURES = {
     "vl_matvec_workspace": [_U32, _U64, _U64, _U32, C.POINTER(_U64)],
     "vl_matvec": [_U32, _U64, _U64, _P, _P, _U32, _P, _P, _U64, _P],
     "vl_read_status": [_P, _P, C.POINTER(_U32)],
+    "vl_moe_workspace": [_P, C.POINTER(_U64)],
+    "vl_moe_layer": [_P, _P, _P, _U64, _P],
+    "vl_moe_read_routes": [_P, _P, _P, _P, _P],
 }
+
+
+class MoeConfig(C.Structure):
+    """vl_moe_config (include/vastloom_hip.h)."""
+    _fields_ = [(n, C.c_uint32) for n in (
+        "tokens", "width", "intermediate", "experts", "top_k", "gate_type", "down_type",
+        "semantics", "routing", "score_fn", "has_shared", "renormalize")] + [
+        ("route_scale", C.c_float), ("routed_limit", C.c_float), ("shared_limit", C.c_float)]
+
+
+class ExpertWeights(C.Structure):
+    """vl_expert_weights: tiled device pointers of one expert."""
+    _fields_ = [("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p)]
+
+
+class MoeInputs(C.Structure):
+    """vl_moe_inputs: device pointers of one layer call."""
+    _fields_ = [("experts", C.c_void_p), ("router", C.c_void_p), ("bias", C.c_void_p),
+                ("table_ids", C.c_void_p), ("given_ids", C.c_void_p),
+                ("given_weights", C.c_void_p), ("x", C.c_void_p), ("out", C.c_void_p)]
+
+
+SEM_DEEPSEEK, SEM_QWEN, SEM_PLAIN = 0, 1, 2
+ROUTE_LEARNED, ROUTE_TABLE, ROUTE_SOFTMAX, ROUTE_GIVEN = 0, 1, 2, 3
+SCORE_SQRT_SOFTPLUS, SCORE_SIGMOID = 0, 1
 _RESTYPES = {"vl_last_error": C.c_char_p}
 
 

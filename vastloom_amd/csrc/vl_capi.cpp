@@ -9,6 +9,7 @@
 #include "../../include/vastloom_hip.h"
 #include "vl_kernels.h"
 #include "vl_layout.h"
+#include "vl_moe.h"
 
 namespace {
 
@@ -123,6 +124,60 @@ int vl_matvec(uint32_t type, uint64_t rows, uint64_t cols, const void* tiled_dev
                                       (uint32_t)rows, (uint32_t)cols, tokens, (uint32_t)rows};
     e = vl::launch_qmv(type, vl::limb_slots(tokens), batch, 1, L.tiles, status, s);
     return e == hipSuccess ? VL_OK : hip_fail(e, "matvec launch");
+}
+
+static bool to_shape(const vl_moe_config* c, vl::MoeShape* s) {
+    if (!c) return false;
+    *s = vl::MoeShape{c->tokens, c->width, c->intermediate, c->experts, c->top_k,
+                      c->gate_type, c->down_type, c->semantics, c->routing, c->score_fn,
+                      c->has_shared, c->renormalize, c->route_scale, c->routed_limit,
+                      c->shared_limit};
+    return vl::moe_shape_ok(*s);
+}
+
+int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes) {
+    vl::MoeShape s;
+    if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
+    if (!bytes) return fail(VL_INVALID_ARGUMENT, "bytes is null");
+    *bytes = vl::moe_workspace_bytes(s);
+    return VL_OK;
+}
+
+int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
+                 uint64_t workspace_bytes, void* stream) {
+    vl::MoeShape s;
+    if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
+    if (!inputs || !inputs->experts || !inputs->x || !inputs->out || !workspace)
+        return fail(VL_INVALID_ARGUMENT, "null input pointer");
+    if ((s.routing == vl::kRouteLearned || s.routing == vl::kRouteSoftmax ||
+         s.routing == vl::kRouteTable) && !inputs->router)
+        return fail(VL_INVALID_ARGUMENT, "routing needs the router weights");
+    if (s.routing == vl::kRouteTable && !inputs->table_ids)
+        return fail(VL_INVALID_ARGUMENT, "table routing needs table ids");
+    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, workspace);
+    if (workspace_bytes < ws.bytes)
+        return fail(VL_INVALID_ARGUMENT, "workspace of %llu bytes is below the %llu needed",
+                    (unsigned long long)workspace_bytes, (unsigned long long)ws.bytes);
+    const vl::MoeInputs in{reinterpret_cast<const vl::MoeExpert*>(inputs->experts),
+                           inputs->router, inputs->bias, inputs->table_ids, inputs->given_ids,
+                           inputs->given_weights, inputs->x, inputs->out};
+    const hipError_t e = vl::launch_moe(s, in, ws, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? VL_OK : hip_fail(e, "MoE launch");
+}
+
+int vl_moe_read_routes(const vl_moe_config* config, const void* workspace, void* stream,
+                       uint32_t* ids_host, float* weights_host) {
+    vl::MoeShape s;
+    if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
+    if (!workspace || !ids_host || !weights_host) return fail(VL_INVALID_ARGUMENT, "null pointer");
+    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, const_cast<void*>(workspace));
+    const uint64_t n = (uint64_t)s.tokens * s.top_k;
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e == hipSuccess)
+        e = hipMemcpy(ids_host, ws.base + ws.off_route_idx, n * 4u, hipMemcpyDeviceToHost);
+    if (e == hipSuccess)
+        e = hipMemcpy(weights_host, ws.base + ws.off_route_w, n * 4u, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? VL_OK : hip_fail(e, "route read");
 }
 
 int vl_read_status(const void* workspace, void* stream, uint32_t* bits) {

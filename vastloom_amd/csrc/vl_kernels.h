@@ -19,10 +19,10 @@ constexpr uint32_t kStatusBadRoute = 4u;
 // 2^30 in magnitude, split into four signed base-256 digits. Stored [group][token slot][limb][32
 // columns] so that one 16-byte load is one lane's MFMA A fragment. Token slots are padded to a
 // power of two no larger than 8.
-inline uint32_t limb_slots(uint32_t tokens) {
+__host__ __device__ inline uint32_t limb_slots(uint32_t tokens) {
     return tokens <= 1 ? 1u : tokens <= 2 ? 2u : tokens <= 4 ? 4u : 8u;
 }
-inline uint64_t limb_bytes(uint32_t cols, uint32_t tokens) {
+__host__ __device__ inline uint64_t limb_bytes(uint32_t cols, uint32_t tokens) {
     return (uint64_t)(cols / 32u) * limb_slots(tokens) * 128u;
 }
 

@@ -1,0 +1,82 @@
+// Host-side interface of the MoE-layer kernels (vl_moe.hip).
+#ifndef VL_MOE_H
+#define VL_MOE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vl {
+
+// Resident (tiled) weights of one expert.
+struct MoeExpert {
+    const uint8_t* gate;
+    const uint8_t* up;
+    const uint8_t* down;
+};
+
+// How the expert's activation is formed and how expert outputs are combined.
+enum MoeSemantics : uint32_t {
+    // execute_expert + moe_forward (deepseek_v4_graph.cpp:1826-1894, :2129-2266): float64 SwiGLU
+    // with optional clamp, route weight applied before the down projection, outputs added in
+    // ascending expert id, shared expert last.
+    kSemDeepseek = 0,
+    // qwen38_expert_mlp_q8 + qwen38_moe_block (qwen3_8_flash_next_reference.cpp:1317-1421):
+    // silu_f(g) * u in float, route weight applied to the expert output in slot order.
+    kSemQwen = 1,
+    // routed_expert_iq1_s_iq3_xxs_f32 (ggml_quantization.cpp:1678-1745): g / (1 + expf(-g)) * u
+    // in float, no clamp, no route weight.
+    kSemPlain = 2,
+};
+
+enum MoeRouting : uint32_t {
+    kRouteLearned = 0,  // top-k of score(logit) + bias (deepseek_v4_reference.cpp:223-255)
+    kRouteTable = 1,    // ids from a per-token table, weights from scores (:275-307)
+    kRouteSoftmax = 2,  // float64 softmax top-k (qwen3_8_flash_next_reference.cpp:1186-1240)
+    kRouteGiven = 3,    // ids and weights supplied by the caller (one expert FFN call)
+};
+
+enum MoeScore : uint32_t { kScoreSqrtSoftplus = 0, kScoreSigmoid = 1 };
+
+constexpr uint32_t kMoeMaxTokens = 8;
+constexpr uint32_t kMoeMaxTopK = 16;
+
+struct MoeShape {
+    uint32_t tokens, width, inter, experts, top_k;
+    uint32_t gate_type, down_type;
+    uint32_t semantics, routing, score_fn, has_shared, renormalize;
+    float route_scale, routed_limit, shared_limit;
+};
+
+// Inputs of one layer call. Router and bias are float32; table ids [tokens][top_k]; given ids
+// and weights [tokens][top_k] for kRouteGiven (weights may be null: no route weight).
+struct MoeInputs {
+    const MoeExpert* experts;  // device array: experts entries, then the shared expert
+    const float* router;       // [experts][width]
+    const float* bias;         // [experts] or null
+    const uint32_t* table_ids;
+    const uint32_t* given_ids;
+    const float* given_weights;
+    const float* x;            // [tokens][width]
+    float* out;                // [tokens][width]
+};
+
+// Device workspace of one layer call, carved by moe_workspace_layout.
+struct MoeWorkspace {
+    uint8_t* base;
+    uint64_t bytes;
+    uint64_t off_header, off_logits, off_route_idx, off_route_w, off_active, off_combine,
+        off_hmax, off_hexp, off_xexp, off_xlimbs, off_h, off_hlimbs, off_ypart;
+    uint32_t max_active;
+};
+
+bool moe_shape_ok(const MoeShape& s);
+uint64_t moe_workspace_bytes(const MoeShape& s);
+MoeWorkspace moe_workspace_layout(const MoeShape& s, void* base);
+
+// Issues the whole layer on the stream. The workspace's first word is the status word.
+hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& ws,
+                      hipStream_t stream);
+
+}  // namespace vl
+
+#endif  // VL_MOE_H

@@ -96,6 +96,111 @@ class DeviceMatrix:
         return y[0] if squeeze else y
 
 
+class DeviceExpert:
+    """Gate (w1), up (w3) and down (w2) of one expert, resident and tiled."""
+
+    def __init__(self, gate_type: int, down_type: int, width: int, intermediate: int,
+                 gate, up, down, stream=None):
+        self.gate = DeviceMatrix(gate_type, intermediate, width, gate, stream)
+        self.up = DeviceMatrix(gate_type, intermediate, width, up, stream)
+        self.down = DeviceMatrix(down_type, width, intermediate, down, stream)
+
+    def release_staging(self) -> None:
+        for m in (self.gate, self.up, self.down):
+            m.release_staging()
+
+    def weights(self) -> _lib.ExpertWeights:
+        return _lib.ExpertWeights(self.gate.ptr(), self.up.ptr(), self.down.ptr())
+
+
+class MoeLayer:
+    """One MoE layer on the device: router, routing, expert SwiGLU FFNs and combine.
+
+    The device counterpart of moe_forward (deepseek semantics,
+    src/inference/deepseek_v4_graph.cpp:1902-2274) and qwen38_moe_block (qwen semantics,
+    src/inference/qwen3_8_flash_next_reference.cpp:1377-1421); one call per layer, no host
+    synchronisation inside.
+    """
+
+    def __init__(self, experts: list[DeviceExpert], shared: DeviceExpert | None, *, width: int,
+                 intermediate: int, top_k: int, gate_type: int, down_type: int,
+                 semantics: int, routing: int, score_fn: int = _lib.SCORE_SIGMOID,
+                 renormalize: bool = True, route_scale: float = 1.0, routed_limit: float = 0.0,
+                 shared_limit: float = 0.0, router: torch.Tensor | None = None,
+                 bias: torch.Tensor | None = None, device="cuda"):
+        self.experts, self.shared = experts, shared
+        self.width, self.intermediate, self.top_k = width, intermediate, top_k
+        self.gate_type, self.down_type = gate_type, down_type
+        self.semantics, self.routing, self.score_fn = semantics, routing, score_fn
+        self.renormalize, self.route_scale = renormalize, route_scale
+        self.routed_limit, self.shared_limit = routed_limit, shared_limit
+        self.router = None if router is None else router.to(device, torch.float32).contiguous()
+        self.bias = None if bias is None else bias.to(device, torch.float32).contiguous()
+        table = [e.weights() for e in experts] + ([shared.weights()] if shared else [])
+        raw = (_lib.ExpertWeights * len(table))(*table)
+        host = torch.frombuffer(bytearray(raw), dtype=torch.uint8)
+        self.expert_table = host.to(device)
+        self._ws: dict[int, torch.Tensor] = {}
+
+    def config(self, tokens: int) -> _lib.MoeConfig:
+        return _lib.MoeConfig(tokens, self.width, self.intermediate, len(self.experts),
+                              self.top_k, self.gate_type, self.down_type, self.semantics,
+                              self.routing, self.score_fn, int(self.shared is not None),
+                              int(self.renormalize), self.route_scale, self.routed_limit,
+                              self.shared_limit)
+
+    def workspace(self, tokens: int) -> torch.Tensor:
+        if tokens not in self._ws:
+            n = C.c_uint64()
+            cfg = self.config(tokens)
+            call("vl_moe_workspace", C.byref(cfg), C.byref(n))
+            self._ws[tokens] = torch.empty(n.value, dtype=torch.uint8,
+                                           device=self.expert_table.device)
+        return self._ws[tokens]
+
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None, *,
+                table_ids: torch.Tensor | None = None, given_ids: torch.Tensor | None = None,
+                given_weights: torch.Tensor | None = None, stream=None,
+                check: bool = True) -> torch.Tensor:
+        x2 = x.reshape(-1, self.width).contiguous()
+        tokens = x2.shape[0]
+        if out is None:
+            out = torch.empty_like(x2)
+        ws = self.workspace(tokens)
+        cfg = self.config(tokens)
+        p = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
+        inputs = _lib.MoeInputs(self.expert_table.data_ptr(), p(self.router), p(self.bias),
+                                p(table_ids), p(given_ids), p(given_weights), x2.data_ptr(),
+                                out.data_ptr())
+        s = _stream(stream)
+        call("vl_moe_layer", C.byref(cfg), C.byref(inputs), ws.data_ptr(), ws.numel(), s)
+        if check:
+            raise_on_status(ws, s, "moe_layer")
+        return out
+
+    def routes(self, tokens: int, stream=None) -> tuple[np.ndarray, np.ndarray]:
+        ids = np.zeros((tokens, self.top_k), np.uint32)
+        w = np.zeros((tokens, self.top_k), np.float32)
+        cfg = self.config(tokens)
+        call("vl_moe_read_routes", C.byref(cfg), self.workspace(tokens).data_ptr(),
+             _stream(stream), ids.ctypes.data, w.ctypes.data)
+        return ids, w
+
+
+def expert_ffn(expert: DeviceExpert, x: torch.Tensor, *, semantics: int,
+               route_weights: torch.Tensor | None = None, limit: float = 0.0,
+               stream=None) -> torch.Tensor:
+    """One expert's SwiGLU FFN for up to 8 tokens: execute_expert (deepseek,
+    deepseek_v4_graph.cpp:1826-1894), qwen38_expert_mlp_q8 (qwen) or
+    routed_expert_iq1_s_iq3_xxs_f32 (plain)."""
+    layer = MoeLayer([expert], None, width=expert.gate.cols, intermediate=expert.gate.rows,
+                     top_k=1, gate_type=expert.gate.qtype, down_type=expert.down.qtype,
+                     semantics=semantics, routing=_lib.ROUTE_GIVEN, routed_limit=limit,
+                     device=x.device)
+    gw = None if route_weights is None else route_weights.to(x.device, torch.float32).reshape(-1, 1).contiguous()
+    return layer.forward(x, given_weights=gw, stream=stream)
+
+
 def read_status(workspace: torch.Tensor, stream: int) -> int:
     bits = C.c_uint32()
     call("vl_read_status", _ptr(workspace), stream, C.byref(bits))

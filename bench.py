@@ -1,0 +1,264 @@
+#!/usr/bin/env python3
+"""Benchmark: quantized expert FFN effective HBM GB/s (and % of peak) and µs per MoE layer, 1 GPU.
+
+A step is one MoE layer over one token: router (float32 [256 x 7168], float64 accumulation),
+sigmoid top-8 routing, eight IQ2_XXS routed experts plus the shared expert (7168 -> 2048 ->
+7168 SwiGLU each), and the ascending-id combine; all weights resident in HBM before timing.
+The value is the layer's quantized weight bytes (9 experts x 11,354,112 B) divided by the
+measured time per layer. Tokens rotate through a pool so that routing (and therefore the
+experts touched) changes every step, and layer instances rotate so that no weights stay in
+cache between their uses.
+
+    python bench.py [--steps K] [--warmup W] [--workload iq2_moe] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=400)
+    p.add_argument("--warmup", type=int, default=40)
+    p.add_argument("--workload", default="iq2_moe",
+                   choices=["q8_expert", "q8_moe", "iq2_moe", "mixed_moe"])
+    p.add_argument("--layers", type=int, default=6,
+                   help="layer instances rotated between steps (defeats caching of weights)")
+    p.add_argument("--token-pool", type=int, default=64)
+    p.add_argument("--profile-steps", type=int, default=100)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    return p.parse_args()
+
+
+def token_pool(wl, count: int) -> np.ndarray:
+    """The workload's own tokens first, then further seeded N(0, 1) tokens."""
+    base = wl.x()
+    rng = np.random.Generator(np.random.PCG64(np.random.SeedSequence([wl.seed, 2, 1])))
+    extra = rng.standard_normal((max(0, count - base.shape[0]) * wl.tokens, wl.width))
+    pool = np.concatenate([base, extra.astype(np.float32)])
+    return pool[: count * wl.tokens].reshape(count, wl.tokens, wl.width)
+
+
+def build_layers(wl, instances: int):
+    import torch
+
+    from vastloom_amd import _lib, ops
+
+    experts = [wl.expert(e) for e in range(wl.experts)]
+    shared = wl.shared()
+    sem = _lib.SEM_QWEN if wl.semantics == "qwen" else _lib.SEM_DEEPSEEK
+    routing = {"softmax": _lib.ROUTE_SOFTMAX, "single": _lib.ROUTE_GIVEN}.get(
+        wl.routing, _lib.ROUTE_LEARNED)
+    router = torch.from_numpy(wl.router())
+    layers = []
+    for _ in range(instances):
+        devs = [ops.DeviceExpert(wl.gate_type, wl.down_type, wl.width, wl.intermediate,
+                                 e.gate, e.up, e.down) for e in experts]
+        sh = (ops.DeviceExpert(wl.gate_type, wl.down_type, wl.width, wl.intermediate,
+                               shared.gate, shared.up, shared.down) if shared else None)
+        torch.cuda.synchronize()
+        for d in devs + ([sh] if sh else []):
+            d.release_staging()
+        layers.append(ops.MoeLayer(devs, sh, width=wl.width, intermediate=wl.intermediate,
+                                   top_k=wl.top_k, gate_type=wl.gate_type,
+                                   down_type=wl.down_type, semantics=sem, routing=routing,
+                                   score_fn=wl.score_fn, router=router))
+    return experts, shared, layers
+
+
+def cpu_baseline(wl, experts, shared, pool, seconds: float) -> dict:
+    """The reference's own CPU kernels (oracle/_ref, built from its sources) on a bounded
+    sample of the same workload: router logits and routing, then per selected expert the
+    reference matvecs (row-split over the runtime policy's threads), SwiGLU and combine."""
+    from oracle.oracle import Oracle, Reference, default_threads
+
+    orc = Oracle()
+    kind = "reference" if Reference.available() else "port"
+    ref = Reference() if kind == "reference" else None
+    threads = default_threads()
+    H, F = wl.width, wl.intermediate
+    router = wl.router()
+
+    def matvec(qtype, data, rows, cols, x):
+        if ref is not None:
+            return ref.matvec(qtype, data, rows, cols, x, threads=threads)
+        return orc.matvec(qtype, data, rows, cols, x, threads=threads)
+
+    def expert(e, x, w_route):
+        g = matvec(e.gate_type, e.gate, F, H, x)
+        u = matvec(e.gate_type, e.up, F, H, x)
+        if wl.semantics == "qwen":
+            h = (np.array([orc.silu_f(float(v)) for v in g], np.float32) * u).astype(np.float32)
+        else:
+            gv, uv = g.astype(np.float64), u.astype(np.float64)
+            h = gv / (1.0 + np.exp(-gv)) * uv
+            if w_route is not None:
+                h = h * np.float64(w_route)
+            h = h.astype(np.float32)
+        return matvec(e.down_type, e.down, H, F, h)
+
+    done, t0 = 0, time.perf_counter()
+    while True:
+        x = pool[done % len(pool)]
+        for t in range(wl.tokens):
+            xt = x[t]
+            if wl.routing == "single":
+                expert(experts[0], xt, None)
+                continue
+            logits = orc.linear_f64(router, xt, wl.experts)
+            if wl.routing == "softmax":
+                ids, w = orc.route_softmax(logits[0], wl.top_k, True)
+            else:
+                ids, w = orc.route_learned(logits, None, wl.top_k, 1.0, wl.score_fn)
+                ids, w = ids[0], w[0]
+            out = np.zeros(H, np.float32)
+            for e, wr in sorted(zip(ids, w)):
+                y = expert(experts[e], xt, wr if wl.semantics == "deepseek" else None)
+                out += y * wr if wl.semantics == "qwen" else y
+            if shared is not None:
+                out += expert(shared, xt, None)
+        done += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    elapsed = time.perf_counter() - t0
+    layer_bytes = layer_weight_bytes(wl)
+    return {"value": round(layer_bytes * done / elapsed / 1e9, 4), "unit": "GB/s",
+            "cores": threads, "kind": kind,
+            "us_per_layer": round(elapsed / done * 1e6, 1),
+            "sample": f"{done} layer(s) of the {wl.name} workload, {wl.tokens} token(s) each, "
+                      f"{elapsed:.1f} s on {threads} thread(s) of {os.cpu_count()} logical CPUs"}
+
+
+def layer_weight_bytes(wl) -> int:
+    routed = 1 if wl.routing == "single" else min(wl.experts, wl.tokens * wl.top_k)
+    if wl.tokens > 1:
+        raise ValueError("per-layer bytes depend on routing for multi-token workloads")
+    return (routed + (1 if wl.has_shared else 0)) * wl.expert_bytes()
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this path "
+              "(no multi-GPU sharding or collectives are built)", file=sys.stderr)
+        return 2
+    import torch
+
+    from vastloom_amd import ops
+    from vastloom_amd.workloads import workload
+
+    wl = workload(args.workload)
+    if wl.tokens != 1:
+        print("bench.py times single-token layers; use the parity tests for multi-token workloads",
+              file=sys.stderr)
+        return 2
+    t_build = time.perf_counter()
+    experts, shared, layers = build_layers(wl, args.layers)
+    pool_host = token_pool(wl, args.token_pool)
+    pool = torch.from_numpy(pool_host).cuda()
+    outs = [torch.empty((wl.tokens, wl.width), dtype=torch.float32, device="cuda")
+            for _ in range(2)]
+    print(f"# built {args.layers} layer instance(s) of {wl.name} in "
+          f"{time.perf_counter() - t_build:.1f}s", file=sys.stderr, flush=True)
+
+    def step(i, **kw):
+        layer = layers[i % len(layers)]
+        return layer.forward(pool[i % len(pool)], outs[i % 2], check=False, **kw)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        step(i)
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    stream = torch.cuda.current_stream().cuda_stream
+    for layer in layers:
+        for ws in layer._ws.values():
+            bits = ops.read_status(ws, stream)
+            if bits:
+                raise RuntimeError(f"layer reported status bits {bits:#x}")
+
+    # Per-stage durations from HIP events on the same stream, in a separate profiled pass.
+    tl = ops.Timeline(args.profile_steps)
+    for i in range(args.profile_steps):
+        step(i, timeline=tl, call_slot=i)
+    torch.cuda.synchronize()
+    stages = [tl.stage_ms(i) for i in range(args.profile_steps)]
+    tl.close()
+    stage_us = {k: round(1000.0 * float(np.mean([s[k] for s in stages])), 2) for k in stages[0]}
+
+    layer_bytes = layer_weight_bytes(wl)
+    gbs = layer_bytes / (ms_per_step * 1e-3) / 1e9
+    # Dominant kernel: the gate/up pass, which reads two matrices of every selected expert.
+    n_exp = (1 if wl.routing == "single" else wl.top_k) + (1 if wl.has_shared else 0)
+    H, F = wl.width, wl.intermediate
+    from vastloom_amd.workloads import storage_bytes
+    gateup_bytes = n_exp * 2 * storage_bytes(wl.gate_type, F, H)
+    gateup_gbs = gateup_bytes / (stage_us["gate_up"] * 1e-6) / 1e9
+    down_gbs = n_exp * storage_bytes(wl.down_type, H, F) / (stage_us["down"] * 1e-6) / 1e9
+
+    result = {
+        "metric": "quant expert FFN effective HBM GB/s (% of peak) + us per MoE layer, 1 GPU",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_layer": round(ms_per_step * 1000.0, 2),
+        "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "iq2_xxs weights, i8xi8->i32 MFMA, f32 accumulate",
+        "data": "synthetic (seeded PCG64; uniform random IQ2_XXS payload bytes, |N(0,1)|*0.01 "
+                "fp16 scales, N(0,0.02) router, N(0,1) tokens)",
+        "config": {"workload": f"{wl.name}: DeepSeek-class MoE layer, width {wl.width}, expert "
+                               f"width {wl.intermediate}, {wl.experts} routed experts top-"
+                               f"{wl.top_k} + {int(wl.has_shared)} shared, 1 token, sigmoid "
+                               f"router, {TYPE(wl.gate_type)} gate/up, {TYPE(wl.down_type)} down",
+                   "quantized_bytes_per_layer": layer_bytes,
+                   "router_bytes_per_layer": wl.router_bytes(),
+                   "layer_instances": args.layers, "token_pool": args.token_pool},
+        "stages_us": stage_us,
+        "roofline": {"bound": "hbm", "kernel": "k_moe_gateup", "achieved": round(gateup_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gateup_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": gateup_bytes,
+                     "down_kernel_achieved": round(down_gbs, 1)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(wl, experts, shared, pool_host, args.cpu_seconds)
+    print(json.dumps(result))
+    return 0
+
+
+def TYPE(t: int) -> str:
+    from vastloom_amd.workloads import TYPE_NAMES
+
+    return TYPE_NAMES[t].upper()
+
+
+if __name__ == "__main__":
+    sys.exit(main())

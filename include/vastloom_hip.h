@@ -181,6 +181,33 @@ int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void*
 int vl_moe_read_routes(const vl_moe_config* config, const void* workspace, void* stream,
                        uint32_t* ids_host, float* weights_host);
 
+/* ---- Stage timing (replaces the reference's steady_clock kernel_ms, which timed a whole
+ * synchronous call: src/cuda/cuda_matvec_accelerator.cpp:258-311) ---------------------------- */
+
+/* Stages of one vl_moe_layer call, in launch order. */
+#define VL_STAGE_ROUTER 0u
+#define VL_STAGE_ROUTE 1u
+#define VL_STAGE_PREP 2u
+#define VL_STAGE_GATE_UP 3u
+#define VL_STAGE_H_PREP 4u
+#define VL_STAGE_DOWN 5u
+#define VL_STAGE_COMBINE 6u
+#define VL_STAGE_COUNT 7u
+
+typedef struct vl_timeline vl_timeline;
+
+/* A set of HIP events for up to `calls` profiled layer calls. */
+int vl_timeline_create(uint32_t calls, vl_timeline** out);
+void vl_timeline_destroy(vl_timeline* timeline);
+
+/* vl_moe_layer that also records events around each stage into slot `call` of the timeline. */
+int vl_moe_layer_profiled(const vl_moe_config* config, const vl_moe_inputs* inputs,
+                          void* workspace, uint64_t workspace_bytes, void* stream,
+                          vl_timeline* timeline, uint32_t call);
+
+/* Milliseconds of each stage of a recorded call (the events must have completed). */
+int vl_timeline_stage_ms(vl_timeline* timeline, uint32_t call, float* ms /* [VL_STAGE_COUNT] */);
+
 #ifdef __cplusplus
 }
 #endif

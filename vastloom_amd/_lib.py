@@ -43,7 +43,14 @@ _SIGNATURES = {
     "vl_moe_workspace": [_P, C.POINTER(_U64)],
     "vl_moe_layer": [_P, _P, _P, _U64, _P],
     "vl_moe_read_routes": [_P, _P, _P, _P, _P],
+    "vl_timeline_create": [_U32, C.POINTER(C.c_void_p)],
+    "vl_timeline_destroy": [_P],
+    "vl_moe_layer_profiled": [_P, _P, _P, _U64, _P, _P, _U32],
+    "vl_timeline_stage_ms": [_P, _U32, C.POINTER(C.c_float)],
 }
+_RESTYPE_NONE = {"vl_timeline_destroy"}
+
+STAGES = ("router", "route", "prep", "gate_up", "h_prep", "down", "combine")
 
 
 class MoeConfig(C.Structure):
@@ -84,7 +91,7 @@ def lib() -> C.CDLL:
         for name, args in _SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = args
-            fn.restype = _RESTYPES.get(name, C.c_int)
+            fn.restype = None if name in _RESTYPE_NONE else _RESTYPES.get(name, C.c_int)
         _lib = handle
     return _lib
 

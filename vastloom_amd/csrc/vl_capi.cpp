@@ -4,7 +4,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <string>
+#include <vector>
 
 #include "../../include/vastloom_hip.h"
 #include "vl_kernels.h"
@@ -122,7 +124,7 @@ int vl_matvec(uint32_t type, uint64_t rows, uint64_t cols, const void* tiled_dev
     vl::QmvBatch batch{};
     batch.inline_jobs[0] = vl::QmvJob{static_cast<const uint8_t*>(tiled_device), xl, xe, y_device,
                                       (uint32_t)rows, (uint32_t)cols, tokens, (uint32_t)rows};
-    e = vl::launch_qmv(type, vl::limb_slots(tokens), batch, 1, L.tiles, status, s);
+    e = vl::launch_qmv(type, vl::limb_slots(tokens), batch, 1, L.tiles, (uint32_t)cols, status, s);
     return e == hipSuccess ? VL_OK : hip_fail(e, "matvec launch");
 }
 
@@ -163,6 +165,67 @@ int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void*
                            inputs->given_weights, inputs->x, inputs->out};
     const hipError_t e = vl::launch_moe(s, in, ws, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? VL_OK : hip_fail(e, "MoE launch");
+}
+
+}  // extern "C"
+
+struct vl_timeline {
+    uint32_t calls = 0;
+    std::vector<hipEvent_t> events;  // calls x (stages + 1)
+};
+
+extern "C" {
+
+int vl_timeline_create(uint32_t calls, vl_timeline** out) {
+    if (!out || calls == 0) return fail(VL_INVALID_ARGUMENT, "invalid timeline request");
+    auto* t = new (std::nothrow) vl_timeline;
+    if (!t) return fail(VL_RESOURCE_EXHAUSTED, "timeline allocation failed");
+    t->calls = calls;
+    t->events.assign((size_t)calls * (vl::kStageCount + 1), nullptr);
+    for (auto& e : t->events) {
+        const hipError_t r = hipEventCreate(&e);
+        if (r != hipSuccess) {
+            vl_timeline_destroy(t);
+            return hip_fail(r, "hipEventCreate");
+        }
+    }
+    *out = t;
+    return VL_OK;
+}
+
+void vl_timeline_destroy(vl_timeline* t) {
+    if (!t) return;
+    for (auto e : t->events)
+        if (e) (void)hipEventDestroy(e);
+    delete t;
+}
+
+int vl_moe_layer_profiled(const vl_moe_config* config, const vl_moe_inputs* inputs,
+                          void* workspace, uint64_t workspace_bytes, void* stream,
+                          vl_timeline* timeline, uint32_t call) {
+    if (!timeline || call >= timeline->calls) return fail(VL_INVALID_ARGUMENT, "bad timeline slot");
+    vl::MoeShape s;
+    if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
+    if (!inputs || !inputs->experts || !inputs->x || !inputs->out || !workspace)
+        return fail(VL_INVALID_ARGUMENT, "null input pointer");
+    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, workspace);
+    if (workspace_bytes < ws.bytes) return fail(VL_INVALID_ARGUMENT, "workspace too small");
+    const vl::MoeInputs in{reinterpret_cast<const vl::MoeExpert*>(inputs->experts),
+                           inputs->router, inputs->bias, inputs->table_ids, inputs->given_ids,
+                           inputs->given_weights, inputs->x, inputs->out};
+    hipEvent_t* ev = timeline->events.data() + (size_t)call * (vl::kStageCount + 1);
+    const hipError_t e = vl::launch_moe(s, in, ws, static_cast<hipStream_t>(stream), ev);
+    return e == hipSuccess ? VL_OK : hip_fail(e, "MoE launch");
+}
+
+int vl_timeline_stage_ms(vl_timeline* t, uint32_t call, float* ms) {
+    if (!t || call >= t->calls || !ms) return fail(VL_INVALID_ARGUMENT, "bad timeline read");
+    hipEvent_t* ev = t->events.data() + (size_t)call * (vl::kStageCount + 1);
+    for (uint32_t i = 0; i < vl::kStageCount; ++i) {
+        const hipError_t r = hipEventElapsedTime(&ms[i], ev[i], ev[i + 1]);
+        if (r != hipSuccess) return hip_fail(r, "hipEventElapsedTime");
+    }
+    return VL_OK;
 }
 
 int vl_moe_read_routes(const vl_moe_config* config, const void* workspace, void* stream,

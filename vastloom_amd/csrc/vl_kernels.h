@@ -52,9 +52,10 @@ hipError_t launch_dequant(const vl_tiled_layout& L, const uint8_t* tiled, float*
 hipError_t launch_prep_limbs(const float* x, uint32_t sets, uint32_t tokens, uint32_t cols,
                              uint64_t x_stride, uint64_t set_stride, int8_t* xl, int* xe,
                              uint32_t* status, hipStream_t stream);
-// Every job has the given type and at most max_tiles tiles; njobs jobs are read from the batch.
+// Every job has the given type, at most max_tiles tiles and at most max_cols columns; njobs jobs
+// are read from the batch.
 hipError_t launch_qmv(uint32_t type, uint32_t token_slots, const QmvBatch& batch, uint32_t njobs,
-                      uint32_t max_tiles, uint32_t* status, hipStream_t stream);
+                      uint32_t max_tiles, uint32_t max_cols, uint32_t* status, hipStream_t stream);
 hipError_t launch_fill_u32(uint32_t* dst, uint32_t count, uint32_t value, hipStream_t stream);
 
 }  // namespace vl

@@ -226,31 +226,40 @@ hipError_t launch_prep_limbs(const float* x, uint32_t sets, uint32_t tokens, uin
 // group; for the A operand it supplies limb (n % 4) of token 2*(n/8) + (n/4)%2.
 // ------------------------------------------------------------------------------------------
 
-template <uint32_t FMT, int NT>
+template <uint32_t FMT, int NT, bool LDS_A>
 __global__ void __launch_bounds__(256) k_qmv(const QmvBatch batch, uint32_t* status) {
     __shared__ LdsTables lds;
     __shared__ float partial[4][NT][32];
+    extern __shared__ __align__(16) int8_t dyn_lds[];
+    __shared__ __align__(16) int8_t s_zero[16];
     const QmvJob job = batch.device_jobs ? batch.device_jobs[blockIdx.y]
                                          : batch.inline_jobs[blockIdx.y];
     vl_tiled_layout L;
     if (job.rows == 0 || !vl_make_layout(FMT, job.rows, job.cols, &L)) return;
     const uint32_t t = blockIdx.x;
     if (t >= L.tiles) return;
-    load_tables<FMT>(lds);
-    __syncthreads();
-
     constexpr int S = Acc<NT>::kSlots;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 31;
     const int hh = lane >> 5;
-    const uint32_t units = units_of<FMT>(L);
+    const uint32_t chunks = chunks_of<FMT>(L);
     const int slot = a_slot_of_lane();
-    const int8_t* abase = slot < (int)job.tokens
-        ? job.xl + ((uint64_t)slot * 4u + a_limb_of_lane()) * 32u + 16u * hh
-        : nullptr;
+    const bool on = slot < (int)job.tokens;
+    const uint32_t lane_off = ((uint32_t)slot * 4u + a_limb_of_lane()) * 32u + 16u * hh;
     float accf[S];
-    tile_partial<FMT, NT>(L, job.w, t, units * wave / 4u, units * (wave + 1) / 4u, abase,
-                          (uint64_t)NT * 128u, lds, accf);
+    tile_partial<FMT, NT>(L, job.w, t, chunks * wave / 4u, chunks * (wave + 1) / 4u,
+                          NT * 128u, lds, accf, [&](uint32_t& stride) -> const int8_t* {
+        load_tables<FMT>(lds);
+        if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(s_zero)[threadIdx.x] = 0;
+        if (LDS_A) stage_limbs<NT>(dyn_lds, job.xl, L.groups, NT, job.tokens,
+                                   [](uint32_t s) { return s; });
+        __syncthreads();
+        if (!on) {
+            stride = 0;
+            return s_zero;
+        }
+        return LDS_A ? dyn_lds + lane_off : job.xl + lane_off;
+    });
 #pragma unroll
     for (int i = 0; i < S; ++i) {
         const int tok = 2 * i + hh;
@@ -273,27 +282,36 @@ __global__ void __launch_bounds__(256) k_qmv(const QmvBatch batch, uint32_t* sta
 
 template <uint32_t FMT>
 static hipError_t launch_qmv_fmt(uint32_t slots, const QmvBatch& jobs, uint32_t njobs,
-                                 uint32_t max_tiles, uint32_t* status, hipStream_t stream) {
+                                 uint32_t max_tiles, uint32_t lds_cols, uint32_t* status,
+                                 hipStream_t stream) {
     const dim3 grid(max_tiles, njobs), block(256);
-    switch (slots) {
-        case 1: hipLaunchKernelGGL((k_qmv<FMT, 1>), grid, block, 0, stream, jobs, status); break;
-        case 2: hipLaunchKernelGGL((k_qmv<FMT, 2>), grid, block, 0, stream, jobs, status); break;
-        case 4: hipLaunchKernelGGL((k_qmv<FMT, 4>), grid, block, 0, stream, jobs, status); break;
-        case 8: hipLaunchKernelGGL((k_qmv<FMT, 8>), grid, block, 0, stream, jobs, status); break;
+    // Activations are staged in LDS when every job's limbs fit.
+    const uint32_t lds_bytes = lds_cols / 32u * slots * 128u;
+    const bool lds_a = lds_bytes <= kMaxLdsLimbBytes;
+    const uint32_t shm = lds_a ? lds_bytes : 0u;
+    switch (slots * 2 + (lds_a ? 1 : 0)) {
+        case 2: hipLaunchKernelGGL((k_qmv<FMT, 1, false>), grid, block, shm, stream, jobs, status); break;
+        case 3: hipLaunchKernelGGL((k_qmv<FMT, 1, true>), grid, block, shm, stream, jobs, status); break;
+        case 4: hipLaunchKernelGGL((k_qmv<FMT, 2, false>), grid, block, shm, stream, jobs, status); break;
+        case 5: hipLaunchKernelGGL((k_qmv<FMT, 2, true>), grid, block, shm, stream, jobs, status); break;
+        case 8: hipLaunchKernelGGL((k_qmv<FMT, 4, false>), grid, block, shm, stream, jobs, status); break;
+        case 9: hipLaunchKernelGGL((k_qmv<FMT, 4, true>), grid, block, shm, stream, jobs, status); break;
+        case 16: hipLaunchKernelGGL((k_qmv<FMT, 8, false>), grid, block, shm, stream, jobs, status); break;
+        case 17: hipLaunchKernelGGL((k_qmv<FMT, 8, true>), grid, block, shm, stream, jobs, status); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
 hipError_t launch_qmv(uint32_t type, uint32_t token_slots, const QmvBatch& jobs, uint32_t njobs,
-                      uint32_t max_tiles, uint32_t* status, hipStream_t stream) {
+                      uint32_t max_tiles, uint32_t max_cols, uint32_t* status, hipStream_t stream) {
     if (njobs == 0 || max_tiles == 0) return hipSuccess;
     if (!jobs.device_jobs && njobs > kInlineJobs) return hipErrorInvalidValue;
     switch (type) {
-        case VL_TYPE_IQ2_XXS: return launch_qmv_fmt<VL_TYPE_IQ2_XXS>(token_slots, jobs, njobs, max_tiles, status, stream);
-        case VL_TYPE_IQ3_XXS: return launch_qmv_fmt<VL_TYPE_IQ3_XXS>(token_slots, jobs, njobs, max_tiles, status, stream);
-        case VL_TYPE_IQ1_S: return launch_qmv_fmt<VL_TYPE_IQ1_S>(token_slots, jobs, njobs, max_tiles, status, stream);
-        case VL_TYPE_Q8_0: return launch_qmv_fmt<VL_TYPE_Q8_0>(token_slots, jobs, njobs, max_tiles, status, stream);
+        case VL_TYPE_IQ2_XXS: return launch_qmv_fmt<VL_TYPE_IQ2_XXS>(token_slots, jobs, njobs, max_tiles, max_cols, status, stream);
+        case VL_TYPE_IQ3_XXS: return launch_qmv_fmt<VL_TYPE_IQ3_XXS>(token_slots, jobs, njobs, max_tiles, max_cols, status, stream);
+        case VL_TYPE_IQ1_S: return launch_qmv_fmt<VL_TYPE_IQ1_S>(token_slots, jobs, njobs, max_tiles, max_cols, status, stream);
+        case VL_TYPE_Q8_0: return launch_qmv_fmt<VL_TYPE_Q8_0>(token_slots, jobs, njobs, max_tiles, max_cols, status, stream);
         default: return hipErrorInvalidValue;
     }
 }

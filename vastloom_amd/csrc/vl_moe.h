@@ -73,9 +73,17 @@ bool moe_shape_ok(const MoeShape& s);
 uint64_t moe_workspace_bytes(const MoeShape& s);
 MoeWorkspace moe_workspace_layout(const MoeShape& s, void* base);
 
-// Issues the whole layer on the stream. The workspace's first word is the status word.
+// Stages of one layer call, in launch order; a profiled call records an event before each
+// stage and one after the last.
+enum MoeStage : uint32_t {
+    kStageRouter = 0, kStageRoute, kStagePrep, kStageGateUp, kStageHPrep, kStageDown,
+    kStageCombine, kStageCount
+};
+
+// Issues the whole layer on the stream. The workspace's first word is the status word. When
+// events is non-null it holds kStageCount + 1 events recorded around the stages.
 hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& ws,
-                      hipStream_t stream);
+                      hipStream_t stream, hipEvent_t* events = nullptr);
 
 }  // namespace vl
 

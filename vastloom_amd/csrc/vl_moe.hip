@@ -51,6 +51,7 @@ bool moe_shape_ok(const MoeShape& s) {
         s.experts == 0 || s.experts > 1024 || s.top_k > s.experts)
         return false;
     if (!vl_block_shape(s.gate_type, &be, &bb) || s.width % be || s.width % 256u) return false;
+    if (s.width > 8192u) return false;  // the routing block stages one token row in registers
     if (!vl_block_shape(s.down_type, &be, &bb) || s.inter % be || s.inter % 32u) return false;
     if (s.semantics > kSemPlain || s.routing > kRouteGiven || s.score_fn > kScoreSigmoid) return false;
     return true;
@@ -100,8 +101,11 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
+// One block per expert row; the four waves take interleaved quarters of the row (every lane
+// keeps its float4 loads in flight), then the partial sums are added in wave order.
 __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeInputs in,
                                                     const MoeWorkspace w) {
+    __shared__ double red[kMoeMaxTokens][4];
     // Per-call words later kernels accumulate into.
     if (blockIdx.x == 0) {
         MoeHeader* h = ws_ptr<MoeHeader>(w, w.off_header);
@@ -110,15 +114,32 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
         for (uint32_t i = threadIdx.x; i < w.max_active * kMoeMaxTokens; i += blockDim.x) hmax[i] = 0;
     }
     if (s.routing == kRouteGiven) return;
-    const uint32_t e = blockIdx.x * 4u + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (e >= s.experts) return;
+    const uint32_t e = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float4* row = reinterpret_cast<const float4*>(in.router + (uint64_t)e * s.width);
-    float* logits = ws_ptr<float>(w, w.off_logits);
+    const uint32_t n4 = s.width / 4u;
+    float4 wv[8];
+    int nv = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t i = threadIdx.x + 256u * j;
+        if (i < n4) { wv[j] = row[i]; nv = j + 1; }
+    }
     for (uint32_t t = 0; t < s.tokens; ++t) {
         const float4* xr = reinterpret_cast<const float4*>(in.x + (uint64_t)t * s.width);
         double acc = 0.0;
-        for (uint32_t i = lane; i < s.width / 4u; i += 64u) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j < nv) {
+                const float4 a = wv[j], b = xr[threadIdx.x + 256u * j];
+                acc += (double)a.x * (double)b.x;
+                acc += (double)a.y * (double)b.y;
+                acc += (double)a.z * (double)b.z;
+                acc += (double)a.w * (double)b.w;
+            }
+        }
+        // Rows wider than 8192 continue with plain loads.
+        for (uint32_t i = threadIdx.x + 2048u; i < n4; i += 256u) {
             const float4 a = row[i], b = xr[i];
             acc += (double)a.x * (double)b.x;
             acc += (double)a.y * (double)b.y;
@@ -126,7 +147,13 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
             acc += (double)a.w * (double)b.w;
         }
         acc = wave_sum_f64(acc);
-        if (lane == 0) logits[t * s.experts + e] = (float)acc;
+        if (lane == 0) red[t][wave] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < s.tokens) {
+        const uint32_t t = threadIdx.x;
+        ws_ptr<float>(w, w.off_logits)[t * s.experts + e] =
+            (float)(((red[t][0] + red[t][1]) + red[t][2]) + red[t][3]);
     }
 }
 
@@ -154,9 +181,161 @@ __device__ __forceinline__ bool beats_d(double ka, uint32_t ia, double kb, uint3
     return ka > kb || (ka == kb && ia < ib);
 }
 
+// Limbs of one token's activations by the whole block: max |x| (all loads issued at once,
+// kept in registers), exponent, then the four digits of round(x * 2^e) for every column, the
+// same encoding as k_prep_limbs. cols <= 4 * 4 * blockDim.x.
+__device__ void prep_token_block(const float* __restrict__ x, uint32_t cols, uint32_t slots,
+                                 uint32_t tok, int8_t* __restrict__ xl, int* __restrict__ xe,
+                                 uint32_t* status, float* red) {
+    constexpr int kPer = 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const uint32_t n4 = cols / 4u;
+    float4 v[kPer];
+    float m = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t i = threadIdx.x + blockDim.x * j;
+        v[j] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        finite &= isfinite(v[j].x) && isfinite(v[j].y) && isfinite(v[j].z) && isfinite(v[j].w);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
+    if (!finite) {
+        atomicOr(status, kStatusNonFiniteInput);
+        m = 0.0f;
+    }
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = 0.0f;
+    for (int i = 0; i < nwaves; ++i) m = fmaxf(m, red[i]);
+    __syncthreads();
+    int q = 0;
+    frexpf(m, &q);
+    const int e = m > 0.0f && isfinite(m) ? 30 - q : 0;
+    if (threadIdx.x == 0) xe[tok] = e;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t i = threadIdx.x + blockDim.x * j;
+        if (i >= n4) continue;
+        const float vs[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        uint32_t packed[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            int X = isfinite(vs[k]) ? (int)rintf(ldexpf(vs[k], e)) : 0;
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const int digit = l < 3 ? (int)(int8_t)(X & 0xff) : X;
+                packed[l] |= ((uint32_t)digit & 0xffu) << (8 * k);
+                X = (X - digit) >> 8;
+            }
+        }
+        const uint32_t k4 = 4u * i;
+        const uint64_t base = ((uint64_t)(k4 / 32u) * slots + tok) * 128u + (k4 % 32u);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) *reinterpret_cast<uint32_t*>(xl + base + 32u * l) = packed[l];
+    }
+}
+
+// Top-k of one token by one wave. Lane l holds experts l, l + 64, ... (PER of them, in
+// registers). Learned routing ranks score + bias with the reference's float keys; softmax
+// ranks float64 probabilities. Returns true when the token cannot be routed (non-finite logits
+// or a non-positive weight sum).
+template <int PER>
+__device__ bool route_token(const float* lg, const float* bias, uint32_t E, uint32_t K,
+                            bool softmax, const MoeShape& s, uint32_t* out_idx, float* out_w) {
+    const int lane = threadIdx.x & 63;
+    double key[PER];
+    float sc[PER];
+    bool taken[PER];
+    bool bad = false;
+    double mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const uint32_t e = lane + 64u * i;
+        taken[i] = e >= E;
+        sc[i] = 0.0f;
+        key[i] = -INFINITY;
+        if (e < E) {
+            const float l = lg[e];
+            bad |= !isfinite(l);
+            if (!softmax) {
+                sc[i] = score_of(l, s.score_fn);
+                key[i] = (double)(sc[i] + (bias ? bias[e] : 0.0f));
+            } else {
+                mx = fmax(mx, (double)l);
+            }
+        }
+    }
+    if (softmax) {
+        for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
+        double sum = 0.0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (lane + 64u * i < E) {
+                key[i] = exp((double)lg[lane + 64u * i] - mx);
+                sum += key[i];
+            }
+        sum = wave_sum_f64(sum);
+        const double inv = sum > 0.0 ? 1.0 / sum : 0.0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (lane + 64u * i < E) key[i] = key[i] * inv;
+    }
+    double sel_sum = 0.0;
+    for (uint32_t k = 0; k < K; ++k) {
+        double bk = -INFINITY;
+        uint32_t bi = 0xffffffffu;
+        float bs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const uint32_t e = lane + 64u * i;
+            if (!taken[i] && (bi == 0xffffffffu || beats_d(key[i], e, bk, bi))) {
+                bk = key[i];
+                bi = e;
+                bs = sc[i];
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            const double ok = __shfl_xor(bk, o);
+            const uint32_t oi = __shfl_xor(bi, o);
+            const float os = __shfl_xor(bs, o);
+            if (oi != 0xffffffffu && (bi == 0xffffffffu || beats_d(ok, oi, bk, bi))) {
+                bk = ok;
+                bi = oi;
+                bs = os;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (lane + 64u * i == bi) taken[i] = true;
+        if (bi >= E) bad = true;
+        const double v = softmax ? bk : (double)bs;
+        if (lane == 0) {
+            out_idx[k] = bi < E ? bi : 0u;
+            out_w[k] = softmax ? (float)bk : bs;
+        }
+        sel_sum += v;
+    }
+    if (lane == 0) {
+        if (!softmax) {
+            bad |= !(sel_sum > 0.0) || isinf(sel_sum);
+            for (uint32_t k = 0; k < K; ++k)
+                out_w[k] = (float)((double)out_w[k] / sel_sum * (double)s.route_scale);
+        } else if (s.renormalize && sel_sum > 0.0) {
+            const double scale = 1.0 / sel_sum;
+            for (uint32_t k = 0; k < K; ++k) out_w[k] = (float)((double)out_w[k] * scale);
+        }
+    }
+    return __any(bad);
+}
+
 __global__ void __launch_bounds__(512) k_moe_route(const MoeShape s, const MoeInputs in,
                                                    const MoeWorkspace w) {
-    constexpr uint32_t kMaxPer = 16;  // candidates per lane: experts <= 1024
     __shared__ uint32_t s_idx[kMoeMaxTokens * kMoeMaxTopK];
     __shared__ float s_w[kMoeMaxTokens * kMoeMaxTopK];
     __shared__ uint32_t s_bad;
@@ -199,92 +378,17 @@ __global__ void __launch_bounds__(512) k_moe_route(const MoeShape s, const MoeIn
                     s_w[t * K + k] = (float)((double)sc[k] / sum * (double)s.route_scale);
             }
         } else {
-            // Candidates of this lane: experts lane, lane + 64, ...
-            double key[kMaxPer];
-            float sc[kMaxPer];
-            bool taken[kMaxPer];
-            double mx = -INFINITY;
-            for (uint32_t i = 0; i < kMaxPer; ++i) {
-                const uint32_t e = lane + 64u * i;
-                taken[i] = e >= E;
-                sc[i] = 0.0f;
-                key[i] = -INFINITY;
-                if (e < E) {
-                    const float l = lg[e];
-                    if (!isfinite(l)) atomicOr(&s_bad, 1u);
-                    if (s.routing == kRouteLearned) {
-                        sc[i] = score_of(l, s.score_fn);
-                        key[i] = (double)(sc[i] + (in.bias ? in.bias[e] : 0.0f));
-                    } else {
-                        mx = fmax(mx, (double)l);
-                    }
-                }
-            }
-            double inv = 0.0;
-            if (s.routing == kRouteSoftmax) {
-                for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
-                double sum = 0.0;
-                for (uint32_t i = 0; i < kMaxPer; ++i) {
-                    const uint32_t e = lane + 64u * i;
-                    if (e < E) {
-                        key[i] = exp((double)lg[e] - mx);
-                        sum += key[i];
-                    }
-                }
-                sum = wave_sum_f64(sum);
-                inv = sum > 0.0 ? 1.0 / sum : 0.0;
-                for (uint32_t i = 0; i < kMaxPer; ++i)
-                    if (lane + 64u * i < E) key[i] = key[i] * inv;
-            }
-            double sel_sum = 0.0;
-            for (uint32_t k = 0; k < K; ++k) {
-                double bk = -INFINITY;
-                uint32_t bi = 0xffffffffu;
-                float bs = 0.0f;
-                for (uint32_t i = 0; i < kMaxPer; ++i) {
-                    const uint32_t e = lane + 64u * i;
-                    if (!taken[i] && (bi == 0xffffffffu || beats_d(key[i], e, bk, bi))) {
-                        bk = key[i];
-                        bi = e;
-                        bs = sc[i];
-                    }
-                }
-                for (int o = 32; o > 0; o >>= 1) {
-                    const double ok = __shfl_xor(bk, o);
-                    const uint32_t oi = __shfl_xor(bi, o);
-                    const float os = __shfl_xor(bs, o);
-                    if (oi != 0xffffffffu && (bi == 0xffffffffu || beats_d(ok, oi, bk, bi))) {
-                        bk = ok;
-                        bi = oi;
-                        bs = os;
-                    }
-                }
-#pragma unroll
-                for (uint32_t i = 0; i < kMaxPer; ++i)
-                    if (lane + 64u * i == bi) taken[i] = true;
-                if (lane == 0) {
-                    s_idx[t * K + k] = bi < E ? bi : 0u;
-                    if (s.routing == kRouteSoftmax) {
-                        s_w[t * K + k] = (float)bk;
-                        sel_sum += bk;
-                    } else {
-                        s_w[t * K + k] = bs;
-                        sel_sum += (double)bs;
-                    }
-                }
-            }
-            if (lane == 0) {
-                if (s.routing == kRouteLearned) {
-                    if (!(sel_sum > 0.0) || isinf(sel_sum)) atomicOr(&s_bad, 1u);
-                    for (uint32_t k = 0; k < K; ++k)
-                        s_w[t * K + k] =
-                            (float)((double)s_w[t * K + k] / sel_sum * (double)s.route_scale);
-                } else if (s.renormalize && sel_sum > 0.0) {
-                    const double scale = 1.0 / sel_sum;
-                    for (uint32_t k = 0; k < K; ++k)
-                        s_w[t * K + k] = (float)((double)s_w[t * K + k] * scale);
-                }
-            }
+            const float* bias = s.routing == kRouteLearned ? in.bias : nullptr;
+            const bool softmax = s.routing == kRouteSoftmax;
+            float* sw = s_w + t * K;
+            uint32_t* si = s_idx + t * K;
+            bool bad = false;
+            if (E <= 64) bad = route_token<1>(lg, bias, E, K, softmax, s, si, sw);
+            else if (E <= 128) bad = route_token<2>(lg, bias, E, K, softmax, s, si, sw);
+            else if (E <= 256) bad = route_token<4>(lg, bias, E, K, softmax, s, si, sw);
+            else if (E <= 512) bad = route_token<8>(lg, bias, E, K, softmax, s, si, sw);
+            else bad = route_token<16>(lg, bias, E, K, softmax, s, si, sw);
+            if (bad && lane == 0) atomicOr(&s_bad, 1u);
         }
     }
     __syncthreads();
@@ -363,6 +467,12 @@ __global__ void __launch_bounds__(512) k_moe_route(const MoeShape s, const MoeIn
         hdr->n_active = s_bad ? 0u : n_routed + (s.has_shared ? 1u : 0u);
         if (s_bad) atomicOr(&hdr->status, kStatusBadRoute);
     }
+    // The tokens' activations as MFMA limbs.
+    __shared__ float s_red[16];
+    for (uint32_t t = 0; t < s.tokens; ++t)
+        prep_token_block(in.x + (uint64_t)t * s.width, s.width, limb_slots(s.tokens), t,
+                         ws_ptr<int8_t>(w, w.off_xlimbs), ws_ptr<int>(w, w.off_xexp),
+                         &hdr->status, s_red);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -398,56 +508,71 @@ __device__ __forceinline__ float swiglu(uint32_t sem, float g, float u, float li
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
 }
 
-template <uint32_t FMT, int NT>
+// Gate and up projections of one active expert over two 32-row tiles, then the SwiGLU.
+// Eight waves: wave w takes tile 2*blockIdx.x + w/4, matrix w%2 (gate, up) and half (w/2)%2 of
+// the columns; the two halves are added in order. Two tiles per block let the grid fit the
+// GPU in one round and halve the activation staging per row.
+template <uint32_t FMT, int NT, bool LDS_A>
 __global__ void __launch_bounds__(512) k_moe_gateup(const MoeShape s, const MoeInputs in,
                                                     const MoeWorkspace w) {
     __shared__ LdsTables lds;
-    __shared__ float partial[2][4][NT][32];
+    __shared__ float partial[2][2][2][NT][32];  // [tile][matrix][half][slot][row]
+    extern __shared__ __align__(16) int8_t dyn_lds[];
+    __shared__ __align__(16) int8_t s_zero[16];
     const MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
     const uint32_t a = blockIdx.y;
     if (a >= hdr->n_active) return;
-    const ActiveExpert ae = ws_ptr<ActiveExpert>(w, w.off_active)[a];
+    const ActiveExpert* aep = ws_ptr<ActiveExpert>(w, w.off_active) + a;
+    const uint32_t ntok = aep->ntok;
     vl_tiled_layout L;
     vl_make_layout(FMT, s.inter, s.width, &L);
-    const uint32_t t = blockIdx.x;
-    if (t >= L.tiles) return;
-    load_tables<FMT>(lds);
-    __syncthreads();
 
     constexpr int S = Acc<NT>::kSlots;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int mat = wave >> 2, w4 = wave & 3;
+    const int tw = wave >> 2, mat = wave & 1, half = (wave >> 1) & 1;
+    const uint32_t t = 2u * blockIdx.x + tw;
+    const bool tile_on = t < L.tiles;
     const uint32_t n = lane & 31;
     const int hh = lane >> 5;
-    const MoeExpert ex = in.experts[ae.expert];
+    const MoeExpert ex = in.experts[aep->expert];
     const uint8_t* W = mat == 0 ? ex.gate : ex.up;
-    const uint32_t units = units_of<FMT>(L);
+    const uint32_t chunks = chunks_of<FMT>(L);
+    const uint32_t c0 = tile_on ? chunks * half / 2u : 0u;
+    const uint32_t c1 = tile_on ? chunks * (half + 1) / 2u : 0u;
     const uint32_t xslots = limb_slots(s.tokens);
     const int slot = a_slot_of_lane();
+    const bool on = slot < (int)ntok;
     const int8_t* xl = ws_ptr<int8_t>(w, w.off_xlimbs);
-    const int8_t* abase = slot < (int)ae.ntok
-        ? xl + ((uint64_t)ae.tok[slot] * 4u + a_limb_of_lane()) * 32u + 16u * hh
-        : nullptr;
+    const uint32_t limb_off = (uint32_t)a_limb_of_lane() * 32u + 16u * hh;
     float accf[S];
-    tile_partial<FMT, NT>(L, W, t, units * w4 / 4u, units * (w4 + 1) / 4u, abase,
-                          (uint64_t)xslots * 128u, lds, accf);
+    tile_partial<FMT, NT>(L, W, tile_on ? t : 0u, c0, c1, (LDS_A ? NT : xslots) * 128u, lds, accf,
+                          [&](uint32_t& stride) -> const int8_t* {
+        load_tables<FMT>(lds);
+        if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(s_zero)[threadIdx.x] = 0;
+        if (LDS_A) stage_limbs<NT>(dyn_lds, xl, L.groups, xslots, ntok,
+                                   [&](uint32_t sl) { return aep->tok[sl]; });
+        __syncthreads();
+        if (!on) {
+            stride = 0;
+            return s_zero;
+        }
+        return LDS_A ? dyn_lds + (uint32_t)slot * 128u + limb_off
+                     : xl + (uint64_t)aep->tok[slot] * 128u + limb_off;
+    });
 #pragma unroll
     for (int i = 0; i < S; ++i) {
         const int sl = 2 * i + hh;
-        if (sl < NT) partial[mat][w4][sl][n] = accf[i];
+        if (sl < NT) partial[tw][mat][half][sl][n] = accf[i];
     }
     __syncthreads();
-    const int tid = threadIdx.x;
-    if (tid < NT * 32) {
-        const int sl = tid / 32, r = tid % 32;
-        const uint32_t row = t * 32u + r;
-        if (sl < (int)ae.ntok && row < s.inter) {
-            const int e = ws_ptr<int>(w, w.off_xexp)[ae.tok[sl]];
-            const float g = ldexpf(((partial[0][0][sl][r] + partial[0][1][sl][r]) + partial[0][2][sl][r]) +
-                                       partial[0][3][sl][r], -e);
-            const float u = ldexpf(((partial[1][0][sl][r] + partial[1][1][sl][r]) + partial[1][2][sl][r]) +
-                                       partial[1][3][sl][r], -e);
-            const float h = swiglu(s.semantics, g, u, ae.limit, ae.apply_w != 0, ae.route_w[sl]);
+    for (uint32_t idx = threadIdx.x; idx < 2u * NT * 32u; idx += blockDim.x) {
+        const uint32_t tt = idx / (NT * 32u), sl = (idx / 32u) % NT, r = idx % 32u;
+        const uint32_t row = (2u * blockIdx.x + tt) * 32u + r;
+        if (sl < ntok && row < s.inter) {
+            const int e = ws_ptr<int>(w, w.off_xexp)[aep->tok[sl]];
+            const float g = ldexpf(partial[tt][0][0][sl][r] + partial[tt][0][1][sl][r], -e);
+            const float u = ldexpf(partial[tt][1][0][sl][r] + partial[tt][1][1][sl][r], -e);
+            const float h = swiglu(s.semantics, g, u, aep->limit, aep->apply_w != 0, aep->route_w[sl]);
             MoeHeader* hw = ws_ptr<MoeHeader>(w, w.off_header);
             if (!isfinite(g) || !isfinite(u) || !isfinite(h)) atomicOr(&hw->status, kStatusNonFiniteOutput);
             ws_ptr<float>(w, w.off_h)[((uint64_t)a * kMoeMaxTokens + sl) * s.inter + row] = h;
@@ -487,11 +612,16 @@ __global__ void __launch_bounds__(256) k_moe_hprep(const MoeShape s, const MoeWo
     }
 }
 
-template <uint32_t FMT, int NT>
-__global__ void __launch_bounds__(256) k_moe_down(const MoeShape s, const MoeInputs in,
+// Down projection of one active expert over four 32-row tiles: wave w takes tile
+// 4*blockIdx.x + w/2 and half w%2 of the columns. The block stages the expert's activation
+// limbs once for its 128 rows.
+template <uint32_t FMT, int NT, bool LDS_A>
+__global__ void __launch_bounds__(512) k_moe_down(const MoeShape s, const MoeInputs in,
                                                   const MoeWorkspace w) {
     __shared__ LdsTables lds;
-    __shared__ float partial[4][NT][32];
+    __shared__ float partial[4][2][NT][32];  // [tile][half][slot][row]
+    extern __shared__ __align__(16) int8_t dyn_lds[];
+    __shared__ __align__(16) int8_t s_zero[16];
     const MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
     const uint32_t a = blockIdx.y;
     if (a >= hdr->n_active) return;
@@ -499,39 +629,48 @@ __global__ void __launch_bounds__(256) k_moe_down(const MoeShape s, const MoeInp
     const uint32_t ntok = act[a].ntok;
     vl_tiled_layout L;
     vl_make_layout(FMT, s.width, s.inter, &L);
-    const uint32_t t = blockIdx.x;
-    if (t >= L.tiles) return;
-    load_tables<FMT>(lds);
-    __syncthreads();
 
     constexpr int S = Acc<NT>::kSlots;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tw = wave >> 1, half = wave & 1;
+    const uint32_t t = 4u * blockIdx.x + tw;
+    const bool tile_on = t < L.tiles;
     const uint32_t n = lane & 31;
     const int hh = lane >> 5;
     const uint8_t* W = in.experts[act[a].expert].down;
-    const uint32_t units = units_of<FMT>(L);
+    const uint32_t chunks = chunks_of<FMT>(L);
+    const uint32_t c0 = tile_on ? chunks * half / 2u : 0u;
+    const uint32_t c1 = tile_on ? chunks * (half + 1) / 2u : 0u;
     const int slot = a_slot_of_lane();
+    const bool on = slot < (int)ntok;
     const int8_t* hl = ws_ptr<int8_t>(w, w.off_hlimbs) + (uint64_t)a * (s.inter / 32u) * kMoeMaxTokens * 128u;
-    const int8_t* abase = slot < (int)ntok
-        ? hl + ((uint64_t)slot * 4u + a_limb_of_lane()) * 32u + 16u * hh
-        : nullptr;
+    const uint32_t lane_off = ((uint32_t)slot * 4u + a_limb_of_lane()) * 32u + 16u * hh;
     float accf[S];
-    tile_partial<FMT, NT>(L, W, t, units * wave / 4u, units * (wave + 1) / 4u, abase,
-                          (uint64_t)kMoeMaxTokens * 128u, lds, accf);
+    tile_partial<FMT, NT>(L, W, tile_on ? t : 0u, c0, c1, (LDS_A ? NT : kMoeMaxTokens) * 128u, lds,
+                          accf, [&](uint32_t& stride) -> const int8_t* {
+        load_tables<FMT>(lds);
+        if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(s_zero)[threadIdx.x] = 0;
+        if (LDS_A) stage_limbs<NT>(dyn_lds, hl, L.groups, kMoeMaxTokens, ntok,
+                                   [](uint32_t sl) { return sl; });
+        __syncthreads();
+        if (!on) {
+            stride = 0;
+            return s_zero;
+        }
+        return LDS_A ? dyn_lds + lane_off : hl + lane_off;
+    });
 #pragma unroll
     for (int i = 0; i < S; ++i) {
         const int sl = 2 * i + hh;
-        if (sl < NT) partial[wave][sl][n] = accf[i];
+        if (sl < NT) partial[tw][half][sl][n] = accf[i];
     }
     __syncthreads();
-    const int tid = threadIdx.x;
-    if (tid < NT * 32) {
-        const int sl = tid / 32, r = tid % 32;
-        const uint32_t row = t * 32u + r;
-        if (sl < (int)ntok && row < s.width) {
+    for (uint32_t idx = threadIdx.x; idx < 4u * NT * 32u; idx += blockDim.x) {
+        const uint32_t tt = idx / (NT * 32u), sl = (idx / 32u) % NT, r = idx % 32u;
+        const uint32_t row = (4u * blockIdx.x + tt) * 32u + r;
+        if (sl < ntok && row < s.width) {
             const int e = ws_ptr<int>(w, w.off_hexp)[a * kMoeMaxTokens + sl];
-            const float y = ldexpf(((partial[0][sl][r] + partial[1][sl][r]) + partial[2][sl][r]) +
-                                       partial[3][sl][r], -e);
+            const float y = ldexpf(partial[tt][0][sl][r] + partial[tt][1][sl][r], -e);
             ws_ptr<float>(w, w.off_ypart)[((uint64_t)a * kMoeMaxTokens + sl) * s.width + row] = y;
         }
     }
@@ -549,13 +688,24 @@ __global__ void __launch_bounds__(256) k_moe_combine(const MoeShape s, const Moe
     }
     const CombineEntry* comb = ws_ptr<CombineEntry>(w, w.off_combine) + (uint64_t)t * (s.top_k + 1u);
     const float* yp = ws_ptr<float>(w, w.off_ypart);
-    float acc = 0.0f;
     const uint32_t n = s.top_k + (s.has_shared ? 1u : 0u);
-    for (uint32_t k = 0; k < n; ++k) {
-        const CombineEntry ce = comb[k];
-        const float y = yp[((uint64_t)(ce.src >> 3) * kMoeMaxTokens + (ce.src & 7u)) * s.width + c];
-        acc = (s.semantics == kSemQwen && k < s.top_k) ? __fadd_rn(acc, __fmul_rn(y, ce.w))
-                                                       : __fadd_rn(acc, y);
+    // All loads first (independent), then the additions in the combine order.
+    float y[kMoeMaxTopK + 1];
+    float wt[kMoeMaxTopK + 1];
+#pragma unroll
+    for (uint32_t k = 0; k < kMoeMaxTopK + 1; ++k) {
+        if (k < n) {
+            const CombineEntry ce = comb[k];
+            wt[k] = ce.w;
+            y[k] = yp[((uint64_t)(ce.src >> 3) * kMoeMaxTokens + (ce.src & 7u)) * s.width + c];
+        }
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < kMoeMaxTopK + 1; ++k) {
+        if (k < n)
+            acc = (s.semantics == kSemQwen && k < s.top_k) ? __fadd_rn(acc, __fmul_rn(y[k], wt[k]))
+                                                           : __fadd_rn(acc, y[k]);
     }
     if (!isfinite(acc)) atomicOr(&hdr->status, kStatusNonFiniteOutput);
     in.out[i] = acc;
@@ -568,37 +718,55 @@ __global__ void __launch_bounds__(256) k_moe_combine(const MoeShape s, const Moe
 template <uint32_t FMT>
 static void launch_gateup_fmt(uint32_t slots, dim3 grid, const MoeShape& s, const MoeInputs& in,
                               const MoeWorkspace& w, hipStream_t st) {
-    switch (slots) {
-        case 1: hipLaunchKernelGGL((k_moe_gateup<FMT, 1>), grid, dim3(512), 0, st, s, in, w); break;
-        case 2: hipLaunchKernelGGL((k_moe_gateup<FMT, 2>), grid, dim3(512), 0, st, s, in, w); break;
-        case 4: hipLaunchKernelGGL((k_moe_gateup<FMT, 4>), grid, dim3(512), 0, st, s, in, w); break;
-        default: hipLaunchKernelGGL((k_moe_gateup<FMT, 8>), grid, dim3(512), 0, st, s, in, w); break;
+    const uint32_t bytes = s.width / 32u * slots * 128u;
+    const bool lds_a = bytes <= kMaxLdsLimbBytes;
+    const uint32_t shm = lds_a ? bytes : 0u;
+    const dim3 blk(512);
+    switch (slots * 2 + (lds_a ? 1 : 0)) {
+        case 2: hipLaunchKernelGGL((k_moe_gateup<FMT, 1, false>), grid, blk, shm, st, s, in, w); break;
+        case 3: hipLaunchKernelGGL((k_moe_gateup<FMT, 1, true>), grid, blk, shm, st, s, in, w); break;
+        case 4: hipLaunchKernelGGL((k_moe_gateup<FMT, 2, false>), grid, blk, shm, st, s, in, w); break;
+        case 5: hipLaunchKernelGGL((k_moe_gateup<FMT, 2, true>), grid, blk, shm, st, s, in, w); break;
+        case 8: hipLaunchKernelGGL((k_moe_gateup<FMT, 4, false>), grid, blk, shm, st, s, in, w); break;
+        case 9: hipLaunchKernelGGL((k_moe_gateup<FMT, 4, true>), grid, blk, shm, st, s, in, w); break;
+        case 16: hipLaunchKernelGGL((k_moe_gateup<FMT, 8, false>), grid, blk, shm, st, s, in, w); break;
+        default: hipLaunchKernelGGL((k_moe_gateup<FMT, 8, true>), grid, blk, shm, st, s, in, w); break;
     }
 }
 
 template <uint32_t FMT>
 static void launch_down_fmt(uint32_t slots, dim3 grid, const MoeShape& s, const MoeInputs& in,
                             const MoeWorkspace& w, hipStream_t st) {
-    switch (slots) {
-        case 1: hipLaunchKernelGGL((k_moe_down<FMT, 1>), grid, dim3(256), 0, st, s, in, w); break;
-        case 2: hipLaunchKernelGGL((k_moe_down<FMT, 2>), grid, dim3(256), 0, st, s, in, w); break;
-        case 4: hipLaunchKernelGGL((k_moe_down<FMT, 4>), grid, dim3(256), 0, st, s, in, w); break;
-        default: hipLaunchKernelGGL((k_moe_down<FMT, 8>), grid, dim3(256), 0, st, s, in, w); break;
+    const uint32_t bytes = s.inter / 32u * slots * 128u;
+    const bool lds_a = bytes <= kMaxLdsLimbBytes;
+    const uint32_t shm = lds_a ? bytes : 0u;
+    const dim3 blk(512);
+    switch (slots * 2 + (lds_a ? 1 : 0)) {
+        case 2: hipLaunchKernelGGL((k_moe_down<FMT, 1, false>), grid, blk, shm, st, s, in, w); break;
+        case 3: hipLaunchKernelGGL((k_moe_down<FMT, 1, true>), grid, blk, shm, st, s, in, w); break;
+        case 4: hipLaunchKernelGGL((k_moe_down<FMT, 2, false>), grid, blk, shm, st, s, in, w); break;
+        case 5: hipLaunchKernelGGL((k_moe_down<FMT, 2, true>), grid, blk, shm, st, s, in, w); break;
+        case 8: hipLaunchKernelGGL((k_moe_down<FMT, 4, false>), grid, blk, shm, st, s, in, w); break;
+        case 9: hipLaunchKernelGGL((k_moe_down<FMT, 4, true>), grid, blk, shm, st, s, in, w); break;
+        case 16: hipLaunchKernelGGL((k_moe_down<FMT, 8, false>), grid, blk, shm, st, s, in, w); break;
+        default: hipLaunchKernelGGL((k_moe_down<FMT, 8, true>), grid, blk, shm, st, s, in, w); break;
     }
 }
 
 hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
-                      hipStream_t st) {
+                      hipStream_t st, hipEvent_t* ev) {
     if (!moe_shape_ok(s)) return hipErrorInvalidValue;
     const uint32_t slots = limb_slots(s.tokens);
-    MoeHeader* hdr = reinterpret_cast<MoeHeader*>(w.base + w.off_header);
-    hipLaunchKernelGGL(k_moe_router, dim3((s.experts + 3) / 4), dim3(256), 0, st, s, in, w);
+    auto mark = [&](uint32_t stage) {
+        if (ev) (void)hipEventRecord(ev[stage], st);
+    };
+    mark(kStageRouter);
+    hipLaunchKernelGGL(k_moe_router, dim3(s.routing == kRouteGiven ? 1u : s.experts), dim3(256), 0, st, s, in, w);
+    mark(kStageRoute);
     hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(512), 0, st, s, in, w);
-    hipError_t e = launch_prep_limbs(in.x, 1, s.tokens, s.width, s.width, 0,
-                                     reinterpret_cast<int8_t*>(w.base + w.off_xlimbs),
-                                     reinterpret_cast<int*>(w.base + w.off_xexp), &hdr->status, st);
-    if (e != hipSuccess) return e;
-    const dim3 g_gu((s.inter + 31) / 32, w.max_active);
+    mark(kStagePrep);
+    mark(kStageGateUp);
+    const dim3 g_gu((s.inter + 63) / 64, w.max_active);
     switch (s.gate_type) {
         case VL_TYPE_IQ2_XXS: launch_gateup_fmt<VL_TYPE_IQ2_XXS>(slots, g_gu, s, in, w, st); break;
         case VL_TYPE_IQ3_XXS: launch_gateup_fmt<VL_TYPE_IQ3_XXS>(slots, g_gu, s, in, w, st); break;
@@ -606,8 +774,10 @@ hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace
         case VL_TYPE_Q8_0: launch_gateup_fmt<VL_TYPE_Q8_0>(slots, g_gu, s, in, w, st); break;
         default: return hipErrorInvalidValue;
     }
+    mark(kStageHPrep);
     hipLaunchKernelGGL(k_moe_hprep, dim3(kMoeMaxTokens, w.max_active), dim3(256), 0, st, s, w);
-    const dim3 g_dn((s.width + 31) / 32, w.max_active);
+    mark(kStageDown);
+    const dim3 g_dn((s.width + 127) / 128, w.max_active);
     switch (s.down_type) {
         case VL_TYPE_IQ2_XXS: launch_down_fmt<VL_TYPE_IQ2_XXS>(slots, g_dn, s, in, w, st); break;
         case VL_TYPE_IQ3_XXS: launch_down_fmt<VL_TYPE_IQ3_XXS>(slots, g_dn, s, in, w, st); break;
@@ -615,8 +785,10 @@ hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace
         case VL_TYPE_Q8_0: launch_down_fmt<VL_TYPE_Q8_0>(slots, g_dn, s, in, w, st); break;
         default: return hipErrorInvalidValue;
     }
+    mark(kStageCombine);
     const uint64_t total = (uint64_t)s.tokens * s.width;
     hipLaunchKernelGGL(k_moe_combine, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, st, s, in, w);
+    mark(kStageCount);
     return hipGetLastError();
 }
 

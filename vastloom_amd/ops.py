@@ -161,7 +161,8 @@ class MoeLayer:
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None, *,
                 table_ids: torch.Tensor | None = None, given_ids: torch.Tensor | None = None,
                 given_weights: torch.Tensor | None = None, stream=None,
-                check: bool = True) -> torch.Tensor:
+                check: bool = True, timeline: "Timeline | None" = None,
+                call_slot: int = 0) -> torch.Tensor:
         x2 = x.reshape(-1, self.width).contiguous()
         tokens = x2.shape[0]
         if out is None:
@@ -173,7 +174,11 @@ class MoeLayer:
                                 p(table_ids), p(given_ids), p(given_weights), x2.data_ptr(),
                                 out.data_ptr())
         s = _stream(stream)
-        call("vl_moe_layer", C.byref(cfg), C.byref(inputs), ws.data_ptr(), ws.numel(), s)
+        if timeline is None:
+            call("vl_moe_layer", C.byref(cfg), C.byref(inputs), ws.data_ptr(), ws.numel(), s)
+        else:
+            call("vl_moe_layer_profiled", C.byref(cfg), C.byref(inputs), ws.data_ptr(),
+                 ws.numel(), s, timeline.handle, call_slot)
         if check:
             raise_on_status(ws, s, "moe_layer")
         return out
@@ -185,6 +190,31 @@ class MoeLayer:
         call("vl_moe_read_routes", C.byref(cfg), self.workspace(tokens).data_ptr(),
              _stream(stream), ids.ctypes.data, w.ctypes.data)
         return ids, w
+
+
+class Timeline:
+    """HIP events around the stages of profiled layer calls (vl_timeline_*)."""
+
+    def __init__(self, calls: int):
+        h = C.c_void_p()
+        call("vl_timeline_create", calls, C.byref(h))
+        self.handle, self.calls = h, calls
+
+    def stage_ms(self, slot: int) -> dict[str, float]:
+        ms = (C.c_float * len(_lib.STAGES))()
+        call("vl_timeline_stage_ms", self.handle, slot, ms)
+        return dict(zip(_lib.STAGES, list(ms)))
+
+    def close(self) -> None:
+        if self.handle:
+            lib().vl_timeline_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def expert_ffn(expert: DeviceExpert, x: torch.Tensor, *, semantics: int,

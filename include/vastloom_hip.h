@@ -75,7 +75,8 @@ int vl_pack_matrix(uint32_t ggml_type, uint64_t rows, uint64_t cols, const void*
 int vl_dequantize(uint32_t ggml_type, uint64_t rows, uint64_t cols, const void* tiled_device,
                   float* out_device, void* stream);
 
-/* Workspace bytes vl_matvec needs for this shape and token count (1..8). */
+/* Workspace bytes vl_matvec needs for this shape and token count (1..8) on the current device
+ * (the size grows with the device's compute-unit count). */
 int vl_matvec_workspace(uint32_t ggml_type, uint64_t rows, uint64_t cols, uint32_t tokens,
                         uint64_t* bytes);
 
@@ -166,6 +167,7 @@ typedef struct vl_moe_inputs {
     float* out;                        /* [tokens][width] float32, device */
 } vl_moe_inputs;
 
+/* Workspace bytes vl_moe_layer needs for this configuration on the current device. */
 int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes);
 
 /* One MoE layer: router logits (float64 accumulation), routing, the selected experts' SwiGLU
@@ -184,15 +186,12 @@ int vl_moe_read_routes(const vl_moe_config* config, const void* workspace, void*
 /* ---- Stage timing (replaces the reference's steady_clock kernel_ms, which timed a whole
  * synchronous call: src/cuda/cuda_matvec_accelerator.cpp:258-311) ---------------------------- */
 
-/* Stages of one vl_moe_layer call, in launch order. */
+/* Stages of one vl_moe_layer call, in launch order: router logits and activation limbs;
+ * routing with the gate/up projections and SwiGLU; the down projections with the combine. */
 #define VL_STAGE_ROUTER 0u
-#define VL_STAGE_ROUTE 1u
-#define VL_STAGE_PREP 2u
-#define VL_STAGE_GATE_UP 3u
-#define VL_STAGE_H_PREP 4u
-#define VL_STAGE_DOWN 5u
-#define VL_STAGE_COMBINE 6u
-#define VL_STAGE_COUNT 7u
+#define VL_STAGE_GATE_UP 1u
+#define VL_STAGE_DOWN 2u
+#define VL_STAGE_COUNT 3u
 
 typedef struct vl_timeline vl_timeline;
 

@@ -50,7 +50,7 @@ _SIGNATURES = {
 }
 _RESTYPE_NONE = {"vl_timeline_destroy"}
 
-STAGES = ("router", "route", "prep", "gate_up", "h_prep", "down", "combine")
+STAGES = ("router", "gate_up", "down")
 
 
 class MoeConfig(C.Structure):

@@ -36,10 +36,15 @@ bool make_layout(uint32_t type, uint64_t rows, uint64_t cols, vl_tiled_layout* L
     return vl_make_layout(type, (uint32_t)rows, (uint32_t)cols, L) != 0;
 }
 
-// Workspace of one matvec call: status word, per-token exponents, input limbs.
+// The status word sits at the start of every workspace.
 constexpr uint64_t kStatusOffset = 0;
-constexpr uint64_t kExpOffset = 64;
-constexpr uint64_t kLimbOffset = 256;
+
+// Persistent blocks of the current device, or 0 with the error recorded.
+uint32_t blocks_or_fail() {
+    const uint32_t b = vl::stream_blocks();
+    if (b == 0) fail(VL_UNSUPPORTED, "no HIP device is current");
+    return b;
+}
 
 }  // namespace
 
@@ -95,7 +100,9 @@ int vl_matvec_workspace(uint32_t type, uint64_t rows, uint64_t cols, uint32_t to
     if (!make_layout(type, rows, cols, &L)) return fail(VL_UNSUPPORTED, "unsupported matrix");
     if (tokens == 0 || tokens > 8) return fail(VL_INVALID_ARGUMENT, "tokens must be 1..8");
     if (!bytes) return fail(VL_INVALID_ARGUMENT, "bytes is null");
-    *bytes = kLimbOffset + vl::limb_bytes((uint32_t)cols, tokens);
+    const uint32_t blocks = blocks_or_fail();
+    if (!blocks) return VL_UNSUPPORTED;
+    *bytes = vl::matvec_workspace_bytes(type, (uint32_t)rows, (uint32_t)cols, tokens, blocks);
     return VL_OK;
 }
 
@@ -112,19 +119,9 @@ int vl_matvec(uint32_t type, uint64_t rows, uint64_t cols, const void* tiled_dev
                     (unsigned long long)workspace_bytes, (unsigned long long)need);
     vl_tiled_layout L;
     make_layout(type, rows, cols, &L);
-    auto* ws = static_cast<uint8_t*>(workspace);
-    auto* status = reinterpret_cast<uint32_t*>(ws + kStatusOffset);
-    auto* xe = reinterpret_cast<int*>(ws + kExpOffset);
-    auto* xl = reinterpret_cast<int8_t*>(ws + kLimbOffset);
-    const auto s = static_cast<hipStream_t>(stream);
-    hipError_t e = vl::launch_fill_u32(status, 1, 0, s);
-    if (e == hipSuccess)
-        e = vl::launch_prep_limbs(x_device, 1, tokens, (uint32_t)cols, cols, 0, xl, xe, status, s);
-    if (e != hipSuccess) return hip_fail(e, "prep launch");
-    vl::QmvBatch batch{};
-    batch.inline_jobs[0] = vl::QmvJob{static_cast<const uint8_t*>(tiled_device), xl, xe, y_device,
-                                      (uint32_t)rows, (uint32_t)cols, tokens, (uint32_t)rows};
-    e = vl::launch_qmv(type, vl::limb_slots(tokens), batch, 1, L.tiles, (uint32_t)cols, status, s);
+    const hipError_t e = vl::launch_matvec(L, static_cast<const uint8_t*>(tiled_device), x_device,
+                                           tokens, y_device, static_cast<uint8_t*>(workspace),
+                                           vl::stream_blocks(), static_cast<hipStream_t>(stream));
     return e == hipSuccess ? VL_OK : hip_fail(e, "matvec launch");
 }
 
@@ -141,7 +138,9 @@ int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes) {
     vl::MoeShape s;
     if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
     if (!bytes) return fail(VL_INVALID_ARGUMENT, "bytes is null");
-    *bytes = vl::moe_workspace_bytes(s);
+    const uint32_t blocks = blocks_or_fail();
+    if (!blocks) return VL_UNSUPPORTED;
+    *bytes = vl::moe_workspace_bytes(s, blocks);
     return VL_OK;
 }
 
@@ -156,7 +155,9 @@ int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void*
         return fail(VL_INVALID_ARGUMENT, "routing needs the router weights");
     if (s.routing == vl::kRouteTable && !inputs->table_ids)
         return fail(VL_INVALID_ARGUMENT, "table routing needs table ids");
-    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, workspace);
+    const uint32_t blocks = blocks_or_fail();
+    if (!blocks) return VL_UNSUPPORTED;
+    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, blocks, workspace);
     if (workspace_bytes < ws.bytes)
         return fail(VL_INVALID_ARGUMENT, "workspace of %llu bytes is below the %llu needed",
                     (unsigned long long)workspace_bytes, (unsigned long long)ws.bytes);
@@ -208,7 +209,9 @@ int vl_moe_layer_profiled(const vl_moe_config* config, const vl_moe_inputs* inpu
     if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
     if (!inputs || !inputs->experts || !inputs->x || !inputs->out || !workspace)
         return fail(VL_INVALID_ARGUMENT, "null input pointer");
-    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, workspace);
+    const uint32_t blocks = blocks_or_fail();
+    if (!blocks) return VL_UNSUPPORTED;
+    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, blocks, workspace);
     if (workspace_bytes < ws.bytes) return fail(VL_INVALID_ARGUMENT, "workspace too small");
     const vl::MoeInputs in{reinterpret_cast<const vl::MoeExpert*>(inputs->experts),
                            inputs->router, inputs->bias, inputs->table_ids, inputs->given_ids,
@@ -233,7 +236,9 @@ int vl_moe_read_routes(const vl_moe_config* config, const void* workspace, void*
     vl::MoeShape s;
     if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
     if (!workspace || !ids_host || !weights_host) return fail(VL_INVALID_ARGUMENT, "null pointer");
-    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, const_cast<void*>(workspace));
+    const uint32_t blocks = blocks_or_fail();
+    if (!blocks) return VL_UNSUPPORTED;
+    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, blocks, const_cast<void*>(workspace));
     const uint64_t n = (uint64_t)s.tokens * s.top_k;
     hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
     if (e == hipSuccess)

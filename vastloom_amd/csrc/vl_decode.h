@@ -13,6 +13,14 @@
 // Lane layout: lane (n, hh) with n = lane % 32 the row within the tile and hh = lane / 32 the
 // K half; it decodes sub-blocks 2hh and 2hh+1, i.e. columns 16hh .. 16hh+15 of the group, in
 // column order (bytes 0..7 the first sub-block, 8..15 the second).
+//
+// Decode tables live in LDS. The 256- and 128-entry tables of IQ2_XXS and IQ3_XXS are held in
+// 32 copies, entry e of copy c at byte e * 256 + c * 8, and lane l reads copy l % 32: the 32
+// lanes of a half-wave then touch 32 different bank pairs whatever entries they look up, which
+// removes the bank conflicts of random lookups. The table address of entry e for a lane is
+// (e << 8) | lane_off with lane_off = (l % 32) * 8, formed by one v_perm_b32 when e is a byte
+// of a payload word and by a shift and a v_and_or_b32 otherwise. The tables start at LDS byte 0,
+// so the table bases fold into the DS instructions' immediate offsets.
 #ifndef VL_DECODE_H
 #define VL_DECODE_H
 
@@ -26,9 +34,13 @@ namespace vl {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-struct IqTables2 { uint64_t codes[256]; uint64_t sign[128]; };
-struct IqTables3 { uint64_t pm[256]; uint64_t sel[128]; };
-struct IqTables1 { uint64_t codes[2048]; };
+// LDS byte offsets of the replicated tables: B (128 entries) first, then A (256 entries), so
+// that both bases fit a DS instruction's 16-bit immediate offset.
+constexpr uint32_t kTabCopies = 32;
+constexpr uint32_t kTabB = 0;
+constexpr uint32_t kTabA = 128u * 256u;
+constexpr uint32_t kReplTableBytes = kTabA + 256u * 256u;  // 96 KiB
+constexpr uint32_t kIq1TableBytes = 2048u * 8u;            // 16 KiB, one copy
 
 __device__ __forceinline__ uint32_t lo32(uint64_t v) { return (uint32_t)v; }
 __device__ __forceinline__ uint32_t hi32(uint64_t v) { return (uint32_t)(v >> 32); }
@@ -37,61 +49,96 @@ __device__ __forceinline__ uint32_t perm(uint32_t high, uint32_t low, uint32_t s
     return __builtin_amdgcn_perm(high, low, sel);
 }
 
-// IQ2_XXS group: qs = four grid indices (one byte per sub-block), aux = four 7-bit sign fields
-// and the 4-bit scale in the top nibble.
-__device__ __forceinline__ i32x4 decode_iq2_xxs(uint32_t qs, uint32_t aux, int hh,
-                                                const IqTables2& t) {
-    const uint32_t q = qs >> (16 * hh);
-    const uint32_t a = aux >> (14 * hh);
-    const uint64_t s0 = t.codes[q & 0xffu] | t.sign[a & 0x7fu];
-    const uint64_t s1 = t.codes[(q >> 8) & 0xffu] | t.sign[(a >> 7) & 0x7fu];
-    i32x4 w;
-    w[0] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, lo32(s0));
-    w[1] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, hi32(s0));
-    w[2] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, lo32(s1));
-    w[3] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, hi32(s1));
-    return w;
+__device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t width) {
+    return __builtin_amdgcn_ubfe(v, off, width);
 }
 
-// IQ3_XXS group: qs8 = eight grid indices (two per sub-block, four lanes each), aux as IQ2_XXS.
-__device__ __forceinline__ i32x4 decode_iq3_xxs(uint64_t qs8, uint32_t aux, int hh,
-                                                const IqTables3& t) {
-    const uint32_t q = (uint32_t)(qs8 >> (32 * hh));
+__device__ __forceinline__ uint64_t lds_u64(const uint8_t* lds, uint32_t addr) {
+    return *reinterpret_cast<const uint64_t*>(lds + addr);
+}
+
+// (byte k of v) << 8 | lane_off, one v_perm_b32.
+__device__ __forceinline__ uint32_t byte_entry(uint32_t v, int k, uint32_t lane_off) {
+    return perm(v, lane_off, 0x0c0c0000u | ((4u + (uint32_t)k) << 8));
+}
+
+// IQ2_XXS group g of a superblock half (vl_layout.h): grid bytes in w[0..3], sign fields in
+// w[4..7]. Codes select from the palette {8, 25, 43, -8, -25, -43}.
+__device__ __forceinline__ i32x4 decode_iq2_xxs(const uint32_t (&w)[8], int g, uint32_t lane_off,
+                                                const uint8_t* lds) {
+    const int q = g >> 1, odd = g & 1;
+    const uint32_t gw = w[q], sw = w[4 + q];
+    const uint32_t a0 = byte_entry(gw, 2 * odd, lane_off);
+    const uint32_t a1 = byte_entry(gw, 2 * odd + 1, lane_off);
+    // Sign fields at bits 14*odd and 14*odd + 7, moved to bits 8..14: one shift, one and-or.
+    const uint32_t b0 = ((odd ? sw >> 6 : sw << 8) & 0x7f00u) | lane_off;
+    const uint32_t b1 = ((odd ? sw >> 13 : sw << 1) & 0x7f00u) | lane_off;
+    const uint64_t s0 = lds_u64(lds, kTabA + a0) | lds_u64(lds, kTabB + b0);
+    const uint64_t s1 = lds_u64(lds, kTabA + a1) | lds_u64(lds, kTabB + b1);
+    i32x4 f;
+    f[0] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, lo32(s0));
+    f[1] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, hi32(s0));
+    f[2] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, lo32(s1));
+    f[3] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, hi32(s1));
+    return f;
+}
+
+// IQ2_XXS scales of one superblock: own = this half's four scale bytes (top bytes of w[4..7],
+// scale nibble in bits 4..7); lo/hi = the bytes of groups 0..3 and 4..7 once both halves'
+// words are known.
+__device__ __forceinline__ uint32_t iq2_scale_bytes(const uint32_t (&w)[8]) {
+    return perm(w[5], w[4], 0x0c0c0703u) | perm(w[7], w[6], 0x07030c0cu);
+}
+
+// 2s+1 from a scale byte (nibble in bits 4..7): (byte >> 3) | 1.
+__device__ __forceinline__ int odd_scale(uint32_t bytes, int k) {
+    return (int)(bfe(bytes, 8u * (uint32_t)k + 3u, 5) | 1u);
+}
+
+// IQ3_XXS group: q = the lane's four grid bytes (two per sub-block), aux = the group's sign and
+// scale word. Magnitude entries hold the four positive values in the low word and their
+// negations in the high word; sign entries select per lane.
+__device__ __forceinline__ i32x4 decode_iq3_xxs(uint32_t q, uint32_t aux, int hh,
+                                                uint32_t lane_off, const uint8_t* lds) {
     const uint32_t a = aux >> (14 * hh);
-    const uint64_t sel0 = t.sel[a & 0x7fu];
-    const uint64_t sel1 = t.sel[(a >> 7) & 0x7fu];
-    const uint64_t g00 = t.pm[q & 0xffu], g01 = t.pm[(q >> 8) & 0xffu];
-    const uint64_t g10 = t.pm[(q >> 16) & 0xffu], g11 = t.pm[q >> 24];
-    i32x4 w;
-    w[0] = (int)perm(hi32(g00), lo32(g00), lo32(sel0));
-    w[1] = (int)perm(hi32(g01), lo32(g01), hi32(sel0));
-    w[2] = (int)perm(hi32(g10), lo32(g10), lo32(sel1));
-    w[3] = (int)perm(hi32(g11), lo32(g11), hi32(sel1));
-    return w;
+    const uint64_t sel0 = lds_u64(lds, kTabB + (((a << 8) & 0x7f00u) | lane_off));
+    const uint64_t sel1 = lds_u64(lds, kTabB + (((a << 1) & 0x7f00u) | lane_off));
+    const uint64_t g00 = lds_u64(lds, kTabA + byte_entry(q, 0, lane_off));
+    const uint64_t g01 = lds_u64(lds, kTabA + byte_entry(q, 1, lane_off));
+    const uint64_t g10 = lds_u64(lds, kTabA + byte_entry(q, 2, lane_off));
+    const uint64_t g11 = lds_u64(lds, kTabA + byte_entry(q, 3, lane_off));
+    i32x4 f;
+    f[0] = (int)perm(hi32(g00), lo32(g00), lo32(sel0));
+    f[1] = (int)perm(hi32(g01), lo32(g01), hi32(sel0));
+    f[2] = (int)perm(hi32(g10), lo32(g10), lo32(sel1));
+    f[3] = (int)perm(hi32(g11), lo32(g11), hi32(sel1));
+    return f;
 }
 
 // IQ1_S group: qs4 = low 8 bits of the four 11-bit grid indices, qh = the group's 16-bit word
 // (3 high index bits per sub-block, 3-bit scale at bit 12, delta sign at bit 15).
 __device__ __forceinline__ i32x4 decode_iq1_s(uint32_t qs4, uint32_t qh, int hh,
-                                              const IqTables1& t) {
+                                              const uint8_t* lds) {
+    const uint64_t* codes = reinterpret_cast<const uint64_t*>(lds);
     const int s0 = 2 * hh;
     const uint32_t i0 = ((qs4 >> (8 * s0)) & 0xffu) | (((qh >> (3 * s0)) & 7u) << 8);
     const uint32_t i1 = ((qs4 >> (8 * s0 + 8)) & 0xffu) | (((qh >> (3 * s0 + 3)) & 7u) << 8);
     const uint64_t dm = (qh & 0x8000u) ? 0x0404040404040404ull : 0ull;
-    const uint64_t c0 = t.codes[i0] | dm;
-    const uint64_t c1 = t.codes[i1] | dm;
-    i32x4 w;
-    w[0] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, lo32(c0));
-    w[1] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, hi32(c0));
-    w[2] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, lo32(c1));
-    w[3] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, hi32(c1));
-    return w;
+    const uint64_t c0 = codes[i0] | dm;
+    const uint64_t c1 = codes[i1] | dm;
+    i32x4 f;
+    f[0] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, lo32(c0));
+    f[1] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, hi32(c0));
+    f[2] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, lo32(c1));
+    f[3] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, hi32(c1));
+    return f;
 }
 
 // Exact binary16 -> binary32 (v_cvt_f32_f16; fp16 denormals are preserved on gfx9).
-__device__ __forceinline__ float half_bits_to_float(uint16_t bits) {
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    const uint16_t b = (uint16_t)bits;
     _Float16 h;
-    __builtin_memcpy(&h, &bits, sizeof h);
+    __builtin_memcpy(&h, &b, sizeof h);
     return (float)h;
 }
 

@@ -1,29 +1,49 @@
 // HIP kernels for the quantized routed-expert path on gfx950 (MI355X).
 //
-//   k_pack          GGUF block bytes -> tiled device layout (vl_layout.h), once per resident matrix
-//   k_dequant       tiled matrix -> float32 rows, through the same decoders as the matvec; used to
-//                   prove the decode bit-exact against the reference
-//   k_prep_limbs    float32 activations -> int8 limbs + per-token exponent (the MFMA A operand)
-//   k_qmv           batched quantized matvec: per 32-row tile, int8 32x32x32 MFMA with the
-//                   decoded weights as B and up to 8 tokens x 4 limbs as A
+//   k_pack      GGUF block bytes -> tiled device layout (vl_layout.h), once per resident matrix
+//   k_dequant   tiled matrix -> float32 rows, through the same chunk loads and decoders as the
+//               matvec; used to prove the decode bit-exact against the reference
+//   k_prep_x    float32 activations -> int8 limbs, one exponent per 256 columns and token
+//   k_matvec    persistent quantized matvec (vl_stream.h): every wave streams an equal share of
+//               the matrix's (tile, superblock) units; the last wave of each tile adds the
+//               tile's partials in a fixed order and writes the rows
 //
-// Numerics of k_qmv: every product w*x is formed exactly in integers (weights are exact small
-// integers times a per-group float factor, activations are 30-bit fixed point per token); each
-// group's int32 MFMA result is scaled by the group's integer scale, summed exactly over the
-// superblock, converted to float once per superblock, and the four waves' K partials are added
-// in a fixed order. The result is deterministic and its error is a few float roundings of the
-// row's partial sums, well inside 1e-5 * |w| * |x|.
+// Numerics of k_matvec: every product w*x is formed exactly in integers (weights are exact small
+// integers times a per-group float factor, activations are 30-bit fixed point per 256-column
+// block); each group's int32 MFMA result is scaled by the group's integer scale, summed exactly
+// over the superblock and converted to float once per superblock. The result is deterministic
+// and its error is a few float roundings of the row's partial sums, well inside
+// 1e-5 * |w| * |x|.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "vl_decode.h"
-#include "vl_qmv_core.h"
 #include "vl_kernels.h"
 #include "vl_layout.h"
-#include "vl_tables.h"
+#include "vl_stream.h"
 
 namespace vl {
 
+uint32_t stream_blocks() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    return cus > 0 ? (uint32_t)cus : 0u;
+}
+
+hipError_t ensure_dynamic_lds(const void* kernel, uint32_t bytes) {
+    static thread_local const void* done[128];
+    static thread_local uint32_t limit[128];
+    static thread_local uint32_t n = 0;
+    for (uint32_t i = 0; i < n; ++i)
+        if (done[i] == kernel && limit[i] >= bytes) return hipSuccess;
+    const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) return e;
+    if (n < 128) {
+        done[n] = kernel;
+        limit[n++] = bytes;
+    }
+    return hipSuccess;
+}
 
 // ------------------------------------------------------------------------------------------
 // Pack: GGUF -> tiled. One thread per (row, superblock) for the IQ formats and per (row,
@@ -32,6 +52,10 @@ namespace vl {
 
 __device__ __forceinline__ void copy_bytes(uint8_t* dst, const uint8_t* src, int n, bool zero) {
     for (int i = 0; i < n; ++i) dst[i] = zero ? 0 : src[i];
+}
+
+__device__ __forceinline__ uint32_t ld_u32_bytes(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
 
 __global__ void k_pack(vl_tiled_layout L, const uint8_t* __restrict__ gguf,
@@ -49,13 +73,25 @@ __global__ void k_pack(vl_tiled_layout L, const uint8_t* __restrict__ gguf,
     uint8_t* S = out + L.plane2;
     switch (L.type) {
         case VL_TYPE_IQ2_XXS: {
-            S = out + L.plane1;
-            for (uint32_t g = 0; g < 8; ++g) {
-                const uint32_t G = 8u * b + g;
-                uint8_t* dst = out + (((uint64_t)t * (NG / 2) + G / 2) * 32u + j) * 16u + (G % 2) * 8u;
-                copy_bytes(dst, src + 2 + 8 * g, 8, pad);
+            // GGUF group g: 4 grid bytes at 2 + 8g, then the sign/scale word.
+            uint32_t grid[8], aux[8];
+            for (int g = 0; g < 8; ++g) {
+                grid[g] = pad ? 0u : ld_u32_bytes(src + 2 + 8 * g);
+                aux[g] = pad ? 0u : ld_u32_bytes(src + 6 + 8 * g);
             }
-            copy_bytes(S + (((uint64_t)t * NB + b) * 32u + j) * 2u, src, 2, pad);
+            for (uint32_t h = 0; h < 2; ++h) {
+                uint32_t wv[8];
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t ga = grid[2 * q] >> (16 * h), gb = grid[2 * q + 1] >> (16 * h);
+                    wv[q] = (ga & 0xffffu) | ((gb & 0xffffu) << 16);
+                    const uint32_t sa = aux[2 * q] >> (14 * h), sb = aux[2 * q + 1] >> (14 * h);
+                    wv[4 + q] = (sa & 0x3fffu) | ((sb & 0x3fffu) << 14) | ((aux[4 * h + q] >> 28) << 28);
+                }
+                uint32_t* dst = reinterpret_cast<uint32_t*>(
+                    out + ((((uint64_t)t * NB + b) * 2u + h) * 32u + j) * 32u);
+                for (int q = 0; q < 8; ++q) dst[q] = wv[q];
+            }
+            copy_bytes(out + L.plane1 + (((uint64_t)t * NB + b) * 32u + j) * 2u, src, 2, pad);
             break;
         }
         case VL_TYPE_IQ3_XXS: {
@@ -107,35 +143,43 @@ template <uint32_t FMT>
 __global__ void __launch_bounds__(256) k_dequant(vl_tiled_layout L, const uint8_t* __restrict__ w,
                                                  float* __restrict__ out) {
 #pragma clang fp contract(off)
-    __shared__ LdsTables lds;
-    load_tables<FMT>(lds);
+    extern __shared__ __align__(16) uint8_t lds[];
+    fill_tables<FMT>(lds);
     __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t n = lane & 31;
-    const int hh = lane >> 5;
-    const uint32_t units = FMT == VL_TYPE_Q8_0 ? L.groups : L.superblocks;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t n = lane & 31u;
+    const int hh = (int)(lane >> 5);
+    const uint32_t units = units_per_row(FMT, L.cols);
     const uint64_t item = (uint64_t)blockIdx.x * 4u + wave;
     if (item >= (uint64_t)L.tiles * units) return;
-    const uint32_t t = (uint32_t)(item / units), u = (uint32_t)(item % units);
+    const uint32_t t = (uint32_t)(item / units), c = (uint32_t)(item % units);
     const uint32_t row = t * 32u + n;
-    UnitPayload up;
-    load_unit<FMT>(L, w, t, n, hh, u, up);
-    uint4 a0 = make_uint4(0, 0, 0, 0), a1 = a0;
-    if (FMT == VL_TYPE_IQ3_XXS) load_iq3_aux(L, w, t, n, u, a0, a1);
-    const float df = half_bits_to_float(up.d) * unit_factor<FMT>();
-    if (row >= L.rows) return;
-    const int ngroups = FMT == VL_TYPE_Q8_0 ? 1 : 8;
-    for (int g = 0; g < ngroups; ++g) {
-        int sc = 1;
-        i32x4 frag;
-        if (FMT == VL_TYPE_Q8_0) {
-            frag[0] = (int)up.p[0].x; frag[1] = (int)up.p[0].y;
-            frag[2] = (int)up.p[0].z; frag[3] = (int)up.p[0].w;
-        } else {
-            frag = decode_group<FMT>(up, a0, a1, g, hh, lds, sc);
+    Chunk ch;
+    load_chunk<FMT>(tile_ref<FMT>(L, w, t), c, L.groups, ch);
+    if (FMT == VL_TYPE_Q8_0) {
+        if (row >= L.rows) return;
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t G = 4u * c + b;
+            if (G >= L.groups) break;
+            const uint4& q = b == 0 ? ch.q0 : b == 1 ? ch.q1 : b == 2 ? ch.q2 : ch.q3;
+            const float d = half_bits_to_float((b < 2 ? ch.d0 : ch.d1) >> (16 * (b & 1)));
+            float* dst = out + (uint64_t)row * L.cols + G * 32u + 16u * hh;
+            for (int e = 0; e < 16; ++e) {
+                const int qv = (int)(int8_t)(word(q, e >> 2) >> (8 * (e & 3)));
+                dst[e] = (float)qv * d;
+            }
         }
-        const uint64_t col0 = (uint64_t)u * (FMT == VL_TYPE_Q8_0 ? 32u : 256u) + 32u * g + 16u * hh;
-        float* dst = out + (uint64_t)row * L.cols + col0;
+        return;
+    }
+    ChunkDecoder<FMT> dec;
+    dec.init(ch);  // all lanes: the IQ2_XXS halves exchange scale bytes
+    if (row >= L.rows) return;
+    const float df = half_bits_to_float(ch.d0) * unit_factor<FMT>();
+    const uint32_t lane_off = n * 8u;
+    for (int g = 0; g < 8; ++g) {
+        int sc = 1;
+        const i32x4 frag = dec.group(ch, g, lane_off, hh, lds, sc);
+        float* dst = out + (uint64_t)row * L.cols + (uint64_t)c * 256u + 32u * g + 16u * hh;
         for (int e = 0; e < 16; ++e) {
             const int q = (int)(int8_t)((uint32_t)frag[e >> 2] >> (8 * (e & 3)));
             dst[e] = (float)(q * sc) * df;
@@ -143,188 +187,241 @@ __global__ void __launch_bounds__(256) k_dequant(vl_tiled_layout L, const uint8_
     }
 }
 
-hipError_t launch_dequant(const vl_tiled_layout& L, const uint8_t* tiled, float* out,
-                          hipStream_t stream) {
-    const uint64_t units = (uint64_t)L.tiles * (L.type == VL_TYPE_Q8_0 ? L.groups : L.superblocks);
-    const dim3 grid((uint32_t)((units + 3) / 4)), block(256);
-    switch (L.type) {
-        case VL_TYPE_IQ2_XXS: hipLaunchKernelGGL(k_dequant<VL_TYPE_IQ2_XXS>, grid, block, 0, stream, L, tiled, out); break;
-        case VL_TYPE_IQ3_XXS: hipLaunchKernelGGL(k_dequant<VL_TYPE_IQ3_XXS>, grid, block, 0, stream, L, tiled, out); break;
-        case VL_TYPE_IQ1_S: hipLaunchKernelGGL(k_dequant<VL_TYPE_IQ1_S>, grid, block, 0, stream, L, tiled, out); break;
-        case VL_TYPE_Q8_0: hipLaunchKernelGGL(k_dequant<VL_TYPE_Q8_0>, grid, block, 0, stream, L, tiled, out); break;
-        default: return hipErrorInvalidValue;
-    }
+template <uint32_t FMT>
+static hipError_t launch_dequant_fmt(const vl_tiled_layout& L, const uint8_t* tiled, float* out,
+                                     hipStream_t stream) {
+    const uint64_t items = (uint64_t)L.tiles * units_per_row(FMT, L.cols);
+    const uint32_t shm = table_bytes<FMT>() + 16u;
+    const hipError_t e = ensure_dynamic_lds((const void*)k_dequant<FMT>, shm);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_dequant<FMT>, dim3((uint32_t)((items + 3) / 4)), dim3(256), shm, stream,
+                       L, tiled, out);
     return hipGetLastError();
 }
 
+hipError_t launch_dequant(const vl_tiled_layout& L, const uint8_t* tiled, float* out,
+                          hipStream_t stream) {
+    switch (L.type) {
+        case VL_TYPE_IQ2_XXS: return launch_dequant_fmt<VL_TYPE_IQ2_XXS>(L, tiled, out, stream);
+        case VL_TYPE_IQ3_XXS: return launch_dequant_fmt<VL_TYPE_IQ3_XXS>(L, tiled, out, stream);
+        case VL_TYPE_IQ1_S: return launch_dequant_fmt<VL_TYPE_IQ1_S>(L, tiled, out, stream);
+        case VL_TYPE_Q8_0: return launch_dequant_fmt<VL_TYPE_Q8_0>(L, tiled, out, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 // ------------------------------------------------------------------------------------------
-// Activations -> limbs. One block per (set, token): max |x|, exponent, then the four digits.
+// Matvec.
 // ------------------------------------------------------------------------------------------
 
-__device__ __forceinline__ float block_max(float v, float* scratch) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (lane == 0) scratch[wave] = v;
-    __syncthreads();
-    float m = 0.0f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) m = fmaxf(m, scratch[i]);
-    __syncthreads();
+// Workspace of one matvec call.
+struct MatvecWs {
+    uint64_t off_xexp, off_xflags, off_xlimbs, off_counters, off_rec, bytes;
+    uint32_t xblocks, slots, tiles;
+};
+
+static inline uint64_t al256(uint64_t v) { return (v + 255u) & ~uint64_t(255); }
+
+static MatvecWs matvec_ws(uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t blocks) {
+    MatvecWs m{};
+    m.xblocks = exp_blocks(cols);
+    m.slots = limb_slots(tokens);
+    m.tiles = (rows + 31u) / 32u;
+    uint64_t o = 256;  // status word and padding
+    m.off_xexp = o; o = al256(o + (uint64_t)m.xblocks * 8u * 4u);
+    m.off_xflags = o; o = al256(o + (uint64_t)m.xblocks * 8u * 4u);
+    m.off_xlimbs = o; o = al256(o + (uint64_t)(cols / 32u) * m.slots * 128u);
+    m.off_counters = o; o = al256(o + (uint64_t)m.tiles * 4u);
+    m.off_rec = o; o = al256(o + ((uint64_t)blocks * kStreamWaves + m.tiles) * m.slots * 64u * 4u);
+    m.bytes = o;
     return m;
 }
 
-__global__ void __launch_bounds__(256) k_prep_limbs(const float* __restrict__ x, uint32_t tokens,
-                                                    uint32_t cols, uint64_t x_stride,
-                                                    uint64_t set_stride, int8_t* __restrict__ xl,
-                                                    int* __restrict__ xe, uint32_t* status) {
-    __shared__ float scratch[16];
-    const uint32_t tok = blockIdx.x, set = blockIdx.y;
-    const uint32_t slots = tokens <= 1 ? 1u : tokens <= 2 ? 2u : tokens <= 4 ? 4u : 8u;
-    const float* xs = x + set * set_stride + tok * x_stride;
-    int8_t* out = xl + (uint64_t)set * (cols / 32u) * slots * 128u;
-    float m = 0.0f;
-    bool finite = true;
-    for (uint32_t k = threadIdx.x; k < cols; k += blockDim.x) {
-        const float v = xs[k];
-        finite &= isfinite(v);
-        m = fmaxf(m, fabsf(v));
+uint64_t matvec_workspace_bytes(uint32_t, uint32_t rows, uint32_t cols, uint32_t tokens,
+                                uint32_t blocks) {
+    return matvec_ws(rows, cols, tokens, blocks).bytes;
+}
+
+__global__ void __launch_bounds__(256) k_prep_x(const float* __restrict__ x, uint32_t cols,
+                                                uint32_t tokens, uint8_t* ws, MatvecWs m) {
+    if (blockIdx.x == 0) {
+        if (threadIdx.x == 0) *reinterpret_cast<uint32_t*>(ws) = 0;
+        uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + m.off_counters);
+        for (uint32_t i = threadIdx.x; i < m.tiles; i += blockDim.x) cnt[i] = 0;
     }
-    if (!finite) atomicOr(status, kStatusNonFiniteInput);
-    m = block_max(finite ? m : 0.0f, scratch);
-    int q = 0;
-    frexpf(m, &q);
-    const int e = m > 0.0f ? 30 - q : 0;
-    if (threadIdx.x == 0) xe[set * 8u + tok] = e;
-    for (uint32_t k4 = threadIdx.x * 4u; k4 < cols; k4 += blockDim.x * 4u) {
-        uint32_t packed[4] = {0, 0, 0, 0};
-        for (int i = 0; i < 4; ++i) {
-            const float v = xs[k4 + i];
-            int X = isfinite(v) ? (int)rintf(ldexpf(v, e)) : 0;
-            for (int l = 0; l < 4; ++l) {
-                const int digit = l < 3 ? (int)(int8_t)(X & 0xff) : X;
-                packed[l] |= ((uint32_t)digit & 0xffu) << (8 * i);
-                X = (X - digit) >> 8;
+    prep_x_block(x, cols, cols, tokens, m.slots, blockIdx.x,
+                 reinterpret_cast<int8_t*>(ws + m.off_xlimbs), reinterpret_cast<int*>(ws + m.off_xexp),
+                 reinterpret_cast<uint32_t*>(ws + m.off_xflags));
+}
+
+template <uint32_t FMT, int NT, bool LDS>
+struct Matvec {
+    uint32_t chunks, nmat, ng;
+    ASrc<LDS, NT * 128u> as;
+    float hscale;
+    vl_tiled_layout L;
+    const uint8_t* W;
+    uint32_t tokens, UJ, TU, NW, wid;
+    uint32_t stage_off, scale_off;
+    const uint8_t* lds;
+    const uint8_t* ws;
+    MatvecWs m;
+    float* y;
+
+    __device__ TileRef tref(uint32_t j, uint32_t) const { return tile_ref<FMT>(L, W, j); }
+
+    __device__ void job_begin(uint32_t) {
+        const uint32_t mm = threadIdx.x & 31u, kh = (threadIdx.x >> 5) & 1u;
+        const uint32_t sl = a_slot(mm), limb = a_limb(mm);
+        const uint32_t off = (sl < tokens ? sl : 0u) * 128u + limb * 32u + 16u * kh;
+        if (LDS) as.off = stage_off + off;
+        else as.ptr = reinterpret_cast<const int8_t*>(ws + m.off_xlimbs) + off;
+    }
+
+    __device__ void scales(uint32_t, uint32_t c, float (&fs)[NT]) const {
+        const uint32_t eb = FMT == VL_TYPE_Q8_0 ? c / 2u : c;
+        const float* sc = reinterpret_cast<const float*>(lds + scale_off) + 8u * eb;
+#pragma unroll
+        for (int s = 0; s < NT; ++s) fs[s] = sc[s];
+    }
+
+    __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&)[NT]) const {
+        const uint32_t lane = threadIdx.x & 63u;
+        float* rec = reinterpret_cast<float*>(const_cast<uint8_t*>(ws) + m.off_rec);
+        float* r = rec + (uint64_t)(wid + j) * (NT * 64u);
+#pragma unroll
+        for (int s = 0; s < NT; ++s) store_shared(r + s * 64u + lane, m0[s]);
+        const uint32_t first = wave_of_unit(j * UJ, NW, TU);
+        const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
+        uint32_t* cnt = reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(ws) + m.off_counters);
+        if (!arrive(cnt + j, last - first + 1u)) return;
+        const uint32_t n = lane & 31u, hh = lane >> 5, row = j * 32u + n;
+        bool bad = false;
+#pragma unroll
+        for (int i = 0; i < (NT + 1) / 2; ++i) {
+            const uint32_t sl = 2u * i + hh;
+            if (sl < tokens) {
+                float v = 0.0f;
+                for (uint32_t k = first; k <= last; ++k) {
+                    const float* rr = rec + (uint64_t)(k + j) * (NT * 64u) + sl * 64u;
+                    v += load_shared(rr + n) + load_shared(rr + 32u + n);
+                }
+                if (row < L.rows) {
+                    bad |= !isfinite(v);
+                    *gp(y + (uint64_t)sl * L.rows + row) = v;
+                }
             }
         }
-        const uint64_t base = ((uint64_t)(k4 / 32u) * slots + tok) * 128u + (k4 % 32u);
-        for (int l = 0; l < 4; ++l) *reinterpret_cast<uint32_t*>(out + base + 32u * l) = packed[l];
+        if (__any(bad) && lane == 0)
+            or_bits(reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(ws)), kStatusNonFiniteOutput);
     }
-}
+};
 
-hipError_t launch_prep_limbs(const float* x, uint32_t sets, uint32_t tokens, uint32_t cols,
-                             uint64_t x_stride, uint64_t set_stride, int8_t* xl, int* xe,
-                             uint32_t* status, hipStream_t stream) {
-    if (tokens == 0 || tokens > 8 || cols % 32u != 0 || sets == 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_prep_limbs, dim3(tokens, sets), dim3(256), 0, stream, x, tokens, cols,
-                       x_stride, set_stride, xl, xe, status);
-    return hipGetLastError();
-}
-
-// ------------------------------------------------------------------------------------------
-// Batched quantized matvec.
-// Block = 4 waves on one 32-row tile of one job; wave w takes a contiguous quarter of the
-// units (superblocks, or Q8_0 blocks). Lane (n, hh): row n of the tile, K half hh of each
-// group; for the A operand it supplies limb (n % 4) of token 2*(n/8) + (n/4)%2.
-// ------------------------------------------------------------------------------------------
-
-template <uint32_t FMT, int NT, bool LDS_A>
-__global__ void __launch_bounds__(256) k_qmv(const QmvBatch batch, uint32_t* status) {
-    __shared__ LdsTables lds;
-    __shared__ float partial[4][NT][32];
-    extern __shared__ __align__(16) int8_t dyn_lds[];
-    __shared__ __align__(16) int8_t s_zero[16];
-    const QmvJob job = batch.device_jobs ? batch.device_jobs[blockIdx.y]
-                                         : batch.inline_jobs[blockIdx.y];
-    vl_tiled_layout L;
-    if (job.rows == 0 || !vl_make_layout(FMT, job.rows, job.cols, &L)) return;
-    const uint32_t t = blockIdx.x;
-    if (t >= L.tiles) return;
-    constexpr int S = Acc<NT>::kSlots;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t n = lane & 31;
-    const int hh = lane >> 5;
-    const uint32_t chunks = chunks_of<FMT>(L);
-    const int slot = a_slot_of_lane();
-    const bool on = slot < (int)job.tokens;
-    const uint32_t lane_off = ((uint32_t)slot * 4u + a_limb_of_lane()) * 32u + 16u * hh;
-    float accf[S];
-    tile_partial<FMT, NT>(L, job.w, t, chunks * wave / 4u, chunks * (wave + 1) / 4u,
-                          NT * 128u, lds, accf, [&](uint32_t& stride) -> const int8_t* {
-        load_tables<FMT>(lds);
-        if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(s_zero)[threadIdx.x] = 0;
-        if (LDS_A) stage_limbs<NT>(dyn_lds, job.xl, L.groups, NT, job.tokens,
-                                   [](uint32_t s) { return s; });
-        __syncthreads();
-        if (!on) {
-            stride = 0;
-            return s_zero;
-        }
-        return LDS_A ? dyn_lds + lane_off : job.xl + lane_off;
-    });
-#pragma unroll
-    for (int i = 0; i < S; ++i) {
-        const int tok = 2 * i + hh;
-        if (tok < NT) partial[wave][tok][n] = accf[i];
+template <uint32_t FMT, int NT, bool LDS>
+__global__ void __launch_bounds__(kStreamThreads) k_matvec(vl_tiled_layout L, const uint8_t* W,
+                                                           uint32_t tokens, float* y, uint8_t* ws,
+                                                           MatvecWs m) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    fill_tables<FMT>(lds);
+    constexpr uint32_t TB = table_bytes<FMT>();
+    const uint32_t stage_bytes = LDS ? (L.cols / 32u) * NT * 128u : 0u;
+    const uint32_t scale_off = TB + stage_bytes;
+    if (LDS) {
+        const uint4* src = reinterpret_cast<const uint4*>(ws + m.off_xlimbs);
+        uint4* dst = reinterpret_cast<uint4*>(lds + TB);
+        for (uint32_t i = threadIdx.x; i < stage_bytes / 16u; i += blockDim.x) dst[i] = ld_u4(src + i);
+    }
+    {
+        const int* xe = reinterpret_cast<const int*>(ws + m.off_xexp);
+        float* sc = reinterpret_cast<float*>(lds + scale_off);
+        for (uint32_t i = threadIdx.x; i < m.xblocks * 8u; i += blockDim.x)
+            sc[i] = (i & 7u) < tokens ? __builtin_amdgcn_ldexpf(1.0f, -*gp(xe + i)) : 0.0f;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const uint32_t* xf = reinterpret_cast<const uint32_t*>(ws + m.off_xflags);
+        uint32_t bits = 0;
+        for (uint32_t xb = 0; xb < m.xblocks; ++xb)
+            for (uint32_t t = 0; t < tokens; ++t)
+                if (xf[8u * xb + t]) bits = kStatusNonFiniteInput;
+        if (bits) or_bits(reinterpret_cast<uint32_t*>(ws), bits);
     }
     __syncthreads();
-    const int tid = threadIdx.x;
-    if (tid < NT * 32) {
-        const int tok = tid / 32, r = tid % 32;
-        const uint32_t row = t * 32u + r;
-        if (tok < (int)job.tokens && row < job.rows) {
-            const float sum = ((partial[0][tok][r] + partial[1][tok][r]) + partial[2][tok][r]) +
-                              partial[3][tok][r];
-            const float y = ldexpf(sum, -job.xe[tok]);
-            if (!isfinite(y)) atomicOr(status, kStatusNonFiniteOutput);
-            job.y[(uint64_t)tok * job.y_stride + row] = y;
-        }
+    Matvec<FMT, NT, LDS> pol;
+    pol.L = L;
+    pol.W = W;
+    pol.tokens = tokens;
+    pol.chunks = units_per_row(FMT, L.cols);
+    pol.nmat = 1;
+    pol.ng = L.groups;
+    pol.UJ = pol.chunks;
+    pol.TU = L.tiles * pol.UJ;
+    pol.NW = active_waves(gridDim.x * kStreamWaves, pol.TU);
+    pol.wid = blockIdx.x * kStreamWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    pol.stage_off = TB;
+    pol.scale_off = scale_off;
+    pol.lds = lds;
+    pol.ws = ws;
+    pol.m = m;
+    pol.y = y;
+    pol.hscale = (threadIdx.x & 32u) ? 65536.0f : 1.0f;
+    stream_range<FMT, NT, LDS>(pol, range_begin(pol.wid, pol.NW, pol.TU),
+                               range_begin(pol.wid + 1u, pol.NW, pol.TU), lds);
+}
+
+// Dynamic LDS of one workgroup on gfx950 (the matvec kernel has no static LDS).
+constexpr uint32_t kMatvecLdsBudget = 160u * 1024u - 256u;
+
+template <uint32_t FMT, int NT>
+static hipError_t launch_matvec_nt(const vl_tiled_layout& L, const uint8_t* w, uint32_t tokens,
+                                   float* y, uint8_t* ws, const MatvecWs& m, uint32_t blocks,
+                                   hipStream_t st) {
+    const uint32_t stage = (L.cols / 32u) * NT * 128u;
+    const uint32_t TB = table_bytes<FMT>();
+    const uint32_t base = TB + m.xblocks * 8u * 4u;
+    if (base + stage <= kMatvecLdsBudget) {
+        const uint32_t shm = base + stage;
+        const hipError_t e = ensure_dynamic_lds((const void*)k_matvec<FMT, NT, true>, shm);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((k_matvec<FMT, NT, true>), dim3(blocks), dim3(kStreamThreads), shm, st,
+                           L, w, tokens, y, ws, m);
+    } else {
+        const uint32_t shm = base;
+        const hipError_t e = ensure_dynamic_lds((const void*)k_matvec<FMT, NT, false>, shm);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((k_matvec<FMT, NT, false>), dim3(blocks), dim3(kStreamThreads), shm, st,
+                           L, w, tokens, y, ws, m);
     }
+    return hipGetLastError();
 }
 
 template <uint32_t FMT>
-static hipError_t launch_qmv_fmt(uint32_t slots, const QmvBatch& jobs, uint32_t njobs,
-                                 uint32_t max_tiles, uint32_t lds_cols, uint32_t* status,
-                                 hipStream_t stream) {
-    const dim3 grid(max_tiles, njobs), block(256);
-    // Activations are staged in LDS when every job's limbs fit.
-    const uint32_t lds_bytes = lds_cols / 32u * slots * 128u;
-    const bool lds_a = lds_bytes <= kMaxLdsLimbBytes;
-    const uint32_t shm = lds_a ? lds_bytes : 0u;
-    switch (slots * 2 + (lds_a ? 1 : 0)) {
-        case 2: hipLaunchKernelGGL((k_qmv<FMT, 1, false>), grid, block, shm, stream, jobs, status); break;
-        case 3: hipLaunchKernelGGL((k_qmv<FMT, 1, true>), grid, block, shm, stream, jobs, status); break;
-        case 4: hipLaunchKernelGGL((k_qmv<FMT, 2, false>), grid, block, shm, stream, jobs, status); break;
-        case 5: hipLaunchKernelGGL((k_qmv<FMT, 2, true>), grid, block, shm, stream, jobs, status); break;
-        case 8: hipLaunchKernelGGL((k_qmv<FMT, 4, false>), grid, block, shm, stream, jobs, status); break;
-        case 9: hipLaunchKernelGGL((k_qmv<FMT, 4, true>), grid, block, shm, stream, jobs, status); break;
-        case 16: hipLaunchKernelGGL((k_qmv<FMT, 8, false>), grid, block, shm, stream, jobs, status); break;
-        case 17: hipLaunchKernelGGL((k_qmv<FMT, 8, true>), grid, block, shm, stream, jobs, status); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
-hipError_t launch_qmv(uint32_t type, uint32_t token_slots, const QmvBatch& jobs, uint32_t njobs,
-                      uint32_t max_tiles, uint32_t max_cols, uint32_t* status, hipStream_t stream) {
-    if (njobs == 0 || max_tiles == 0) return hipSuccess;
-    if (!jobs.device_jobs && njobs > kInlineJobs) return hipErrorInvalidValue;
-    switch (type) {
-        case VL_TYPE_IQ2_XXS: return launch_qmv_fmt<VL_TYPE_IQ2_XXS>(token_slots, jobs, njobs, max_tiles, max_cols, status, stream);
-        case VL_TYPE_IQ3_XXS: return launch_qmv_fmt<VL_TYPE_IQ3_XXS>(token_slots, jobs, njobs, max_tiles, max_cols, status, stream);
-        case VL_TYPE_IQ1_S: return launch_qmv_fmt<VL_TYPE_IQ1_S>(token_slots, jobs, njobs, max_tiles, max_cols, status, stream);
-        case VL_TYPE_Q8_0: return launch_qmv_fmt<VL_TYPE_Q8_0>(token_slots, jobs, njobs, max_tiles, max_cols, status, stream);
-        default: return hipErrorInvalidValue;
+static hipError_t launch_matvec_fmt(const vl_tiled_layout& L, const uint8_t* w, uint32_t tokens,
+                                    float* y, uint8_t* ws, const MatvecWs& m, uint32_t blocks,
+                                    hipStream_t st) {
+    switch (m.slots) {
+        case 1: return launch_matvec_nt<FMT, 1>(L, w, tokens, y, ws, m, blocks, st);
+        case 2: return launch_matvec_nt<FMT, 2>(L, w, tokens, y, ws, m, blocks, st);
+        case 4: return launch_matvec_nt<FMT, 4>(L, w, tokens, y, ws, m, blocks, st);
+        default: return launch_matvec_nt<FMT, 8>(L, w, tokens, y, ws, m, blocks, st);
     }
 }
 
-__global__ void k_fill_u32(uint32_t* dst, uint32_t count, uint32_t value) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < count) dst[i] = value;
-}
-
-hipError_t launch_fill_u32(uint32_t* dst, uint32_t count, uint32_t value, hipStream_t stream) {
-    if (count == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_fill_u32, dim3((count + 255) / 256), dim3(256), 0, stream, dst, count, value);
-    return hipGetLastError();
+hipError_t launch_matvec(const vl_tiled_layout& L, const uint8_t* w, const float* x,
+                         uint32_t tokens, float* y, uint8_t* workspace, uint32_t blocks,
+                         hipStream_t stream) {
+    if (tokens == 0 || tokens > 8 || L.cols % 32u != 0 || blocks == 0) return hipErrorInvalidValue;
+    const MatvecWs m = matvec_ws(L.rows, L.cols, tokens, blocks);
+    hipLaunchKernelGGL(k_prep_x, dim3(m.xblocks), dim3(256), 0, stream, x, L.cols, tokens,
+                       workspace, m);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (L.type) {
+        case VL_TYPE_IQ2_XXS: return launch_matvec_fmt<VL_TYPE_IQ2_XXS>(L, w, tokens, y, workspace, m, blocks, stream);
+        case VL_TYPE_IQ3_XXS: return launch_matvec_fmt<VL_TYPE_IQ3_XXS>(L, w, tokens, y, workspace, m, blocks, stream);
+        case VL_TYPE_IQ1_S: return launch_matvec_fmt<VL_TYPE_IQ1_S>(L, w, tokens, y, workspace, m, blocks, stream);
+        case VL_TYPE_Q8_0: return launch_matvec_fmt<VL_TYPE_Q8_0>(L, w, tokens, y, workspace, m, blocks, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace vl

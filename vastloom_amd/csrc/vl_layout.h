@@ -10,8 +10,8 @@
 // Planes, in order, for a matrix of R rows (Rp = R rounded up to 32, T = Rp/32 tiles), K
 // columns, NB = K/256 superblocks and NG = K/32 groups per row; j is the row within its tile:
 //
-//   IQ2_XXS  P: [T][NG/2][32 j][16 B]  two groups' 8-byte payloads (4 grid bytes, sign/scale word)
-//            S: [T][NB][32 j] u16      superblock scale d
+//   IQ2_XXS  P: [T][NB][2 h][32 j][32 B]  half h of row j's superblock (see below)
+//            S: [T][NB][32 j] u16           superblock scale d
 //   IQ3_XXS  Q: [T][NG/2][32 j][16 B]  two groups' 8 grid-index bytes
 //            A: [T][NG/4][32 j][16 B]  four groups' sign/scale words
 //            S: [T][NB][32 j] u16
@@ -20,6 +20,15 @@
 //            S: [T][NB][32 j] u16
 //   Q8_0     Q: [T][NG][32 j][32 B]    the block's 32 int8 quants
 //            S: [T][NG][32 j] u16      block scale d
+//
+// IQ2_XXS half h of a superblock row holds what the MFMA lane that takes K half h of every
+// group needs: sub-blocks 2h and 2h+1 of each of the 8 groups, as eight 32-bit words
+//   w[q]     q = 0..3: grid bytes of groups 2q and 2q+1: g(2q,2h), g(2q,2h+1), g(2q+1,2h),
+//            g(2q+1,2h+1) in bytes 0..3
+//   w[4+q]   q = 0..3: the 7-bit sign fields of the same four sub-blocks at bits 0, 7, 14 and
+//            21, and at bits 28..31 the 4-bit scale of group 4h+q
+// so that each of the 32 lanes of a half-wave loads its own 32 contiguous bytes, and the two
+// halves of a row exchange their four scales once per superblock.
 #ifndef VL_LAYOUT_H
 #define VL_LAYOUT_H
 
@@ -80,7 +89,7 @@ static inline VL_HD int vl_make_layout(uint32_t type, uint32_t rows, uint32_t co
     switch (type) {
         case VL_TYPE_IQ2_XXS:
             L.plane0 = 0;
-            L.plane1 = rp * L.groups * 8u;
+            L.plane1 = rp * L.superblocks * 64u;
             L.plane2 = L.plane1;
             L.bytes = L.plane1 + rp * L.superblocks * 2u;
             break;

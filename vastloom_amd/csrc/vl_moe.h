@@ -60,28 +60,31 @@ struct MoeInputs {
     float* out;                // [tokens][width]
 };
 
-// Device workspace of one layer call, carved by moe_workspace_layout.
+// Device workspace of one layer call, carved by moe_workspace_layout. The first word is the
+// status word. Sizes depend on the persistent grid (waves) of the device the call runs on.
 struct MoeWorkspace {
     uint8_t* base;
     uint64_t bytes;
-    uint64_t off_header, off_logits, off_route_idx, off_route_w, off_active, off_combine,
-        off_hmax, off_hexp, off_xexp, off_xlimbs, off_h, off_hlimbs, off_ypart;
-    uint32_t max_active;
+    uint64_t off_header, off_logits, off_scores, off_keys, off_route_idx, off_route_w, off_active, off_combine,
+        off_xexp, off_xflags, off_xlimbs, off_counters, off_rec_gu, off_rec_dn, off_h,
+        off_hslab, off_ypart;
+    uint32_t max_active, slots, waves, blocks;
+    uint32_t tiles_gu, tiles_dn, hblocks, xblocks;  // gate/up and down tiles, h and x exponent blocks
+    uint32_t counters;                                // u32 words at off_counters
+    uint32_t stage;                                   // experts one down block converts h for
 };
 
 bool moe_shape_ok(const MoeShape& s);
-uint64_t moe_workspace_bytes(const MoeShape& s);
-MoeWorkspace moe_workspace_layout(const MoeShape& s, void* base);
+// blocks: persistent blocks of the matvec kernels (one per CU).
+uint64_t moe_workspace_bytes(const MoeShape& s, uint32_t blocks);
+MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base);
 
 // Stages of one layer call, in launch order; a profiled call records an event before each
 // stage and one after the last.
-enum MoeStage : uint32_t {
-    kStageRouter = 0, kStageRoute, kStagePrep, kStageGateUp, kStageHPrep, kStageDown,
-    kStageCombine, kStageCount
-};
+enum MoeStage : uint32_t { kStageRouter = 0, kStageGateUp, kStageDown, kStageCount };
 
-// Issues the whole layer on the stream. The workspace's first word is the status word. When
-// events is non-null it holds kStageCount + 1 events recorded around the stages.
+// Issues the whole layer on the stream. When events is non-null it holds kStageCount + 1
+// events recorded around the stages.
 hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& ws,
                       hipStream_t stream, hipEvent_t* events = nullptr);
 

@@ -1,16 +1,18 @@
-// MoE layer on the device, for up to 8 tokens routed to top-k of E experts plus a shared expert:
+// MoE layer on the device, for up to 8 tokens routed to top-k of E experts plus a shared expert,
+// in three launches:
 //
-//   k_moe_router   gate logits, float64 accumulation per expert row (the reference's linear_f /
-//                  gate_logits numerics), and the per-call status/maximum words zeroed
-//   k_moe_route    per-token scores and top-k (one wave per token), then the active-expert list:
-//                  distinct experts in ascending id with their tokens, and each token's combine
-//                  order
-//   k_prep_limbs   the tokens' int8 limbs (vl_kernels.hip)
-//   k_moe_gateup   per (active expert, 32-row tile): gate and up tiles in one block (4 waves each,
-//                  int8 MFMA), then the SwiGLU of the semantics into h; |h| maxima per token
-//   k_moe_hprep    h -> limbs with one exponent per (expert, token)
-//   k_moe_down     per (active expert, 32-row tile) down projection into per-expert partials
-//   k_moe_combine  partials -> layer output in the reference's combine order
+//   k_moe_router   gate logits (float64 accumulation per expert row, the reference's linear_f /
+//                  gate_logits numerics); the tokens' int8 limbs with one exponent per 256
+//                  columns; the per-call status word and handoff counters zeroed
+//   k_moe_gateup   persistent: every block first routes (per-token scores and top-k, then the
+//                  active-expert list: distinct experts in ascending id with their tokens, and
+//                  each token's combine order; block 0 publishes it), then its waves stream the
+//                  gate and up tiles of all active experts (vl_stream.h). The last wave of a tile
+//                  adds its partials, applies the SwiGLU of the semantics and stores h; the last
+//                  tile of each 256-row block of h turns it into limbs for the down projection
+//   k_moe_down     persistent: the waves stream the down tiles of all active experts; the last
+//                  wave of a tile stores the expert's rows, and the last expert of a tile combines
+//                  the layer output rows in the reference's combine order
 //
 // The routing, clamp, route-weight placement and combine order follow the reference code named
 // in vl_moe.h. Every reduction has a fixed order, so results are deterministic.
@@ -19,7 +21,7 @@
 
 #include "vl_kernels.h"
 #include "vl_moe.h"
-#include "vl_qmv_core.h"
+#include "vl_stream.h"
 
 namespace vl {
 
@@ -43,6 +45,8 @@ struct CombineEntry {
     float w;
 };
 
+constexpr uint32_t kMaxActive = kMoeMaxTokens * kMoeMaxTopK + 1;
+
 static inline uint64_t align256(uint64_t v) { return (v + 255u) & ~uint64_t(255); }
 
 bool moe_shape_ok(const MoeShape& s) {
@@ -51,7 +55,6 @@ bool moe_shape_ok(const MoeShape& s) {
         s.experts == 0 || s.experts > 1024 || s.top_k > s.experts)
         return false;
     if (!vl_block_shape(s.gate_type, &be, &bb) || s.width % be || s.width % 256u) return false;
-    if (s.width > 8192u) return false;  // the routing block stages one token row in registers
     if (!vl_block_shape(s.down_type, &be, &bb) || s.inter % be || s.inter % 32u) return false;
     if (s.semantics > kSemPlain || s.routing > kRouteGiven || s.score_fn > kScoreSigmoid) return false;
     return true;
@@ -62,38 +65,104 @@ static uint32_t max_active(const MoeShape& s) {
     return routed + (s.has_shared ? 1u : 0u);
 }
 
-MoeWorkspace moe_workspace_layout(const MoeShape& s, void* base) {
+// Bytes of one expert's h limbs, [inter/32][slots][4][32].
+__host__ __device__ inline uint32_t down_expert_bytes(uint32_t inter, uint32_t slots) {
+    return (inter / 32u) * slots * 128u;
+}
+
+MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base) {
     MoeWorkspace w{};
     w.base = static_cast<uint8_t*>(base);
     w.max_active = max_active(s);
-    const uint64_t A = w.max_active, T = s.tokens, K = s.top_k;
+    w.slots = limb_slots(s.tokens);
+    w.blocks = blocks;
+    w.waves = blocks * kStreamWaves;
+    w.tiles_gu = (s.inter + 31u) / 32u;
+    w.tiles_dn = (s.width + 31u) / 32u;
+    w.hblocks = exp_blocks(s.inter);
+    w.xblocks = exp_blocks(s.width);
+    const uint64_t A = w.max_active, T = s.tokens, K = s.top_k, NT = w.slots;
+    // Most experts the units of one down block can touch, for any number of active experts.
+    const uint64_t UJ = units_per_row(s.down_type, s.inter);
+    const uint64_t per_block = blocks ? (A * w.tiles_dn * UJ + blocks - 1u) / blocks : 1u;
+    const uint64_t stage = (per_block > 0 ? per_block - 1u : 0u) / (w.tiles_dn * UJ) + 2u;
+    w.stage = (uint32_t)(stage < A ? stage : A);
+    w.counters = (uint32_t)(A * w.tiles_gu + A * w.tiles_dn + w.tiles_dn + A * w.hblocks * 8u);
     uint64_t o = 0;
     w.off_header = o; o = align256(o + sizeof(MoeHeader));
     w.off_logits = o; o = align256(o + T * s.experts * 4u);
+    w.off_scores = o; o = align256(o + T * s.experts * 4u);
+    w.off_keys = o; o = align256(o + T * s.experts * 4u);
     w.off_route_idx = o; o = align256(o + T * K * 4u);
     w.off_route_w = o; o = align256(o + T * K * 4u);
     w.off_active = o; o = align256(o + A * sizeof(ActiveExpert));
     w.off_combine = o; o = align256(o + T * (K + 1) * sizeof(CombineEntry));
-    w.off_hmax = o; o = align256(o + A * kMoeMaxTokens * 4u);
-    w.off_hexp = o; o = align256(o + A * kMoeMaxTokens * 4u);
-    w.off_xexp = o; o = align256(o + kMoeMaxTokens * 4u);
-    w.off_xlimbs = o; o = align256(o + limb_bytes(s.width, s.tokens));
-    w.off_h = o; o = align256(o + A * kMoeMaxTokens * s.inter * 4u);
-    w.off_hlimbs = o; o = align256(o + A * (s.inter / 32u) * kMoeMaxTokens * 128u);
-    w.off_ypart = o; o = align256(o + A * kMoeMaxTokens * (uint64_t)s.width * 4u);
+    w.off_xexp = o; o = align256(o + (uint64_t)w.xblocks * 8u * 4u);
+    w.off_xflags = o; o = align256(o + (uint64_t)w.xblocks * 8u * 4u);
+    w.off_xlimbs = o; o = align256(o + (uint64_t)(s.width / 32u) * NT * 128u);
+    w.off_counters = o; o = align256(o + (uint64_t)w.counters * 4u);
+    w.off_rec_gu = o; o = align256(o + (w.waves + A * w.tiles_gu) * 2u * NT * 64u * 4u);
+    w.off_rec_dn = o; o = align256(o + (w.waves + A * w.tiles_dn) * NT * 64u * 4u);
+    w.off_h = o; o = align256(o + A * NT * s.inter * 4u);
+    w.off_hslab = o; o = align256(o + (uint64_t)blocks * w.stage * down_expert_bytes(s.inter, w.slots));
+    w.off_ypart = o; o = align256(o + A * NT * (uint64_t)s.width * 4u);
     w.bytes = o;
     return w;
 }
 
-uint64_t moe_workspace_bytes(const MoeShape& s) { return moe_workspace_layout(s, nullptr).bytes; }
+uint64_t moe_workspace_bytes(const MoeShape& s, uint32_t blocks) {
+    return moe_workspace_layout(s, blocks, nullptr).bytes;
+}
 
 template <typename T>
 __device__ __forceinline__ T* ws_ptr(const MoeWorkspace& w, uint64_t off) {
     return reinterpret_cast<T*>(w.base + off);
 }
 
+// Counter regions (u32 words at off_counters).
+struct MoeCounters {
+    uint32_t* gu;    // [A][tiles_gu]   gate/up tile handoff
+    uint32_t* dn;    // [A][tiles_dn]   down tile handoff
+    uint32_t* tile;  // [tiles_dn]      experts done per output tile
+    uint32_t* hmax;  // [A][hblocks][8] max |h| bits per 256-row block of h and slot
+};
+
+__device__ __forceinline__ MoeCounters counters_of(const MoeWorkspace& w) {
+    MoeCounters c;
+    uint32_t* p = ws_ptr<uint32_t>(w, w.off_counters);
+    const uint32_t A = w.max_active;
+    c.gu = p;
+    c.dn = c.gu + A * w.tiles_gu;
+    c.tile = c.dn + A * w.tiles_dn;
+    c.hmax = c.tile + w.tiles_dn;
+    return c;
+}
+
 // ------------------------------------------------------------------------------------------
-// Router logits: one wave per expert row, float64 products and sums, one rounding.
+// Scores and selection keys.
+// ------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ float score_of(float logit, uint32_t fn) {
+    const double p = (double)logit;
+    if (fn == kScoreSigmoid) {
+        if (p >= 0.0) return (float)(1.0 / (1.0 + exp(-p)));
+        const double q = exp(p);
+        return (float)(q / (1.0 + q));
+    }
+    const double sp = (p > 0.0 ? p : 0.0) + log1p(exp(-fabs(p)));
+    return (float)sqrt(sp);
+}
+
+// Order-preserving map of a float to uint32: a larger float gives a larger key, and every key of
+// a finite float is above 1 (non-finite keys are 1; such a token is refused anyway).
+__device__ __forceinline__ uint32_t float_key(float f) {
+    if (!isfinite(f)) return 1u;
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// ------------------------------------------------------------------------------------------
+// Router logits and activation limbs.
 // ------------------------------------------------------------------------------------------
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
@@ -101,22 +170,25 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
-// One block per expert row; the four waves take interleaved quarters of the row (every lane
-// keeps its float4 loads in flight), then the partial sums are added in wave order.
+// Block b: expert row b's logits (four waves take interleaved quarters of the row with every
+// lane's float4 loads in flight; partial sums added in wave order), then the limbs of column
+// block b of every token. Block 0 also zeroes the status word and the handoff counters.
 __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeInputs in,
                                                     const MoeWorkspace w) {
     __shared__ double red[kMoeMaxTokens][4];
-    // Per-call words later kernels accumulate into.
-    if (blockIdx.x == 0) {
+    const uint32_t b = blockIdx.x;
+    if (b == 0) {
         MoeHeader* h = ws_ptr<MoeHeader>(w, w.off_header);
         if (threadIdx.x < 2) (&h->status)[threadIdx.x] = 0;
-        uint32_t* hmax = ws_ptr<uint32_t>(w, w.off_hmax);
-        for (uint32_t i = threadIdx.x; i < w.max_active * kMoeMaxTokens; i += blockDim.x) hmax[i] = 0;
+        uint32_t* cnt = ws_ptr<uint32_t>(w, w.off_counters);
+        for (uint32_t i = threadIdx.x; i < w.counters; i += blockDim.x) cnt[i] = 0;
     }
-    if (s.routing == kRouteGiven) return;
-    const uint32_t e = blockIdx.x;
+    if (b < w.xblocks)
+        prep_x_block(in.x, s.width, s.width, s.tokens, w.slots, b, ws_ptr<int8_t>(w, w.off_xlimbs),
+                     ws_ptr<int>(w, w.off_xexp), ws_ptr<uint32_t>(w, w.off_xflags));
+    if (s.routing == kRouteGiven || b >= s.experts) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const float4* row = reinterpret_cast<const float4*>(in.router + (uint64_t)e * s.width);
+    const float4* row = reinterpret_cast<const float4*>(in.router + (uint64_t)b * s.width);
     const uint32_t n4 = s.width / 4u;
     float4 wv[8];
     int nv = 0;
@@ -131,329 +203,283 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if (j < nv) {
-                const float4 a = wv[j], b = xr[threadIdx.x + 256u * j];
-                acc += (double)a.x * (double)b.x;
-                acc += (double)a.y * (double)b.y;
-                acc += (double)a.z * (double)b.z;
-                acc += (double)a.w * (double)b.w;
+                const float4 a = wv[j], c = xr[threadIdx.x + 256u * j];
+                acc += (double)a.x * (double)c.x;
+                acc += (double)a.y * (double)c.y;
+                acc += (double)a.z * (double)c.z;
+                acc += (double)a.w * (double)c.w;
             }
         }
         // Rows wider than 8192 continue with plain loads.
         for (uint32_t i = threadIdx.x + 2048u; i < n4; i += 256u) {
-            const float4 a = row[i], b = xr[i];
-            acc += (double)a.x * (double)b.x;
-            acc += (double)a.y * (double)b.y;
-            acc += (double)a.z * (double)b.z;
-            acc += (double)a.w * (double)b.w;
+            const float4 a = row[i], c = xr[i];
+            acc += (double)a.x * (double)c.x;
+            acc += (double)a.y * (double)c.y;
+            acc += (double)a.z * (double)c.z;
+            acc += (double)a.w * (double)c.w;
         }
         acc = wave_sum_f64(acc);
         if (lane == 0) red[t][wave] = acc;
     }
     __syncthreads();
     if (threadIdx.x < s.tokens) {
+        // Logit, score and selection key: learned routing ranks score + bias (the reference's
+        // float keys), softmax routing ranks probabilities, which order as the logits do.
         const uint32_t t = threadIdx.x;
-        ws_ptr<float>(w, w.off_logits)[t * s.experts + e] =
-            (float)(((red[t][0] + red[t][1]) + red[t][2]) + red[t][3]);
-    }
-}
-
-// ------------------------------------------------------------------------------------------
-// Routing.
-// ------------------------------------------------------------------------------------------
-
-__device__ __forceinline__ float score_of(float logit, uint32_t fn) {
-    const double p = (double)logit;
-    if (fn == kScoreSigmoid) {
-        if (p >= 0.0) return (float)(1.0 / (1.0 + exp(-p)));
-        const double q = exp(p);
-        return (float)(q / (1.0 + q));
-    }
-    const double sp = (p > 0.0 ? p : 0.0) + log1p(exp(-fabs(p)));
-    return (float)sqrt(sp);
-}
-
-// Key order for selection: larger key first, ties to the lower id.
-__device__ __forceinline__ bool beats(float ka, uint32_t ia, float kb, uint32_t ib) {
-    return ka > kb || (ka == kb && ia < ib);
-}
-
-__device__ __forceinline__ bool beats_d(double ka, uint32_t ia, double kb, uint32_t ib) {
-    return ka > kb || (ka == kb && ia < ib);
-}
-
-// Limbs of one token's activations by the whole block: max |x| (all loads issued at once,
-// kept in registers), exponent, then the four digits of round(x * 2^e) for every column, the
-// same encoding as k_prep_limbs. cols <= 4 * 4 * blockDim.x.
-__device__ void prep_token_block(const float* __restrict__ x, uint32_t cols, uint32_t slots,
-                                 uint32_t tok, int8_t* __restrict__ xl, int* __restrict__ xe,
-                                 uint32_t* status, float* red) {
-    constexpr int kPer = 4;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    const uint32_t n4 = cols / 4u;
-    float4 v[kPer];
-    float m = 0.0f;
-    bool finite = true;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const uint32_t i = threadIdx.x + blockDim.x * j;
-        v[j] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        finite &= isfinite(v[j].x) && isfinite(v[j].y) && isfinite(v[j].z) && isfinite(v[j].w);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
-    }
-    if (!finite) {
-        atomicOr(status, kStatusNonFiniteInput);
-        m = 0.0f;
-    }
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    m = 0.0f;
-    for (int i = 0; i < nwaves; ++i) m = fmaxf(m, red[i]);
-    __syncthreads();
-    int q = 0;
-    frexpf(m, &q);
-    const int e = m > 0.0f && isfinite(m) ? 30 - q : 0;
-    if (threadIdx.x == 0) xe[tok] = e;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const uint32_t i = threadIdx.x + blockDim.x * j;
-        if (i >= n4) continue;
-        const float vs[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-        uint32_t packed[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            int X = isfinite(vs[k]) ? (int)rintf(ldexpf(vs[k], e)) : 0;
-#pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                const int digit = l < 3 ? (int)(int8_t)(X & 0xff) : X;
-                packed[l] |= ((uint32_t)digit & 0xffu) << (8 * k);
-                X = (X - digit) >> 8;
-            }
+        const uint64_t i = (uint64_t)t * s.experts + b;
+        const float logit = (float)(((red[t][0] + red[t][1]) + red[t][2]) + red[t][3]);
+        float score = 0.0f;
+        uint32_t key;
+        if (s.routing == kRouteSoftmax) {
+            key = float_key(logit);
+        } else {
+            score = score_of(logit, s.score_fn);
+            key = float_key(score + ((s.routing == kRouteLearned && in.bias) ? *gp(in.bias + b) : 0.0f));
         }
-        const uint32_t k4 = 4u * i;
-        const uint64_t base = ((uint64_t)(k4 / 32u) * slots + tok) * 128u + (k4 % 32u);
-#pragma unroll
-        for (int l = 0; l < 4; ++l) *reinterpret_cast<uint32_t*>(xl + base + 32u * l) = packed[l];
+        *gp(ws_ptr<float>(w, w.off_logits) + i) = logit;
+        *gp(ws_ptr<float>(w, w.off_scores) + i) = score;
+        *gp(ws_ptr<uint32_t>(w, w.off_keys) + i) = key;
     }
 }
 
-// Top-k of one token by one wave. Lane l holds experts l, l + 64, ... (PER of them, in
-// registers). Learned routing ranks score + bias with the reference's float keys; softmax
-// ranks float64 probabilities. Returns true when the token cannot be routed (non-finite logits
-// or a non-positive weight sum).
+// ------------------------------------------------------------------------------------------
+// Routing (run by every gate/up block; block 0 publishes the result).
+// ------------------------------------------------------------------------------------------
+
+// Maximum over the wave, by DPP row operations (all lanes active); the result is uniform.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xb1, 0xf, 0xf, false));   // quad [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4e, 0xf, 0xf, false));   // quad [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xf, 0xf, false));  // row half mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xf, 0xf, false));  // row mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xa, 0xf, false));  // row bcast 15
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xc, 0xf, false));  // row bcast 31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Per-token selection scratch in LDS.
+struct TopKLds {
+    uint32_t id[kMoeMaxTopK];
+    float val[kMoeMaxTopK];
+    double p[kMoeMaxTopK];
+};
+
+// Top-k of one token by one wave (all lanes active). Lane l holds experts l, l + 64, ... (PER of
+// them) with the selection keys of the router kernel. Round k takes the largest remaining key,
+// ties to the lowest id (a DPP wave maximum, then the first ballot lane), so the experts come
+// out in the reference's rank order; lanes k < K then form the weights with the reference's
+// float64 arithmetic, summing in rank order. Returns true when the token cannot be routed
+// (non-finite logits or a non-positive weight sum).
 template <int PER>
-__device__ bool route_token(const float* lg, const float* bias, uint32_t E, uint32_t K,
-                            bool softmax, const MoeShape& s, uint32_t* out_idx, float* out_w) {
-    const int lane = threadIdx.x & 63;
-    double key[PER];
-    float sc[PER];
-    bool taken[PER];
+__device__ bool route_topk(const float* lg, const float* scr, const uint32_t* keys, uint32_t E,
+                           uint32_t K, bool softmax, const MoeShape& s, TopKLds& tk,
+                           uint32_t* out_idx, float* out_w) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t key[PER];
+    float lv[PER], sv[PER];
     bool bad = false;
-    double mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const uint32_t e = lane + 64u * i;
-        taken[i] = e >= E;
-        sc[i] = 0.0f;
-        key[i] = -INFINITY;
+        key[i] = 0;
+        lv[i] = sv[i] = 0.0f;
         if (e < E) {
-            const float l = lg[e];
-            bad |= !isfinite(l);
-            if (!softmax) {
-                sc[i] = score_of(l, s.score_fn);
-                key[i] = (double)(sc[i] + (bias ? bias[e] : 0.0f));
-            } else {
-                mx = fmax(mx, (double)l);
-            }
+            key[i] = *gp(keys + e);
+            lv[i] = *gp(lg + e);
+            sv[i] = *gp(scr + e);
+            bad |= !isfinite(lv[i]);
         }
     }
-    if (softmax) {
-        for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
-        double sum = 0.0;
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (lane + 64u * i < E) {
-                key[i] = exp((double)lg[lane + 64u * i] - mx);
-                sum += key[i];
-            }
-        sum = wave_sum_f64(sum);
-        const double inv = sum > 0.0 ? 1.0 / sum : 0.0;
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (lane + 64u * i < E) key[i] = key[i] * inv;
-    }
-    double sel_sum = 0.0;
     for (uint32_t k = 0; k < K; ++k) {
-        double bk = -INFINITY;
-        uint32_t bi = 0xffffffffu;
-        float bs = 0.0f;
+        uint32_t best = 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) best = max(best, key[i]);
+        const uint32_t m = wave_max_u32(best);
+        uint32_t id = 0xffffffffu;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const uint32_t e = lane + 64u * i;
-            if (!taken[i] && (bi == 0xffffffffu || beats_d(key[i], e, bk, bi))) {
-                bk = key[i];
-                bi = e;
-                bs = sc[i];
-            }
+            const uint64_t hit = __ballot(key[i] == m && m != 0);
+            if (id == 0xffffffffu && hit) id = 64u * i + (uint32_t)__builtin_ctzll(hit);
         }
-        for (int o = 32; o > 0; o >>= 1) {
-            const double ok = __shfl_xor(bk, o);
-            const uint32_t oi = __shfl_xor(bi, o);
-            const float os = __shfl_xor(bs, o);
-            if (oi != 0xffffffffu && (bi == 0xffffffffu || beats_d(ok, oi, bk, bi))) {
-                bk = ok;
-                bi = oi;
-                bs = os;
-            }
+        if (id == 0xffffffffu) {
+            bad = true;
+            id = 0;
         }
+        const uint32_t wl = id & 63u, wi = id >> 6;
+        float l = lv[0], sc = sv[0];
+#pragma unroll
+        for (int i = 1; i < PER; ++i)
+            if (wi == (uint32_t)i) {
+                l = lv[i];
+                sc = sv[i];
+            }
 #pragma unroll
         for (int i = 0; i < PER; ++i)
-            if (lane + 64u * i == bi) taken[i] = true;
-        if (bi >= E) bad = true;
-        const double v = softmax ? bk : (double)bs;
+            if (wi == (uint32_t)i && lane == wl) key[i] = 0;
+        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax ? l : sc), wl));
         if (lane == 0) {
-            out_idx[k] = bi < E ? bi : 0u;
-            out_w[k] = softmax ? (float)bk : bs;
+            tk.id[k] = id;
+            tk.val[k] = v;
         }
-        sel_sum += v;
     }
-    if (lane == 0) {
+    double sum_all = 0.0, mx = 0.0;
+    if (softmax) {
+        // The largest key is the largest logit: the first selected expert's.
+        mx = (double)__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(tk.val[0])));
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (lane + 64u * i < E) sum_all += exp((double)lv[i] - mx);
+        sum_all = wave_sum_f64(sum_all);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    double pk = 0.0;
+    float vk = 0.0f;
+    if (lane < K) {
+        vk = tk.val[lane];
+        pk = softmax ? exp((double)vk - mx) * (sum_all > 0.0 ? 1.0 / sum_all : 0.0) : (double)vk;
+        tk.p[lane] = pk;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane < K) {
+        double sel_sum = 0.0;
+        for (uint32_t q = 0; q < K; ++q) sel_sum += tk.p[q];
+        float wk;
         if (!softmax) {
             bad |= !(sel_sum > 0.0) || isinf(sel_sum);
-            for (uint32_t k = 0; k < K; ++k)
-                out_w[k] = (float)((double)out_w[k] / sel_sum * (double)s.route_scale);
-        } else if (s.renormalize && sel_sum > 0.0) {
-            const double scale = 1.0 / sel_sum;
-            for (uint32_t k = 0; k < K; ++k) out_w[k] = (float)((double)out_w[k] * scale);
+            wk = (float)((double)vk / sel_sum * (double)s.route_scale);
+        } else {
+            wk = (float)pk;
+            if (s.renormalize && sel_sum > 0.0) wk = (float)((double)wk * (1.0 / sel_sum));
         }
+        out_idx[lane] = tk.id[lane];
+        out_w[lane] = wk;
     }
     return __any(bad);
 }
 
-__global__ void __launch_bounds__(512) k_moe_route(const MoeShape s, const MoeInputs in,
-                                                   const MoeWorkspace w) {
-    __shared__ uint32_t s_idx[kMoeMaxTokens * kMoeMaxTopK];
-    __shared__ float s_w[kMoeMaxTokens * kMoeMaxTopK];
-    __shared__ uint32_t s_bad;
-    MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
-    const float* logits = ws_ptr<float>(w, w.off_logits);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+struct RouteLds {
+    TopKLds topk[kMoeMaxTokens];
+    uint32_t idx[kMoeMaxTokens * kMoeMaxTopK];
+    float wt[kMoeMaxTokens * kMoeMaxTopK];
+    uint32_t first[kMoeMaxTokens * kMoeMaxTopK];
+    uint32_t bad[kMoeMaxTokens];
+    uint32_t n_active;
+    ActiveExpert act[kMaxActive];
+};
+
+
+// Routing of token t by one wave: ids and weights into rt.idx/wt, refusal into rt.bad[t].
+__device__ __forceinline__ void route_token_wave(const MoeShape& s, const MoeInputs& in,
+                                                 const MoeWorkspace& w, uint32_t t, RouteLds& rt) {
+    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t K = s.top_k, E = s.experts;
-    if (threadIdx.x == 0) s_bad = 0;
-    __syncthreads();
-
-    // Phase A: one wave per token.
-    if (wave < (int)s.tokens) {
-        const uint32_t t = wave;
-        const float* lg = logits + (uint64_t)t * E;
-        if (s.routing == kRouteGiven || s.routing == kRouteTable) {
-            for (uint32_t k = lane; k < K; k += 64) {
-                uint32_t id = 0;
-                if (s.routing == kRouteGiven) id = in.given_ids ? in.given_ids[t * K + k] : 0u;
-                else id = in.table_ids[t * K + k];
-                if (id >= E) { atomicOr(&s_bad, 1u); id = 0; }
-                s_idx[t * K + k] = id;
-            }
-            __builtin_amdgcn_wave_barrier();
-            // Duplicate experts within one token are refused.
-            for (uint32_t k = lane; k < K; k += 64)
-                for (uint32_t j = 0; j < k; ++j)
-                    if (s_idx[t * K + j] == s_idx[t * K + k]) atomicOr(&s_bad, 1u);
-            if (s.routing == kRouteGiven) {
-                for (uint32_t k = lane; k < K; k += 64)
-                    s_w[t * K + k] = in.given_weights ? in.given_weights[t * K + k] : 1.0f;
-            } else if (lane == 0) {
-                double sum = 0.0;
-                float sc[kMoeMaxTopK];
-                for (uint32_t k = 0; k < K; ++k) {
-                    sc[k] = score_of(lg[s_idx[t * K + k]], s.score_fn);
-                    sum += (double)sc[k];
-                }
-                if (!(sum > 0.0) || isinf(sum)) atomicOr(&s_bad, 1u);
-                for (uint32_t k = 0; k < K; ++k)
-                    s_w[t * K + k] = (float)((double)sc[k] / sum * (double)s.route_scale);
-            }
-        } else {
-            const float* bias = s.routing == kRouteLearned ? in.bias : nullptr;
-            const bool softmax = s.routing == kRouteSoftmax;
-            float* sw = s_w + t * K;
-            uint32_t* si = s_idx + t * K;
-            bool bad = false;
-            if (E <= 64) bad = route_token<1>(lg, bias, E, K, softmax, s, si, sw);
-            else if (E <= 128) bad = route_token<2>(lg, bias, E, K, softmax, s, si, sw);
-            else if (E <= 256) bad = route_token<4>(lg, bias, E, K, softmax, s, si, sw);
-            else if (E <= 512) bad = route_token<8>(lg, bias, E, K, softmax, s, si, sw);
-            else bad = route_token<16>(lg, bias, E, K, softmax, s, si, sw);
-            if (bad && lane == 0) atomicOr(&s_bad, 1u);
+    const uint64_t base = (uint64_t)t * E;
+    bool bad = false;
+    if (s.routing == kRouteGiven || s.routing == kRouteTable) {
+        for (uint32_t k = lane; k < K; k += 64) {
+            uint32_t id = 0;
+            if (s.routing == kRouteGiven) id = in.given_ids ? *gp(in.given_ids + t * K + k) : 0u;
+            else id = *gp(in.table_ids + t * K + k);
+            if (id >= E) { bad = true; id = 0; }
+            rt.idx[t * K + k] = id;
         }
+        __builtin_amdgcn_wave_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        // Duplicate experts within one token are refused.
+        for (uint32_t k = lane; k < K; k += 64)
+            for (uint32_t j = 0; j < k; ++j)
+                if (rt.idx[t * K + j] == rt.idx[t * K + k]) bad = true;
+        if (s.routing == kRouteGiven) {
+            for (uint32_t k = lane; k < K; k += 64)
+                rt.wt[t * K + k] = in.given_weights ? *gp(in.given_weights + t * K + k) : 1.0f;
+        } else if (lane == 0) {
+            const float* lg = ws_ptr<const float>(w, w.off_logits) + base;
+            const float* scr = ws_ptr<const float>(w, w.off_scores) + base;
+            double sum = 0.0;
+            float sc[kMoeMaxTopK];
+            for (uint32_t k = 0; k < K; ++k) {
+                const uint32_t e = rt.idx[t * K + k];
+                bad |= !isfinite(*gp(lg + e));
+                sc[k] = *gp(scr + e);
+                sum += (double)sc[k];
+            }
+            if (!(sum > 0.0) || isinf(sum)) bad = true;
+            for (uint32_t k = 0; k < K; ++k)
+                rt.wt[t * K + k] = (float)((double)sc[k] / sum * (double)s.route_scale);
+        }
+    } else {
+        const float* lg = ws_ptr<const float>(w, w.off_logits) + base;
+        const float* scr = ws_ptr<const float>(w, w.off_scores) + base;
+        const uint32_t* keys = ws_ptr<const uint32_t>(w, w.off_keys) + base;
+        const bool softmax = s.routing == kRouteSoftmax;
+        TopKLds& tk = rt.topk[t];
+        uint32_t* si = rt.idx + t * K;
+        float* sw = rt.wt + t * K;
+        if (E <= 64) bad = route_topk<1>(lg, scr, keys, E, K, softmax, s, tk, si, sw);
+        else if (E <= 128) bad = route_topk<2>(lg, scr, keys, E, K, softmax, s, tk, si, sw);
+        else if (E <= 256) bad = route_topk<4>(lg, scr, keys, E, K, softmax, s, tk, si, sw);
+        else if (E <= 512) bad = route_topk<8>(lg, scr, keys, E, K, softmax, s, tk, si, sw);
+        else bad = route_topk<16>(lg, scr, keys, E, K, softmax, s, tk, si, sw);
     }
-    __syncthreads();
+    bad = __any(bad);
+    if (lane == 0) rt.bad[t] = bad ? 1u : 0u;
+}
 
-    // Phase B: the active-expert list. Distinct experts are numbered in ascending id by a
-    // prefix count over per-expert "used" flags; each (token, slot) pair then finds its expert's
-    // active index, its slot among that expert's tokens (ascending token), and its place in the
-    // token's combine order.
-    const uint32_t P = s.tokens * K;
-    ActiveExpert* act = ws_ptr<ActiveExpert>(w, w.off_active);
-    CombineEntry* comb = ws_ptr<CombineEntry>(w, w.off_combine);
-    uint32_t* ridx = ws_ptr<uint32_t>(w, w.off_route_idx);
-    float* rw = ws_ptr<float>(w, w.off_route_w);
-    __shared__ uint32_t s_used[1024];
-    __shared__ uint32_t s_wave_count[8];
-    for (uint32_t e = threadIdx.x; e < 1024; e += blockDim.x) s_used[e] = 0;
-    __syncthreads();
-    if (threadIdx.x < P) s_used[s_idx[threadIdx.x]] = 1;
-    __syncthreads();
-    // Exclusive prefix over 1024 flags: wave v owns experts [128v, 128v + 128).
-    const uint32_t e0 = 128u * wave + lane, e1 = e0 + 64u;
-    const uint64_t m0 = __ballot(s_used[e0] != 0), m1 = __ballot(s_used[e1] != 0);
-    const uint64_t below = (1ull << lane) - 1ull;
-    if (lane == 0) s_wave_count[wave] = (uint32_t)(__popcll(m0) + __popcll(m1));
-    __syncthreads();
-    uint32_t base = 0, n_routed = 0;
-    for (int v = 0; v < 8; ++v) {
-        if (v < wave) base += s_wave_count[v];
-        n_routed += s_wave_count[v];
-    }
-    const uint32_t pre0 = base + (uint32_t)__popcll(m0 & below);
-    const uint32_t pre1 = base + (uint32_t)__popcll(m0) + (uint32_t)__popcll(m1 & below);
-    __syncthreads();
-    s_used[e0] = pre0;
-    s_used[e1] = pre1;
-    __syncthreads();
+// After route_token_wave for every token (and a barrier), the whole block builds the active-expert
+// list: distinct experts in ascending id, each with its tokens in ascending order, and every
+// token's combine order. publish also writes them (and the routes) to the workspace.
+__device__ __forceinline__ void build_active(const MoeShape& s, const MoeWorkspace& w, bool publish,
+                                            RouteLds& rt) {
+    const uint32_t K = s.top_k, E = s.experts, P = s.tokens * K;
     const uint32_t p = threadIdx.x;
     if (p < P) {
-        const uint32_t e = s_idx[p], t = p / K, k = p % K;
-        const float wt = s_w[p];
-        ridx[p] = e;
-        rw[p] = wt;
-        const uint32_t a = s_used[e];
-        uint32_t slot = 0, ntok = 0, pos = 0;
+        uint32_t first = 1;
+        for (uint32_t q = 0; q < p; ++q) first &= rt.idx[q] != rt.idx[p] ? 1u : 0u;
+        rt.first[p] = first;
+    }
+    __syncthreads();
+    bool bad = false;
+    for (uint32_t t = 0; t < s.tokens; ++t) bad |= rt.bad[t] != 0;
+    CombineEntry* comb = ws_ptr<CombineEntry>(w, w.off_combine);
+    if (p < P) {
+        const uint32_t e = rt.idx[p], t = p / K, k = p % K;
+        const float wt = rt.wt[p];
+        if (publish) {
+            *gp(ws_ptr<uint32_t>(w, w.off_route_idx) + p) = e;
+            *gp(ws_ptr<float>(w, w.off_route_w) + p) = wt;
+        }
+        uint32_t a = 0, slot = 0, ntok = 0, pos = 0;
         for (uint32_t q = 0; q < P; ++q) {
-            if (s_idx[q] == e) {
+            const uint32_t eq = rt.idx[q];
+            a += (rt.first[q] && eq < e) ? 1u : 0u;
+            if (eq == e) {
                 ++ntok;
                 if (q < p) ++slot;
             }
         }
-        for (uint32_t j = 0; j < K; ++j) pos += s_idx[t * K + j] < e ? 1u : 0u;
-        act[a].tok[slot] = t;
-        act[a].route_w[slot] = wt;
+        for (uint32_t j = 0; j < K; ++j) pos += rt.idx[t * K + j] < e ? 1u : 0u;
+        rt.act[a].tok[slot] = t;
+        rt.act[a].route_w[slot] = wt;
         if (slot == 0) {
-            act[a].expert = e;
-            act[a].ntok = ntok;
-            act[a].apply_w = s.semantics == kSemDeepseek ? 1u : 0u;
-            act[a].limit = s.routed_limit;
+            rt.act[a].expert = e;
+            rt.act[a].ntok = ntok;
+            rt.act[a].apply_w = s.semantics == kSemDeepseek ? 1u : 0u;
+            rt.act[a].limit = s.routed_limit;
         }
         const uint32_t at = s.semantics == kSemDeepseek ? pos : k;
-        comb[t * (K + 1) + at] = CombineEntry{(a << 3) | slot, s.semantics == kSemQwen ? wt : 1.0f};
+        if (publish) {
+            uint32_t* ce = reinterpret_cast<uint32_t*>(comb + t * (K + 1) + at);
+            *gp(ce) = (a << 3) | slot;
+            *gp(ce + 1) = __float_as_uint(s.semantics == kSemQwen ? wt : 1.0f);
+        }
     }
     if (threadIdx.x == 0) {
+        uint32_t n_routed = 0;
+        for (uint32_t q = 0; q < P; ++q) n_routed += rt.first[q];
         if (s.has_shared) {
-            ActiveExpert& sh = act[n_routed];
+            ActiveExpert& sh = rt.act[n_routed];
             sh.expert = E;
             sh.ntok = s.tokens;
             sh.apply_w = 0;
@@ -461,22 +487,36 @@ __global__ void __launch_bounds__(512) k_moe_route(const MoeShape s, const MoeIn
             for (uint32_t t = 0; t < s.tokens; ++t) {
                 sh.tok[t] = t;
                 sh.route_w[t] = 1.0f;
-                comb[t * (K + 1) + K] = CombineEntry{(n_routed << 3) | t, 1.0f};
+                if (publish) {
+                    uint32_t* ce = reinterpret_cast<uint32_t*>(comb + t * (K + 1) + K);
+                    *gp(ce) = (n_routed << 3) | t;
+                    *gp(ce + 1) = __float_as_uint(1.0f);
+                }
             }
         }
-        hdr->n_active = s_bad ? 0u : n_routed + (s.has_shared ? 1u : 0u);
-        if (s_bad) atomicOr(&hdr->status, kStatusBadRoute);
+        rt.n_active = bad ? 0u : n_routed + (s.has_shared ? 1u : 0u);
+        if (publish) {
+            MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
+            *gp(&hdr->n_active) = rt.n_active;
+            uint32_t bits = bad ? kStatusBadRoute : 0u;
+            const uint32_t* xf = ws_ptr<uint32_t>(w, w.off_xflags);
+            for (uint32_t xb = 0; xb < w.xblocks; ++xb)
+                for (uint32_t t = 0; t < s.tokens; ++t)
+                    if (*gp(xf + 8u * xb + t)) bits |= kStatusNonFiniteInput;
+            if (bits) or_bits(&hdr->status, bits);
+        }
     }
-    // The tokens' activations as MFMA limbs.
-    __shared__ float s_red[16];
-    for (uint32_t t = 0; t < s.tokens; ++t)
-        prep_token_block(in.x + (uint64_t)t * s.width, s.width, limb_slots(s.tokens), t,
-                         ws_ptr<int8_t>(w, w.off_xlimbs), ws_ptr<int>(w, w.off_xexp),
-                         &hdr->status, s_red);
+    __syncthreads();
+    if (publish) {
+        const uint32_t words = rt.n_active * (uint32_t)(sizeof(ActiveExpert) / 4u);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(rt.act);
+        uint32_t* dst = ws_ptr<uint32_t>(w, w.off_active);
+        for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) *gp(dst + i) = src[i];
+    }
 }
 
 // ------------------------------------------------------------------------------------------
-// Expert projections.
+// SwiGLU.
 // ------------------------------------------------------------------------------------------
 
 __device__ __forceinline__ float silu_f(float v) {
@@ -508,288 +548,547 @@ __device__ __forceinline__ float swiglu(uint32_t sem, float g, float u, float li
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
 }
 
-// Gate and up projections of one active expert over two 32-row tiles, then the SwiGLU.
-// Eight waves: wave w takes tile 2*blockIdx.x + w/4, matrix w%2 (gate, up) and half (w/2)%2 of
-// the columns; the two halves are added in order. Two tiles per block let the grid fit the
-// GPU in one round and halve the activation staging per row.
-template <uint32_t FMT, int NT, bool LDS_A>
-__global__ void __launch_bounds__(512) k_moe_gateup(const MoeShape s, const MoeInputs in,
-                                                    const MoeWorkspace w) {
-    __shared__ LdsTables lds;
-    __shared__ float partial[2][2][2][NT][32];  // [tile][matrix][half][slot][row]
-    extern __shared__ __align__(16) int8_t dyn_lds[];
-    __shared__ __align__(16) int8_t s_zero[16];
-    const MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
-    const uint32_t a = blockIdx.y;
-    if (a >= hdr->n_active) return;
-    const ActiveExpert* aep = ws_ptr<ActiveExpert>(w, w.off_active) + a;
-    const uint32_t ntok = aep->ntok;
-    vl_tiled_layout L;
-    vl_make_layout(FMT, s.inter, s.width, &L);
+// ------------------------------------------------------------------------------------------
+// Stream policies.
+// ------------------------------------------------------------------------------------------
 
-    constexpr int S = Acc<NT>::kSlots;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int tw = wave >> 2, mat = wave & 1, half = (wave >> 1) & 1;
-    const uint32_t t = 2u * blockIdx.x + tw;
-    const bool tile_on = t < L.tiles;
-    const uint32_t n = lane & 31;
-    const int hh = lane >> 5;
-    const MoeExpert ex = in.experts[aep->expert];
-    const uint8_t* W = mat == 0 ? ex.gate : ex.up;
-    const uint32_t chunks = chunks_of<FMT>(L);
-    const uint32_t c0 = tile_on ? chunks * half / 2u : 0u;
-    const uint32_t c1 = tile_on ? chunks * (half + 1) / 2u : 0u;
-    const uint32_t xslots = limb_slots(s.tokens);
-    const int slot = a_slot_of_lane();
-    const bool on = slot < (int)ntok;
-    const int8_t* xl = ws_ptr<int8_t>(w, w.off_xlimbs);
-    const uint32_t limb_off = (uint32_t)a_limb_of_lane() * 32u + 16u * hh;
-    float accf[S];
-    tile_partial<FMT, NT>(L, W, tile_on ? t : 0u, c0, c1, (LDS_A ? NT : xslots) * 128u, lds, accf,
-                          [&](uint32_t& stride) -> const int8_t* {
-        load_tables<FMT>(lds);
-        if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(s_zero)[threadIdx.x] = 0;
-        if (LDS_A) stage_limbs<NT>(dyn_lds, xl, L.groups, xslots, ntok,
-                                   [&](uint32_t sl) { return aep->tok[sl]; });
-        __syncthreads();
-        if (!on) {
-            stride = 0;
-            return s_zero;
-        }
-        return LDS_A ? dyn_lds + (uint32_t)slot * 128u + limb_off
-                     : xl + (uint64_t)aep->tok[slot] * 128u + limb_off;
-    });
-#pragma unroll
-    for (int i = 0; i < S; ++i) {
-        const int sl = 2 * i + hh;
-        if (sl < NT) partial[tw][mat][half][sl][n] = accf[i];
+// Sum of a job's records for (matrix mat, slot s, row n): records first..last in order, each
+// record's two lane halves in order.
+template <int NT>
+__device__ __forceinline__ float sum_records(const float* rec, uint32_t rec_floats, uint32_t j,
+                                             uint32_t first, uint32_t last, uint32_t mat,
+                                             uint32_t s, uint32_t n) {
+    float v = 0.0f;
+    for (uint32_t k = first; k <= last; ++k) {
+        const float* r = rec + (uint64_t)(k + j) * rec_floats + (mat * NT + s) * 64u;
+        v += load_shared(r + n) + load_shared(r + 32u + n);
     }
-    __syncthreads();
-    for (uint32_t idx = threadIdx.x; idx < 2u * NT * 32u; idx += blockDim.x) {
-        const uint32_t tt = idx / (NT * 32u), sl = (idx / 32u) % NT, r = idx % 32u;
-        const uint32_t row = (2u * blockIdx.x + tt) * 32u + r;
-        if (sl < ntok && row < s.inter) {
-            const int e = ws_ptr<int>(w, w.off_xexp)[aep->tok[sl]];
-            const float g = ldexpf(partial[tt][0][0][sl][r] + partial[tt][0][1][sl][r], -e);
-            const float u = ldexpf(partial[tt][1][0][sl][r] + partial[tt][1][1][sl][r], -e);
-            const float h = swiglu(s.semantics, g, u, aep->limit, aep->apply_w != 0, aep->route_w[sl]);
-            MoeHeader* hw = ws_ptr<MoeHeader>(w, w.off_header);
-            if (!isfinite(g) || !isfinite(u) || !isfinite(h)) atomicOr(&hw->status, kStatusNonFiniteOutput);
-            ws_ptr<float>(w, w.off_h)[((uint64_t)a * kMoeMaxTokens + sl) * s.inter + row] = h;
-            atomicMax(ws_ptr<uint32_t>(w, w.off_hmax) + a * kMoeMaxTokens + sl,
-                      __float_as_uint(isfinite(h) ? fabsf(h) : 0.0f));
-        }
-    }
+    return v;
 }
 
-// h of (active expert, token) -> limbs, layout [a][group][8 slots][4][32].
-__global__ void __launch_bounds__(256) k_moe_hprep(const MoeShape s, const MoeWorkspace w) {
-    const MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
-    const uint32_t sl = blockIdx.x, a = blockIdx.y;
-    if (a >= hdr->n_active) return;
-    const ActiveExpert* act = ws_ptr<ActiveExpert>(w, w.off_active);
-    if (sl >= act[a].ntok) return;
-    const float m = __uint_as_float(ws_ptr<uint32_t>(w, w.off_hmax)[a * kMoeMaxTokens + sl]);
-    int q = 0;
-    frexpf(m, &q);
-    const int e = m > 0.0f ? 30 - q : 0;
-    if (threadIdx.x == 0) ws_ptr<int>(w, w.off_hexp)[a * kMoeMaxTokens + sl] = e;
-    const float* h = ws_ptr<float>(w, w.off_h) + ((uint64_t)a * kMoeMaxTokens + sl) * s.inter;
-    int8_t* out = ws_ptr<int8_t>(w, w.off_hlimbs) + (uint64_t)a * (s.inter / 32u) * kMoeMaxTokens * 128u;
-    for (uint32_t k4 = threadIdx.x * 4u; k4 < s.inter; k4 += blockDim.x * 4u) {
-        uint32_t packed[4] = {0, 0, 0, 0};
-        for (int i = 0; i < 4; ++i) {
-            const float v = h[k4 + i];
-            int X = isfinite(v) ? (int)rintf(ldexpf(v, e)) : 0;
-            for (int l = 0; l < 4; ++l) {
-                const int digit = l < 3 ? (int)(int8_t)(X & 0xff) : X;
-                packed[l] |= ((uint32_t)digit & 0xffu) << (8 * i);
-                X = (X - digit) >> 8;
+// Tile epilogues run out of line: they are rare, and inlined into the streaming loop their
+// float64 code would compete with the in-flight weight buffers for registers.
+
+// Last wave of gate/up tile job j: gate/up sums, SwiGLU, the tile's h rows, and the maxima of |h|
+// per 256-row block and slot (the down kernel's limb exponents).
+struct GateUpFixup {
+    const float* rec;  // gate/up records
+    float* h;          // [A][NT][inter]
+    uint32_t* hmax;    // [A][hblocks][8]
+    uint32_t* status;
+    uint32_t j, first, last, tiles, hblocks, inter, semantics;
+    ActiveExpert ae;   // the tile's expert
+};
+
+template <int NT>
+__device__ __attribute__((noinline)) void gateup_fixup(GateUpFixup f) {
+    const uint32_t a = f.j / f.tiles, t = f.j - a * f.tiles;
+    const ActiveExpert& ae = f.ae;
+    const uint32_t lane = threadIdx.x & 63u, n = lane & 31u, hh = lane >> 5;
+    const uint32_t row = t * 32u + n, sb = t / 8u, F = f.inter;
+    const uint32_t nt = uni(ae.ntok);
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < (NT + 1) / 2; ++i) {
+        const uint32_t sl = 2u * i + hh;
+        float hmag = 0.0f;
+        if (sl < nt) {
+            const float g = sum_records<NT>(f.rec, 2u * NT * 64u, f.j, f.first, f.last, 0, sl, n);
+            const float u = sum_records<NT>(f.rec, 2u * NT * 64u, f.j, f.first, f.last, 1, sl, n);
+            if (row < F) {
+                const float h = swiglu(f.semantics, g, u, ae.limit, ae.apply_w != 0, ae.route_w[sl]);
+                bad |= !isfinite(g) || !isfinite(u) || !isfinite(h);
+                *gp(f.h + ((uint64_t)a * NT + sl) * F + row) = h;
+                hmag = isfinite(h) ? fabsf(h) : 0.0f;
             }
         }
-        const uint64_t base = ((uint64_t)(k4 / 32u) * kMoeMaxTokens + sl) * 128u + (k4 % 32u);
-        for (int l = 0; l < 4; ++l) *reinterpret_cast<uint32_t*>(out + base + 32u * l) = packed[l];
+        for (int o = 16; o > 0; o >>= 1) hmag = fmaxf(hmag, __shfl_xor(hmag, o));
+        if (n == 0 && sl < nt)
+            __hip_atomic_fetch_max(gp(f.hmax + ((uint64_t)a * f.hblocks + sb) * 8u + sl),
+                                   __float_as_uint(hmag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (__any(bad) && lane == 0) or_bits(f.status, kStatusNonFiniteOutput);
 }
 
-// Down projection of one active expert over four 32-row tiles: wave w takes tile
-// 4*blockIdx.x + w/2 and half w%2 of the columns. The block stages the expert's activation
-// limbs once for its 128 rows.
-template <uint32_t FMT, int NT, bool LDS_A>
-__global__ void __launch_bounds__(512) k_moe_down(const MoeShape s, const MoeInputs in,
-                                                  const MoeWorkspace w) {
-    __shared__ LdsTables lds;
-    __shared__ float partial[4][2][NT][32];  // [tile][half][slot][row]
-    extern __shared__ __align__(16) int8_t dyn_lds[];
-    __shared__ __align__(16) int8_t s_zero[16];
-    const MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
-    const uint32_t a = blockIdx.y;
-    if (a >= hdr->n_active) return;
-    const ActiveExpert* act = ws_ptr<ActiveExpert>(w, w.off_active);
-    const uint32_t ntok = act[a].ntok;
+// Gate and up projections: job j = (active expert a, tile t) = (j / tiles, j % tiles), two
+// matrices per job.
+template <uint32_t FMT, int NT, bool LDS>
+struct GateUp {
+    // wave loop interface
+    uint32_t chunks, nmat, ng;
+    ASrc<LDS, NT * 128u> as;
+    float hscale;
+    // context
+    MoeShape s;
+    MoeInputs in;
+    MoeWorkspace w;
     vl_tiled_layout L;
-    vl_make_layout(FMT, s.width, s.inter, &L);
+    uint32_t tiles, UJ, TU, NW, wid;
+    uint32_t stage_off, scale_off;
+    const uint8_t* lds;
+    const RouteLds* rt;
+    const uint8_t* const* wptr;  // [a][2] gate, up
+    uint32_t ntok;
+    uint32_t tok[NT];
 
-    constexpr int S = Acc<NT>::kSlots;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int tw = wave >> 1, half = wave & 1;
-    const uint32_t t = 4u * blockIdx.x + tw;
-    const bool tile_on = t < L.tiles;
-    const uint32_t n = lane & 31;
-    const int hh = lane >> 5;
-    const uint8_t* W = in.experts[act[a].expert].down;
-    const uint32_t chunks = chunks_of<FMT>(L);
-    const uint32_t c0 = tile_on ? chunks * half / 2u : 0u;
-    const uint32_t c1 = tile_on ? chunks * (half + 1) / 2u : 0u;
-    const int slot = a_slot_of_lane();
-    const bool on = slot < (int)ntok;
-    const int8_t* hl = ws_ptr<int8_t>(w, w.off_hlimbs) + (uint64_t)a * (s.inter / 32u) * kMoeMaxTokens * 128u;
-    const uint32_t lane_off = ((uint32_t)slot * 4u + a_limb_of_lane()) * 32u + 16u * hh;
-    float accf[S];
-    tile_partial<FMT, NT>(L, W, tile_on ? t : 0u, c0, c1, (LDS_A ? NT : kMoeMaxTokens) * 128u, lds,
-                          accf, [&](uint32_t& stride) -> const int8_t* {
-        load_tables<FMT>(lds);
-        if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(s_zero)[threadIdx.x] = 0;
-        if (LDS_A) stage_limbs<NT>(dyn_lds, hl, L.groups, kMoeMaxTokens, ntok,
-                                   [](uint32_t sl) { return sl; });
-        __syncthreads();
-        if (!on) {
-            stride = 0;
-            return s_zero;
-        }
-        return LDS_A ? dyn_lds + lane_off : hl + lane_off;
-    });
+    __device__ TileRef tref(uint32_t j, uint32_t mat) const {
+        const uint32_t a = j / tiles, t = j - a * tiles;
+        return tile_ref<FMT>(L, uni_ptr(wptr[2u * a + mat]), t);
+    }
+
+    __device__ void job_begin(uint32_t j) {
+        const uint32_t a = j / tiles;
+        const ActiveExpert& ae = rt->act[a];
+        ntok = uni(ae.ntok);
 #pragma unroll
-    for (int i = 0; i < S; ++i) {
-        const int sl = 2 * i + hh;
-        if (sl < NT) partial[tw][half][sl][n] = accf[i];
+        for (int s2 = 0; s2 < NT; ++s2) tok[s2] = uni(ae.tok[(uint32_t)s2 < ntok ? s2 : 0]);
+        const uint32_t m = threadIdx.x & 31u, kh = (threadIdx.x >> 5) & 1u;
+        const uint32_t sl = a_slot(m), limb = a_limb(m);
+        const uint32_t tk = ae.tok[sl < ntok ? sl : 0u];
+        const uint32_t off = tk * 128u + limb * 32u + 16u * kh;
+        if (LDS) as.off = stage_off + off;
+        else as.ptr = ws_ptr<int8_t>(w, w.off_xlimbs) + off;
+    }
+
+    __device__ void scales(uint32_t, uint32_t c, float (&fs)[NT]) const {
+        const uint32_t eb = FMT == VL_TYPE_Q8_0 ? c / 2u : c;
+        const float* sc = reinterpret_cast<const float*>(lds + scale_off) + 8u * eb;
+#pragma unroll
+        for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? sc[tok[s2]] : 0.0f;
+    }
+
+    __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&m1)[NT]) const {
+        const uint32_t lane = threadIdx.x & 63u;
+        constexpr uint32_t RF = 2u * NT * 64u;
+        float* rec = ws_ptr<float>(w, w.off_rec_gu);
+        float* r = rec + (uint64_t)(wid + j) * RF;
+#pragma unroll
+        for (int s2 = 0; s2 < NT; ++s2) {
+            store_shared(r + s2 * 64u + lane, m0[s2]);
+            store_shared(r + (NT + s2) * 64u + lane, m1[s2]);
+        }
+        const uint32_t first = wave_of_unit(j * UJ, NW, TU);
+        const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
+        const MoeCounters cn = counters_of(w);
+        if (!arrive(cn.gu + j, last - first + 1u)) return;
+        GateUpFixup f;
+        f.ae = rt->act[j / tiles];
+        f.rec = rec;
+        f.h = ws_ptr<float>(w, w.off_h);
+        f.hmax = cn.hmax;
+        f.status = &ws_ptr<MoeHeader>(w, w.off_header)->status;
+        f.j = j;
+        f.first = first;
+        f.last = last;
+        f.tiles = tiles;
+        f.hblocks = w.hblocks;
+        f.inter = s.inter;
+        f.semantics = s.semantics;
+        gateup_fixup<NT>(f);
+    }
+};
+
+// Dynamic LDS of the gate/up kernel, from byte 0: decode tables, staged activation limbs (LDS
+// path), the 2^-e scales of the activation blocks, the routing state and the weight pointers.
+struct GateUpLds {
+    uint32_t stage, scale, route, wptr, bytes;
+};
+__host__ __device__ inline GateUpLds gateup_lds(uint32_t table_bytes, uint32_t stage_bytes,
+                                                uint32_t xblocks) {
+    GateUpLds l;
+    l.stage = table_bytes;
+    l.scale = l.stage + stage_bytes;
+    l.route = (l.scale + xblocks * 8u * 4u + 15u) & ~15u;
+    l.wptr = (l.route + (uint32_t)sizeof(RouteLds) + 15u) & ~15u;
+    l.bytes = l.wptr + kMaxActive * 2u * 8u;
+    return l;
+}
+
+template <uint32_t FMT, int NT, bool LDS>
+__global__ void __launch_bounds__(kStreamThreads) k_moe_gateup(const MoeShape s, const MoeInputs in,
+                                                               const MoeWorkspace w) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr uint32_t TB = table_bytes<FMT>();
+    const uint32_t stage_bytes = LDS ? (s.width / 32u) * NT * 128u : 0u;
+    const GateUpLds lay = gateup_lds(TB, stage_bytes, w.xblocks);
+    RouteLds& rt = *reinterpret_cast<RouteLds*>(lds + lay.route);
+    const uint8_t** wptr = reinterpret_cast<const uint8_t**>(lds + lay.wptr);
+    const uint32_t wave = threadIdx.x >> 6;
+    if (wave < s.tokens) {
+        // Waves 0..tokens-1 route; the others fill the decode tables and stage the activations.
+        route_token_wave(s, in, w, wave, rt);
+    } else {
+        const uint32_t tid = threadIdx.x - 64u * s.tokens, nthr = blockDim.x - 64u * s.tokens;
+        fill_tables<FMT>(lds, tid, nthr);
+        if (LDS) {
+            const uint4* src = ws_ptr<const uint4>(w, w.off_xlimbs);
+            uint4* dst = reinterpret_cast<uint4*>(lds + lay.stage);
+            for (uint32_t i = tid; i < stage_bytes / 16u; i += nthr) dst[i] = ld_u4(src + i);
+        }
+        const int* xe = ws_ptr<const int>(w, w.off_xexp);
+        float* sc = reinterpret_cast<float*>(lds + lay.scale);
+        for (uint32_t i = tid; i < w.xblocks * 8u; i += nthr)
+            sc[i] = (i & 7u) < s.tokens ? __builtin_amdgcn_ldexpf(1.0f, -*gp(xe + i)) : 0.0f;
     }
     __syncthreads();
-    for (uint32_t idx = threadIdx.x; idx < 4u * NT * 32u; idx += blockDim.x) {
-        const uint32_t tt = idx / (NT * 32u), sl = (idx / 32u) % NT, r = idx % 32u;
-        const uint32_t row = (4u * blockIdx.x + tt) * 32u + r;
-        if (sl < ntok && row < s.width) {
-            const int e = ws_ptr<int>(w, w.off_hexp)[a * kMoeMaxTokens + sl];
-            const float y = ldexpf(partial[tt][0][sl][r] + partial[tt][1][sl][r], -e);
-            ws_ptr<float>(w, w.off_ypart)[((uint64_t)a * kMoeMaxTokens + sl) * s.width + row] = y;
+    build_active(s, w, blockIdx.x == 0, rt);
+    for (uint32_t i = threadIdx.x; i < 2u * rt.n_active; i += blockDim.x) {
+        const MoeExpert& ex = in.experts[rt.act[i / 2u].expert];
+        wptr[i] = (i % 2u) ? ex.up : ex.gate;
+    }
+    __syncthreads();
+    GateUp<FMT, NT, LDS> pol;
+    pol.s = s;
+    pol.in = in;
+    pol.w = w;
+    vl_make_layout(FMT, s.inter, s.width, &pol.L);
+    pol.chunks = units_per_row(FMT, s.width);
+    pol.nmat = 2;
+    pol.ng = pol.L.groups;
+    pol.tiles = w.tiles_gu;
+    pol.UJ = 2u * pol.chunks;
+    pol.TU = uni(rt.n_active) * w.tiles_gu * pol.UJ;
+    pol.NW = active_waves(gridDim.x * kStreamWaves, pol.TU);
+    pol.wid = blockIdx.x * kStreamWaves + uni(threadIdx.x >> 6);
+    pol.stage_off = lay.stage;
+    pol.scale_off = lay.scale;
+    pol.lds = lds;
+    pol.rt = &rt;
+    pol.wptr = wptr;
+    pol.hscale = (threadIdx.x & 32u) ? 65536.0f : 1.0f;
+    pol.ntok = 0;
+    stream_range<FMT, NT, LDS>(pol, range_begin(pol.wid, pol.NW, pol.TU),
+                               range_begin(pol.wid + 1u, pol.NW, pol.TU), lds);
+}
+
+// Last wave of down job j: the expert's output rows of tile t; the last expert of tile t then
+// combines the layer output rows in each token's combine order.
+struct DownFixup {
+    const float* rec;  // down records
+    float* ypart;      // [A][NT][width]
+    float* out;        // [tokens][width]
+    const CombineEntry* comb;
+    uint32_t* tile_cnt;
+    uint32_t* status;
+    uint32_t j, first, last, tiles, n_active, width, tokens, top_k, has_shared, semantics, ntok;
+};
+
+template <int NT>
+__device__ __attribute__((noinline)) void down_fixup(DownFixup f) {
+    const uint32_t a = f.j / f.tiles, t = f.j - a * f.tiles;
+    const uint32_t lane = threadIdx.x & 63u, n = lane & 31u, hh = lane >> 5;
+    const uint32_t row = t * 32u + n, H = f.width;
+    const uint32_t nt = f.ntok;
+#pragma unroll
+    for (int i = 0; i < (NT + 1) / 2; ++i) {
+        const uint32_t sl = 2u * i + hh;
+        if (sl < nt) {
+            const float y = sum_records<NT>(f.rec, NT * 64u, f.j, f.first, f.last, 0, sl, n);
+            if (row < H) store_shared(f.ypart + ((uint64_t)a * NT + sl) * H + row, y);
         }
+    }
+    if (!arrive(f.tile_cnt + t, f.n_active)) return;
+    const uint32_t K = f.top_k, nent = K + (f.has_shared ? 1u : 0u);
+    bool bad = false;
+    for (uint32_t idx = lane; idx < f.tokens * 32u; idx += 64u) {
+        const uint32_t tk = idx / 32u, r = t * 32u + idx % 32u;
+        if (r >= H) continue;
+        float acc = 0.0f;
+        for (uint32_t k = 0; k < nent; ++k) {
+            const uint32_t* ce = reinterpret_cast<const uint32_t*>(f.comb + tk * (K + 1u) + k);
+            const uint32_t src = *gp(ce);
+            const float wt = __uint_as_float(*gp(ce + 1));
+            const float y = load_shared(f.ypart + ((uint64_t)(src >> 3) * NT + (src & 7u)) * H + r);
+            acc = (f.semantics == kSemQwen && k < K) ? __fadd_rn(acc, __fmul_rn(y, wt))
+                                                    : __fadd_rn(acc, y);
+        }
+        bad |= !isfinite(acc);
+        *gp(f.out + (uint64_t)tk * H + r) = acc;
+    }
+    if (__any(bad) && lane == 0) or_bits(f.status, kStatusNonFiniteOutput);
+}
+
+// Down projection: job j = (active expert a, tile t of the output rows). The block turns the h of
+// the experts its units touch (a0 .. a0 + stage - 1) into limbs, in LDS when LDS is set and in
+// the block's slab of the workspace otherwise, layout [expert][inter/32][NT][4][32].
+template <uint32_t FMT, int NT, bool LDS>
+struct Down {
+    uint32_t chunks, nmat, ng;
+    ASrc<LDS, NT * 128u> as;
+    float hscale;
+    MoeShape s;
+    MoeInputs in;
+    MoeWorkspace w;
+    uint32_t n_active;
+    vl_tiled_layout L;
+    uint32_t tiles, UJ, TU, NW, wid;
+    uint32_t a0, expert_bytes, stage_off, scale_off;
+    const int8_t* slab;
+    const uint8_t* lds;
+    const ActiveExpert* act;
+    const uint8_t* const* wptr;
+    uint32_t cur_a, ntok;
+
+    __device__ TileRef tref(uint32_t j, uint32_t) const {
+        const uint32_t a = j / tiles, t = j - a * tiles;
+        return tile_ref<FMT>(L, uni_ptr(wptr[a]), t);
+    }
+
+    __device__ void job_begin(uint32_t j) {
+        cur_a = j / tiles;
+        ntok = uni(act[cur_a].ntok);
+        const uint32_t m = threadIdx.x & 31u, kh = (threadIdx.x >> 5) & 1u;
+        const uint32_t sl = a_slot(m), limb = a_limb(m);
+        const uint32_t off = (cur_a - a0) * expert_bytes + (sl < ntok ? sl : 0u) * 128u + limb * 32u + 16u * kh;
+        if (LDS) as.off = stage_off + off;
+        else as.ptr = slab + off;
+    }
+
+    __device__ void scales(uint32_t, uint32_t c, float (&fs)[NT]) const {
+        const uint32_t eb = FMT == VL_TYPE_Q8_0 ? c / 2u : c;
+        const float* sc = reinterpret_cast<const float*>(lds + scale_off) + ((cur_a - a0) * w.hblocks + eb) * 8u;
+#pragma unroll
+        for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? sc[s2] : 0.0f;
+    }
+
+    __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&)[NT]) const {
+        const uint32_t lane = threadIdx.x & 63u;
+        constexpr uint32_t RF = NT * 64u;
+        float* rec = ws_ptr<float>(w, w.off_rec_dn);
+        float* r = rec + (uint64_t)(wid + j) * RF;
+#pragma unroll
+        for (int s2 = 0; s2 < NT; ++s2) store_shared(r + s2 * 64u + lane, m0[s2]);
+        const uint32_t first = wave_of_unit(j * UJ, NW, TU);
+        const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
+        const MoeCounters cn = counters_of(w);
+        if (!arrive(cn.dn + j, last - first + 1u)) return;
+        DownFixup f;
+        f.rec = rec;
+        f.ypart = ws_ptr<float>(w, w.off_ypart);
+        f.out = in.out;
+        f.comb = ws_ptr<const CombineEntry>(w, w.off_combine);
+        f.tile_cnt = cn.tile;
+        f.status = &ws_ptr<MoeHeader>(w, w.off_header)->status;
+        f.j = j;
+        f.first = first;
+        f.last = last;
+        f.tiles = tiles;
+        f.n_active = n_active;
+        f.width = s.width;
+        f.tokens = s.tokens;
+        f.top_k = s.top_k;
+        f.has_shared = s.has_shared;
+        f.semantics = s.semantics;
+        f.ntok = uni(act[j / tiles].ntok);
+        down_fixup<NT>(f);
+    }
+};
+
+// h of experts a0..a1 -> limbs (dst, [expert - a0][inter/32][NT][4][32]) with one exponent per
+// 256-row block and slot from the gate/up kernel's maxima; scale[(a - a0)][block][8] = 2^-e.
+template <int NT>
+__device__ __forceinline__ void convert_h(const MoeWorkspace& w, uint32_t inter, uint32_t a0,
+                                          uint32_t a1, const ActiveExpert* act, int8_t* dst,
+                                          float* scale) {
+    const uint32_t* hmax = counters_of(w).hmax;
+    const float* h = ws_ptr<const float>(w, w.off_h);
+    const uint32_t na = a1 - a0 + 1u;
+    for (uint32_t i = threadIdx.x; i < na * w.hblocks * 8u; i += blockDim.x) {
+        const uint32_t m = *gp(hmax + (uint64_t)a0 * w.hblocks * 8u + i);
+        scale[i] = __builtin_amdgcn_ldexpf(1.0f, -limb_exponent(__uint_as_float(m)));
+    }
+    const uint32_t quads = inter / 4u;
+    for (uint32_t i = threadIdx.x; i < na * NT * quads; i += blockDim.x) {
+        const uint32_t q = i % quads, sl = (i / quads) % NT, al = i / (quads * NT);
+        const uint32_t a = a0 + al, col = 4u * q;
+        if (sl >= act[a].ntok) continue;
+        const uint32_t m = *gp(hmax + ((uint64_t)a * w.hblocks + col / 256u) * 8u + sl);
+        const int e = limb_exponent(__uint_as_float(m));
+        const float4 f4 = ld_f4(h + ((uint64_t)a * NT + sl) * inter + col);
+        const float v[4] = {f4.x, f4.y, f4.z, f4.w};
+        uint32_t packed[4];
+        limbs4(v, e, packed);
+        int8_t* d = dst + (uint64_t)al * down_expert_bytes(inter, NT) +
+                    ((uint64_t)(col / 32u) * NT + sl) * 128u + (col % 32u);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) *reinterpret_cast<uint32_t*>(d + 32u * l) = packed[l];
     }
 }
 
-__global__ void __launch_bounds__(256) k_moe_combine(const MoeShape s, const MoeInputs in,
-                                                     const MoeWorkspace w) {
-    MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (uint64_t)s.tokens * s.width) return;
-    const uint32_t t = (uint32_t)(i / s.width), c = (uint32_t)(i % s.width);
-    if (hdr->n_active == 0) {
-        in.out[i] = 0.0f;
+// Dynamic LDS of the down kernel, from byte 0: decode tables, staged h limbs (LDS path), the 2^-e
+// scales of the staged experts' h blocks, the active list and the down weight pointers.
+struct DownLds {
+    uint32_t stage, scale, act, wptr, bytes;
+};
+__host__ __device__ inline DownLds down_lds(uint32_t table_bytes, uint32_t stage_bytes,
+                                            uint32_t stage, uint32_t hblocks) {
+    DownLds l;
+    l.stage = table_bytes;
+    l.scale = l.stage + stage_bytes;
+    l.act = (l.scale + stage * hblocks * 8u * 4u + 15u) & ~15u;
+    l.wptr = l.act + kMaxActive * (uint32_t)sizeof(ActiveExpert);
+    l.bytes = l.wptr + kMaxActive * 8u;
+    return l;
+}
+
+template <uint32_t FMT, int NT, bool LDS>
+__global__ void __launch_bounds__(kStreamThreads) k_moe_down(const MoeShape s, const MoeInputs in,
+                                                             const MoeWorkspace w) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const MoeHeader* hdr = ws_ptr<const MoeHeader>(w, w.off_header);
+    const uint32_t n_active = uni(*gp(&hdr->n_active));
+    const uint32_t tiles = w.tiles_dn, UJ = units_per_row(FMT, s.inter);
+    const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * kStreamWaves, TU);
+    // Experts this block's units touch.
+    const uint32_t ub0 = range_begin(blockIdx.x * kStreamWaves, NW, TU);
+    const uint32_t ub1 = range_begin((blockIdx.x + 1u) * kStreamWaves, NW, TU);
+    const uint32_t a0 = ub0 < ub1 ? (ub0 / UJ) / tiles : 0u;
+    const uint32_t a1 = ub0 < ub1 ? ((ub1 - 1u) / UJ) / tiles : 0u;
+    constexpr uint32_t TB = table_bytes<FMT>();
+    const uint32_t eb = down_expert_bytes(s.inter, NT);
+    const uint32_t stage_bytes = LDS ? w.stage * eb : 0u;
+    const DownLds lay = down_lds(TB, stage_bytes, w.stage, w.hblocks);
+    ActiveExpert* act = reinterpret_cast<ActiveExpert*>(lds + lay.act);
+    const uint8_t** wptr = reinterpret_cast<const uint8_t**>(lds + lay.wptr);
+    int8_t* slab = ws_ptr<int8_t>(w, w.off_hslab) + (uint64_t)blockIdx.x * w.stage * eb;
+    {
+        const uint32_t words = n_active * (uint32_t)(sizeof(ActiveExpert) / 4u);
+        const uint32_t* src = ws_ptr<const uint32_t>(w, w.off_active);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(act);
+        for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) dst[i] = *gp(src + i);
+    }
+    fill_tables<FMT>(lds);
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n_active; i += blockDim.x)
+        wptr[i] = in.experts[act[i].expert].down;
+    if (ub0 < ub1)
+        convert_h<NT>(w, s.inter, a0, a1, act, LDS ? reinterpret_cast<int8_t*>(lds + lay.stage) : slab,
+                      reinterpret_cast<float*>(lds + lay.scale));
+    __syncthreads();
+    if (n_active == 0) {
+        if (blockIdx.x == 0)
+            for (uint32_t i = threadIdx.x; i < s.tokens * s.width; i += blockDim.x) *gp(in.out + i) = 0.0f;
         return;
     }
-    const CombineEntry* comb = ws_ptr<CombineEntry>(w, w.off_combine) + (uint64_t)t * (s.top_k + 1u);
-    const float* yp = ws_ptr<float>(w, w.off_ypart);
-    const uint32_t n = s.top_k + (s.has_shared ? 1u : 0u);
-    // All loads first (independent), then the additions in the combine order.
-    float y[kMoeMaxTopK + 1];
-    float wt[kMoeMaxTopK + 1];
-#pragma unroll
-    for (uint32_t k = 0; k < kMoeMaxTopK + 1; ++k) {
-        if (k < n) {
-            const CombineEntry ce = comb[k];
-            wt[k] = ce.w;
-            y[k] = yp[((uint64_t)(ce.src >> 3) * kMoeMaxTokens + (ce.src & 7u)) * s.width + c];
-        }
-    }
-    float acc = 0.0f;
-#pragma unroll
-    for (uint32_t k = 0; k < kMoeMaxTopK + 1; ++k) {
-        if (k < n)
-            acc = (s.semantics == kSemQwen && k < s.top_k) ? __fadd_rn(acc, __fmul_rn(y[k], wt[k]))
-                                                           : __fadd_rn(acc, y[k]);
-    }
-    if (!isfinite(acc)) atomicOr(&hdr->status, kStatusNonFiniteOutput);
-    in.out[i] = acc;
+    Down<FMT, NT, LDS> pol;
+    pol.s = s;
+    pol.in = in;
+    pol.w = w;
+    pol.n_active = n_active;
+    vl_make_layout(FMT, s.width, s.inter, &pol.L);
+    pol.chunks = UJ;
+    pol.nmat = 1;
+    pol.ng = pol.L.groups;
+    pol.tiles = tiles;
+    pol.UJ = UJ;
+    pol.TU = TU;
+    pol.NW = NW;
+    pol.wid = blockIdx.x * kStreamWaves + uni(threadIdx.x >> 6);
+    pol.a0 = a0;
+    pol.expert_bytes = eb;
+    pol.stage_off = lay.stage;
+    pol.scale_off = lay.scale;
+    pol.slab = slab;
+    pol.lds = lds;
+    pol.act = act;
+    pol.wptr = wptr;
+    pol.hscale = (threadIdx.x & 32u) ? 65536.0f : 1.0f;
+    pol.cur_a = 0;
+    pol.ntok = 0;
+    stream_range<FMT, NT, LDS>(pol, range_begin(pol.wid, NW, TU), range_begin(pol.wid + 1u, NW, TU), lds);
 }
 
 // ------------------------------------------------------------------------------------------
 // Launch sequence.
 // ------------------------------------------------------------------------------------------
 
-template <uint32_t FMT>
-static void launch_gateup_fmt(uint32_t slots, dim3 grid, const MoeShape& s, const MoeInputs& in,
-                              const MoeWorkspace& w, hipStream_t st) {
-    const uint32_t bytes = s.width / 32u * slots * 128u;
-    const bool lds_a = bytes <= kMaxLdsLimbBytes;
-    const uint32_t shm = lds_a ? bytes : 0u;
-    const dim3 blk(512);
-    switch (slots * 2 + (lds_a ? 1 : 0)) {
-        case 2: hipLaunchKernelGGL((k_moe_gateup<FMT, 1, false>), grid, blk, shm, st, s, in, w); break;
-        case 3: hipLaunchKernelGGL((k_moe_gateup<FMT, 1, true>), grid, blk, shm, st, s, in, w); break;
-        case 4: hipLaunchKernelGGL((k_moe_gateup<FMT, 2, false>), grid, blk, shm, st, s, in, w); break;
-        case 5: hipLaunchKernelGGL((k_moe_gateup<FMT, 2, true>), grid, blk, shm, st, s, in, w); break;
-        case 8: hipLaunchKernelGGL((k_moe_gateup<FMT, 4, false>), grid, blk, shm, st, s, in, w); break;
-        case 9: hipLaunchKernelGGL((k_moe_gateup<FMT, 4, true>), grid, blk, shm, st, s, in, w); break;
-        case 16: hipLaunchKernelGGL((k_moe_gateup<FMT, 8, false>), grid, blk, shm, st, s, in, w); break;
-        default: hipLaunchKernelGGL((k_moe_gateup<FMT, 8, true>), grid, blk, shm, st, s, in, w); break;
-    }
+// LDS of one workgroup on gfx950; the stream kernels keep all their LDS in the dynamic part.
+constexpr uint32_t kLdsBudget = 160u * 1024u;
+
+template <typename K, typename... Args>
+static hipError_t launch_stream(K kernel, uint32_t blocks, uint32_t shm, hipStream_t st,
+                                Args... args) {
+    const hipError_t e = ensure_dynamic_lds((const void*)kernel, shm);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kStreamThreads), shm, st, args...);
+    return hipGetLastError();
+}
+
+template <uint32_t FMT, int NT>
+static hipError_t launch_gateup_nt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
+                                   hipStream_t st) {
+    const uint32_t stage = (s.width / 32u) * NT * 128u;
+    const GateUpLds staged = gateup_lds(table_bytes<FMT>(), stage, w.xblocks);
+    if (staged.bytes <= kLdsBudget)
+        return launch_stream(k_moe_gateup<FMT, NT, true>, w.blocks, staged.bytes, st, s, in, w);
+    const GateUpLds plain = gateup_lds(table_bytes<FMT>(), 0u, w.xblocks);
+    return launch_stream(k_moe_gateup<FMT, NT, false>, w.blocks, plain.bytes, st, s, in, w);
 }
 
 template <uint32_t FMT>
-static void launch_down_fmt(uint32_t slots, dim3 grid, const MoeShape& s, const MoeInputs& in,
-                            const MoeWorkspace& w, hipStream_t st) {
-    const uint32_t bytes = s.inter / 32u * slots * 128u;
-    const bool lds_a = bytes <= kMaxLdsLimbBytes;
-    const uint32_t shm = lds_a ? bytes : 0u;
-    const dim3 blk(512);
-    switch (slots * 2 + (lds_a ? 1 : 0)) {
-        case 2: hipLaunchKernelGGL((k_moe_down<FMT, 1, false>), grid, blk, shm, st, s, in, w); break;
-        case 3: hipLaunchKernelGGL((k_moe_down<FMT, 1, true>), grid, blk, shm, st, s, in, w); break;
-        case 4: hipLaunchKernelGGL((k_moe_down<FMT, 2, false>), grid, blk, shm, st, s, in, w); break;
-        case 5: hipLaunchKernelGGL((k_moe_down<FMT, 2, true>), grid, blk, shm, st, s, in, w); break;
-        case 8: hipLaunchKernelGGL((k_moe_down<FMT, 4, false>), grid, blk, shm, st, s, in, w); break;
-        case 9: hipLaunchKernelGGL((k_moe_down<FMT, 4, true>), grid, blk, shm, st, s, in, w); break;
-        case 16: hipLaunchKernelGGL((k_moe_down<FMT, 8, false>), grid, blk, shm, st, s, in, w); break;
-        default: hipLaunchKernelGGL((k_moe_down<FMT, 8, true>), grid, blk, shm, st, s, in, w); break;
+static hipError_t launch_gateup_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
+                                    hipStream_t st) {
+    switch (w.slots) {
+        case 1: return launch_gateup_nt<FMT, 1>(s, in, w, st);
+        case 2: return launch_gateup_nt<FMT, 2>(s, in, w, st);
+        case 4: return launch_gateup_nt<FMT, 4>(s, in, w, st);
+        default: return launch_gateup_nt<FMT, 8>(s, in, w, st);
+    }
+}
+
+template <uint32_t FMT, int NT>
+static hipError_t launch_down_nt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
+                                 hipStream_t st) {
+    const DownLds staged = down_lds(table_bytes<FMT>(), w.stage * down_expert_bytes(s.inter, NT),
+                                    w.stage, w.hblocks);
+    if (staged.bytes <= kLdsBudget)
+        return launch_stream(k_moe_down<FMT, NT, true>, w.blocks, staged.bytes, st, s, in, w);
+    const DownLds plain = down_lds(table_bytes<FMT>(), 0u, w.stage, w.hblocks);
+    return launch_stream(k_moe_down<FMT, NT, false>, w.blocks, plain.bytes, st, s, in, w);
+}
+
+template <uint32_t FMT>
+static hipError_t launch_down_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
+                                  hipStream_t st) {
+    switch (w.slots) {
+        case 1: return launch_down_nt<FMT, 1>(s, in, w, st);
+        case 2: return launch_down_nt<FMT, 2>(s, in, w, st);
+        case 4: return launch_down_nt<FMT, 4>(s, in, w, st);
+        default: return launch_down_nt<FMT, 8>(s, in, w, st);
     }
 }
 
 hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
                       hipStream_t st, hipEvent_t* ev) {
-    if (!moe_shape_ok(s)) return hipErrorInvalidValue;
-    const uint32_t slots = limb_slots(s.tokens);
+    if (!moe_shape_ok(s) || w.blocks == 0) return hipErrorInvalidValue;
     auto mark = [&](uint32_t stage) {
         if (ev) (void)hipEventRecord(ev[stage], st);
     };
     mark(kStageRouter);
-    hipLaunchKernelGGL(k_moe_router, dim3(s.routing == kRouteGiven ? 1u : s.experts), dim3(256), 0, st, s, in, w);
-    mark(kStageRoute);
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(512), 0, st, s, in, w);
-    mark(kStagePrep);
+    const uint32_t router_blocks = s.routing == kRouteGiven ? 1u : s.experts;
+    hipLaunchKernelGGL(k_moe_router, dim3(router_blocks > w.xblocks ? router_blocks : w.xblocks),
+                       dim3(256), 0, st, s, in, w);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     mark(kStageGateUp);
-    const dim3 g_gu((s.inter + 63) / 64, w.max_active);
     switch (s.gate_type) {
-        case VL_TYPE_IQ2_XXS: launch_gateup_fmt<VL_TYPE_IQ2_XXS>(slots, g_gu, s, in, w, st); break;
-        case VL_TYPE_IQ3_XXS: launch_gateup_fmt<VL_TYPE_IQ3_XXS>(slots, g_gu, s, in, w, st); break;
-        case VL_TYPE_IQ1_S: launch_gateup_fmt<VL_TYPE_IQ1_S>(slots, g_gu, s, in, w, st); break;
-        case VL_TYPE_Q8_0: launch_gateup_fmt<VL_TYPE_Q8_0>(slots, g_gu, s, in, w, st); break;
+        case VL_TYPE_IQ2_XXS: e = launch_gateup_fmt<VL_TYPE_IQ2_XXS>(s, in, w, st); break;
+        case VL_TYPE_IQ3_XXS: e = launch_gateup_fmt<VL_TYPE_IQ3_XXS>(s, in, w, st); break;
+        case VL_TYPE_IQ1_S: e = launch_gateup_fmt<VL_TYPE_IQ1_S>(s, in, w, st); break;
+        case VL_TYPE_Q8_0: e = launch_gateup_fmt<VL_TYPE_Q8_0>(s, in, w, st); break;
         default: return hipErrorInvalidValue;
     }
-    mark(kStageHPrep);
-    hipLaunchKernelGGL(k_moe_hprep, dim3(kMoeMaxTokens, w.max_active), dim3(256), 0, st, s, w);
+    if (e != hipSuccess) return e;
     mark(kStageDown);
-    const dim3 g_dn((s.width + 127) / 128, w.max_active);
     switch (s.down_type) {
-        case VL_TYPE_IQ2_XXS: launch_down_fmt<VL_TYPE_IQ2_XXS>(slots, g_dn, s, in, w, st); break;
-        case VL_TYPE_IQ3_XXS: launch_down_fmt<VL_TYPE_IQ3_XXS>(slots, g_dn, s, in, w, st); break;
-        case VL_TYPE_IQ1_S: launch_down_fmt<VL_TYPE_IQ1_S>(slots, g_dn, s, in, w, st); break;
-        case VL_TYPE_Q8_0: launch_down_fmt<VL_TYPE_Q8_0>(slots, g_dn, s, in, w, st); break;
+        case VL_TYPE_IQ2_XXS: e = launch_down_fmt<VL_TYPE_IQ2_XXS>(s, in, w, st); break;
+        case VL_TYPE_IQ3_XXS: e = launch_down_fmt<VL_TYPE_IQ3_XXS>(s, in, w, st); break;
+        case VL_TYPE_IQ1_S: e = launch_down_fmt<VL_TYPE_IQ1_S>(s, in, w, st); break;
+        case VL_TYPE_Q8_0: e = launch_down_fmt<VL_TYPE_Q8_0>(s, in, w, st); break;
         default: return hipErrorInvalidValue;
     }
-    mark(kStageCombine);
-    const uint64_t total = (uint64_t)s.tokens * s.width;
-    hipLaunchKernelGGL(k_moe_combine, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, st, s, in, w);
     mark(kStageCount);
-    return hipGetLastError();
+    return e;
 }
 
 }  // namespace vl

@@ -1,0 +1,560 @@
+// Shared device code of the quantized matvec kernels ("stream" kernels).
+//
+// Work model. A kernel's work is a list of jobs (one job = one 32-row tile of one matrix, or of
+// a gate/up pair of matrices), each split into units (one unit = one IQ superblock, or four
+// Q8_0 blocks, of the tile's columns). The units of all jobs form one sequence, and every
+// wave of a persistent grid takes an equal contiguous range of it, so the whole grid finishes
+// together whatever the job count. A wave accumulates its share of a job in registers and
+// hands it over as a record; the last wave to finish a job sums the job's records in wave
+// order (a fixed order: results are deterministic) and runs the job's epilogue.
+//
+// Record handoff between waves on different XCDs uses only agent-scope atomic stores and loads
+// (which the gfx9 memory model makes coherent across the per-XCD L2s by themselves) and a
+// relaxed counter; a wave waits for its record stores to complete (s_waitcnt vmcnt(0)) before
+// it bumps the counter. This avoids the agent-scope fences, whose L2 write-back/invalidate
+// costs tens of nanoseconds each and serializes.
+//
+// MFMA operands (v_mfma_i32_32x32x32_i8). Lane (m, kh) = (lane % 32, lane / 32).
+//   B: weight row m of the tile, columns 16kh .. 16kh+15 of the group (vl_decode.h).
+//   A: row m carries limb l of token slot s, m = 8(s/2) + 4(l/2) + 2(s%2) + (l%2), so that in
+//      the result lane half kh holds limbs 2kh and 2kh+1 of slot s in registers 2s and 2s+1.
+//      One token therefore needs two result registers per lane, eight tokens sixteen.
+// Activations are int8 limbs of X = round(x * 2^e) (|X| <= 2^30) with one exponent per 256
+// columns and token; group results are scaled by the integer group scale and summed exactly
+// over a superblock, converted to float once per superblock, and scaled by the superblock's
+// weight factor, 2^-e and 65536 for the high limbs.
+#ifndef VL_STREAM_H
+#define VL_STREAM_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vl_decode.h"
+#include "vl_layout.h"
+#include "vl_tables.h"
+
+namespace vl {
+
+static __device__ const DecodeTables g_tables = make_decode_tables();
+
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Global-memory view of a pointer. Pointers that reach the kernels inside structures are
+// generic (flat) to the compiler; flat accesses also count against the LDS counter and block
+// LDS scheduling, so every global access in the stream kernels goes through this cast.
+#define VL_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ VL_GLOBAL T* gp(T* p) { return (VL_GLOBAL T*)p; }
+
+// 16-byte global load/store as ext-vector types (the HIP vector classes do not bind to
+// address-space qualified references).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_f4(const float* p) {
+    const f32x4 v = *gp(reinterpret_cast<const f32x4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 ld_u4(const void* p) {
+    const u32x4 v = *gp(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// A pointer every lane holds the same value of, moved to scalar registers.
+template <typename T>
+__device__ __forceinline__ T* uni_ptr(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint64_t lo = uni((uint32_t)v), hi = uni((uint32_t)(v >> 32));
+    return reinterpret_cast<T*>((hi << 32) | lo);
+}
+
+// Waves per persistent block, and blocks per CU.
+constexpr uint32_t kStreamWaves = 16;
+constexpr uint32_t kStreamThreads = kStreamWaves * 64;
+
+template <uint32_t FMT>
+__host__ __device__ constexpr uint32_t table_bytes() {
+    return FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_IQ3_XXS ? kReplTableBytes
+         : FMT == VL_TYPE_IQ1_S ? kIq1TableBytes : 0u;
+}
+
+// Columns of one unit.
+template <uint32_t FMT>
+__host__ __device__ constexpr uint32_t unit_cols() {
+    return FMT == VL_TYPE_Q8_0 ? 128u : 256u;
+}
+
+__host__ __device__ inline uint32_t units_per_row(uint32_t type, uint32_t cols) {
+    const uint32_t uc = type == VL_TYPE_Q8_0 ? 128u : 256u;
+    return (cols + uc - 1u) / uc;
+}
+
+// Exponent blocks (256 columns) of a row of activations.
+__host__ __device__ inline uint32_t exp_blocks(uint32_t cols) { return (cols + 255u) / 256u; }
+
+// Fills the block's decode tables in LDS, threads tid0, tid0 + nthr, ... of the block taking
+// part (the caller synchronizes).
+template <uint32_t FMT>
+__device__ __forceinline__ void fill_tables(uint8_t* lds, uint32_t tid0 = threadIdx.x,
+                                            uint32_t nthr = blockDim.x) {
+    if (FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_IQ3_XXS) {
+        constexpr uint32_t nB = 128u * kTabCopies / 2u, nA = 256u * kTabCopies / 2u;  // uint4 stores
+        for (uint32_t i = tid0; i < nB + nA; i += nthr) {
+            uint64_t v;
+            uint32_t off;
+            if (i < nB) {
+                const uint32_t e = i / (kTabCopies / 2u);
+                v = FMT == VL_TYPE_IQ2_XXS ? g_tables.sign_sel[e] : g_tables.iq3_sel[e];
+                off = kTabB + i * 16u;
+            } else {
+                const uint32_t k = i - nB, e = k / (kTabCopies / 2u);
+                v = FMT == VL_TYPE_IQ2_XXS ? g_tables.iq2_codes[e] : g_tables.iq3_pm[e];
+                off = kTabA + k * 16u;
+            }
+            *reinterpret_cast<uint4*>(lds + off) = make_uint4(lo32(v), hi32(v), lo32(v), hi32(v));
+        }
+    } else if (FMT == VL_TYPE_IQ1_S) {
+        for (uint32_t i = tid0; i < 2048u; i += nthr)
+            reinterpret_cast<uint64_t*>(lds)[i] = g_tables.iq1_codes[i];
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Weight chunks (one unit of one tile, this lane's share).
+// ------------------------------------------------------------------------------------------
+
+struct TileRef {
+    const uint8_t* p0;
+    const uint8_t* p1;
+    const uint8_t* p2;
+};
+
+template <uint32_t FMT>
+__device__ __forceinline__ TileRef tile_ref(const vl_tiled_layout& L, const uint8_t* w, uint32_t t) {
+    const uint64_t NB = L.superblocks, NG = L.groups;
+    TileRef r;
+    if (FMT == VL_TYPE_IQ2_XXS) {
+        r.p0 = w + t * NB * 2048u;
+        r.p1 = w + L.plane1 + t * NB * 64u;
+        r.p2 = r.p1;
+    } else if (FMT == VL_TYPE_IQ3_XXS) {
+        r.p0 = w + t * NB * 2048u;
+        r.p1 = w + L.plane1 + t * NB * 1024u;
+        r.p2 = w + L.plane2 + t * NB * 64u;
+    } else if (FMT == VL_TYPE_IQ1_S) {
+        r.p0 = w + t * NB * 1024u;
+        r.p1 = w + L.plane1 + t * NB * 512u;
+        r.p2 = w + L.plane2 + t * NB * 64u;
+    } else {
+        r.p0 = w + t * NG * 1024u;
+        r.p1 = w + L.plane1 + t * NG * 64u;
+        r.p2 = r.p1;
+    }
+    return r;
+}
+
+struct Chunk {
+    uint4 q0, q1, q2, q3;
+    uint4 a0, a1;
+    uint32_t d0, d1;
+};
+
+__device__ __forceinline__ uint4 ld_stream(const uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load(gp(reinterpret_cast<const u32x4*>(p)));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    return *gp(reinterpret_cast<const uint16_t*>(p));
+}
+
+// ng: groups per row (bounds the last Q8_0 unit).
+template <uint32_t FMT>
+__device__ __forceinline__ void load_chunk(const TileRef& tr, uint32_t c, uint32_t ng, Chunk& ch) {
+    const uint32_t lane = threadIdx.x & 63u, n = lane & 31u, hh = lane >> 5;
+    if (FMT == VL_TYPE_IQ2_XXS) {
+        const uint8_t* P = tr.p0 + (uint64_t)c * 2048u + lane * 32u;
+        ch.q0 = ld_stream(P);
+        ch.q1 = ld_stream(P + 16);
+        ch.d0 = ld_u16(tr.p1 + (uint64_t)c * 64u + n * 2u);
+    } else if (FMT == VL_TYPE_IQ3_XXS) {
+        const uint8_t* Q = tr.p0 + (uint64_t)c * 2048u + n * 16u;
+        ch.q0 = ld_stream(Q);
+        ch.q1 = ld_stream(Q + 512);
+        ch.q2 = ld_stream(Q + 1024);
+        ch.q3 = ld_stream(Q + 1536);
+        const uint8_t* A = tr.p1 + (uint64_t)c * 1024u + n * 16u;
+        ch.a0 = ld_stream(A);
+        ch.a1 = ld_stream(A + 512);
+        ch.d0 = ld_u16(tr.p2 + (uint64_t)c * 64u + n * 2u);
+    } else if (FMT == VL_TYPE_IQ1_S) {
+        const uint8_t* Q = tr.p0 + (uint64_t)c * 1024u + n * 16u;
+        ch.q0 = ld_stream(Q);
+        ch.q1 = ld_stream(Q + 512);
+        ch.q2 = ld_stream(tr.p1 + (uint64_t)c * 512u + n * 16u);
+        ch.d0 = ld_u16(tr.p2 + (uint64_t)c * 64u + n * 2u);
+    } else {
+        uint4 q[4];
+        uint32_t d[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t G = 4u * c + b;
+            if (G < ng) {
+                q[b] = ld_stream(tr.p0 + (uint64_t)G * 1024u + n * 32u + hh * 16u);
+                d[b] = ld_u16(tr.p1 + (uint64_t)G * 64u + n * 2u);
+            } else {
+                q[b] = make_uint4(0, 0, 0, 0);
+                d[b] = 0;
+            }
+        }
+        ch.q0 = q[0]; ch.q1 = q[1]; ch.q2 = q[2]; ch.q3 = q[3];
+        ch.d0 = d[0] | (d[1] << 16);
+        ch.d1 = d[2] | (d[3] << 16);
+    }
+}
+
+__device__ __forceinline__ uint32_t word(const uint4& q, int i) {
+    return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
+}
+
+// Payload words of an IQ2_XXS chunk in the order of vl_layout.h.
+__device__ __forceinline__ void iq2_words(const Chunk& ch, uint32_t (&w)[8]) {
+    w[0] = ch.q0.x; w[1] = ch.q0.y; w[2] = ch.q0.z; w[3] = ch.q0.w;
+    w[4] = ch.q1.x; w[5] = ch.q1.y; w[6] = ch.q1.z; w[7] = ch.q1.w;
+}
+
+template <uint32_t FMT>
+__device__ __forceinline__ float unit_factor() {
+    return FMT == VL_TYPE_IQ3_XXS ? 0.25f : FMT == VL_TYPE_Q8_0 ? 1.0f : 0.125f;
+}
+
+// Per-group B fragments and integer scales of one IQ chunk, in the order the MFMA loop uses
+// them. For IQ2_XXS the two halves of a row exchange their scale bytes here.
+template <uint32_t FMT>
+struct ChunkDecoder {
+    uint32_t w[8];
+    uint32_t sc_lo, sc_hi;  // IQ2_XXS: scale bytes of groups 0..3 and 4..7
+    __device__ __forceinline__ void init(const Chunk& ch) {
+        if (FMT == VL_TYPE_IQ2_XXS) {
+            iq2_words(ch, w);
+            const uint32_t own = iq2_scale_bytes(w);
+            const uint32_t other = (uint32_t)__shfl_xor((int)own, 32);
+            const bool hi_half = (threadIdx.x & 32u) != 0;
+            sc_lo = hi_half ? other : own;
+            sc_hi = hi_half ? own : other;
+        }
+    }
+    __device__ __forceinline__ i32x4 group(const Chunk& ch, int g, uint32_t lane_off, int hh,
+                                           const uint8_t* lds, int& sc) const {
+        if (FMT == VL_TYPE_IQ2_XXS) {
+            sc = odd_scale(g < 4 ? sc_lo : sc_hi, g & 3);
+            return decode_iq2_xxs(w, g, lane_off, lds);
+        } else if (FMT == VL_TYPE_IQ3_XXS) {
+            const uint4& q = g < 2 ? ch.q0 : g < 4 ? ch.q1 : g < 6 ? ch.q2 : ch.q3;
+            const uint32_t qs = word(q, 2 * (g & 1) + hh);
+            const uint32_t aux = word(g < 4 ? ch.a0 : ch.a1, g & 3);
+            sc = 2 * (int)(aux >> 28) + 1;
+            return decode_iq3_xxs(qs, aux, hh, lane_off, lds);
+        } else {  // IQ1_S
+            const uint32_t qs4 = word(g < 4 ? ch.q0 : ch.q1, g & 3);
+            const uint32_t qh = (word(ch.q2, g >> 1) >> (16 * (g & 1))) & 0xffffu;
+            sc = 2 * (int)((qh >> 12) & 7u) + 1;
+            return decode_iq1_s(qs4, qh, hh, lds);
+        }
+    }
+};
+
+// ------------------------------------------------------------------------------------------
+// A operand: where a lane reads its limb row.
+// ------------------------------------------------------------------------------------------
+
+// Token slot and limb carried by A row m (inverse of m = 8(s/2) + 4(l/2) + 2(s%2) + l%2).
+__device__ __forceinline__ uint32_t a_slot(uint32_t m) { return 2u * (m / 8u) + (m / 2u) % 2u; }
+__device__ __forceinline__ uint32_t a_limb(uint32_t m) { return 2u * ((m / 4u) % 2u) + m % 2u; }
+
+// Limb source of one lane: activation limbs are stored [group][slot][4 limbs][32 columns], so
+// consecutive groups of one (slot, limb) row are STRIDE = slots * 128 bytes apart. Lanes whose
+// token slot is unused read slot 0's row: their products land in result registers of unused
+// slots (scaled by 0) or in registers that are never read, so every lane has the same stride.
+template <bool LDS, uint32_t STRIDE>
+struct ASrc {
+    const int8_t* ptr;  // global source (LDS == false)
+    uint32_t off;       // LDS byte offset (LDS == true)
+    __device__ __forceinline__ i32x4 load(const uint8_t* lds, uint32_t G) const {
+        if (LDS) return *reinterpret_cast<const i32x4*>(lds + off + G * STRIDE);
+        return *gp(reinterpret_cast<const i32x4*>(ptr + (uint64_t)G * STRIDE));
+    }
+};
+
+// ------------------------------------------------------------------------------------------
+// Chunk processing: accf[s] += this lane's partial of (row, slot s) over the unit.
+// ------------------------------------------------------------------------------------------
+
+// df: weight factor of the lane's row for the unit (d times the format factor, times 65536 in
+// the high-limb half); fs[s]: 2^-e of slot s for the unit's exponent block.
+template <uint32_t FMT, int NT, bool LDS>
+__device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint32_t ng,
+                                              const ASrc<LDS, NT * 128u>& as, const uint8_t* lds,
+                                              float hscale, const float (&fs)[NT], float (&accf)[NT]) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const int hh = (int)(lane >> 5);
+    const uint32_t lane_off = (lane & 31u) * 8u;
+    const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    if (FMT == VL_TYPE_Q8_0) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t G = 4u * c + b;
+            if (G >= ng) break;
+            const i32x4 afr = as.load(lds, G);
+            const uint4& q = b == 0 ? ch.q0 : b == 1 ? ch.q1 : b == 2 ? ch.q2 : ch.q3;
+            i32x4 bfr;
+            bfr[0] = (int)q.x; bfr[1] = (int)q.y; bfr[2] = (int)q.z; bfr[3] = (int)q.w;
+            const i32x16 r = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr, bfr, zero16, 0, 0, 0);
+            const uint32_t dw = b < 2 ? ch.d0 : ch.d1;
+            const float d = half_bits_to_float(dw >> (16 * (b & 1))) * hscale;
+#pragma unroll
+            for (int s = 0; s < NT; ++s)
+                accf[s] += (d * fs[s]) * ((float)r[2 * s] + 256.0f * (float)r[2 * s + 1]);
+        }
+        return;
+    }
+    i32x4 afr[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) afr[g] = as.load(lds, 8u * c + g);
+    ChunkDecoder<FMT> dec;
+    dec.init(ch);
+    int acc[2 * NT];
+#pragma unroll
+    for (int i = 0; i < 2 * NT; ++i) acc[i] = 0;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        int sc;
+        const i32x4 bfr = dec.group(ch, g, lane_off, hh, lds, sc);
+        const i32x16 r = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[g], bfr, zero16, 0, 0, 0);
+        // |r| < 2^18 and sc <= 31: the 24-bit multiply is exact; the superblock sum stays
+        // below 2^27.
+#pragma unroll
+        for (int i = 0; i < 2 * NT; ++i) acc[i] += __mul24(sc, r[i]);
+    }
+    const float df = half_bits_to_float(ch.d0) * (unit_factor<FMT>() * hscale);
+#pragma unroll
+    for (int s = 0; s < NT; ++s)
+        accf[s] += (df * fs[s]) * ((float)acc[2 * s] + 256.0f * (float)acc[2 * s + 1]);
+}
+
+// Units in flight per wave, by the register size of a chunk.
+template <uint32_t FMT>
+struct StreamDepth {
+    static constexpr int kValue = FMT == VL_TYPE_IQ2_XXS ? 4 : FMT == VL_TYPE_IQ1_S ? 3 : 2;
+};
+
+// ------------------------------------------------------------------------------------------
+// Unit ranges and record handoff.
+// ------------------------------------------------------------------------------------------
+
+// Waves that take part: every one of them gets at least one unit, so the waves holding a
+// job's units are exactly the consecutive waves from the first to the last of them.
+__device__ __forceinline__ uint32_t active_waves(uint32_t nw, uint32_t total) {
+    return total < nw ? total : nw;
+}
+// Wave w of nw active waves takes units [w*total/nw, (w+1)*total/nw); waves beyond nw none.
+__device__ __forceinline__ uint32_t range_begin(uint32_t w, uint32_t nw, uint32_t total) {
+    return w < nw ? (uint32_t)((uint64_t)w * total / nw) : total;
+}
+// The wave whose range holds unit u.
+__device__ __forceinline__ uint32_t wave_of_unit(uint32_t u, uint32_t nw, uint32_t total) {
+    return (uint32_t)((((uint64_t)u + 1u) * nw - 1u) / total);
+}
+
+__device__ __forceinline__ void store_shared(float* p, float v) {
+    __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_shared(const float* p) {
+    return __hip_atomic_load(gp(const_cast<float*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void or_bits(uint32_t* p, uint32_t bits) {
+    __hip_atomic_fetch_or(gp(p), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_shared_u32(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_shared_u32(const uint32_t* p) {
+    return __hip_atomic_load(gp(const_cast<uint32_t*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Publishes this wave's record stores and counts the wave in; returns true in every lane of
+// the last wave of the job's kc contributors (which then owns the job's records and resets
+// the counter for the next launch).
+__device__ __forceinline__ bool arrive(uint32_t* counter, uint32_t kc) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's record stores have completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    uint32_t old = 0;
+    if ((threadIdx.x & 63u) == 0)
+        old = __hip_atomic_fetch_add(gp(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = (uint32_t)__shfl((int)old, 0);
+    const bool last = old == kc - 1u;
+    if (last && (threadIdx.x & 63u) == 0)
+        __hip_atomic_store(gp(counter), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return last;
+}
+
+// ------------------------------------------------------------------------------------------
+// Activations -> limbs.
+// ------------------------------------------------------------------------------------------
+
+// Four limbs (signed base-256 digits, the top one carrying the sign) of round(v * 2^e) for
+// four consecutive values, one 32-bit word per limb. Non-finite values encode as zero.
+__device__ __forceinline__ void limbs4(const float (&v)[4], int e, uint32_t (&packed)[4]) {
+    packed[0] = packed[1] = packed[2] = packed[3] = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        int X = isfinite(v[k]) ? (int)rintf(ldexpf(v[k], e)) : 0;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const int digit = l < 3 ? (int)(int8_t)(X & 0xff) : X;
+            packed[l] |= ((uint32_t)digit & 0xffu) << (8 * k);
+            X = (X - digit) >> 8;
+        }
+    }
+}
+
+// Exponent that brings m = max |v| (finite, >= 0) to just below 2^30.
+__device__ __forceinline__ int limb_exponent(float m) {
+    int q = 0;
+    frexpf(m, &q);
+    return m > 0.0f ? 30 - q : 0;
+}
+
+// One wave per token: limbs of columns [256 xb, 256 xb + 256) of token t of x ([tokens][cols],
+// token stride x_stride) into xl ([cols/32][slots][4][32]), the block's exponent into
+// xe[8 xb + t] and a non-finite flag into flags[8 xb + t] (written whatever its value).
+// cols is a multiple of 32.
+__device__ __forceinline__ void prep_x_block(const float* __restrict__ x, uint64_t x_stride,
+                                             uint32_t cols, uint32_t tokens, uint32_t slots,
+                                             uint32_t xb, int8_t* __restrict__ xl,
+                                             int* __restrict__ xe, uint32_t* __restrict__ flags) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const uint32_t col = xb * 256u + lane * 4u;
+    for (uint32_t t = wave; t < tokens; t += nwaves) {
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (col < cols) {
+            const float4 f = ld_f4(x + t * x_stride + col);
+            v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+        }
+        bool finite = true;
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            finite &= isfinite(v[k]);
+            if (isfinite(v[k])) m = fmaxf(m, fabsf(v[k]));
+        }
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const bool all_finite = __all(finite);
+        const int e = limb_exponent(m);
+        if (lane == 0) {
+            *gp(xe + 8u * xb + t) = e;
+            *gp(flags + 8u * xb + t) = all_finite ? 0u : 1u;
+        }
+        if (col < cols) {
+            uint32_t packed[4];
+            limbs4(v, e, packed);
+            const uint64_t base = ((uint64_t)(col / 32u) * slots + t) * 128u + (col % 32u);
+#pragma unroll
+            for (int l = 0; l < 4; ++l) *gp(reinterpret_cast<uint32_t*>(xl + base + 32u * l)) = packed[l];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// The wave loop.
+//
+// Policy interface (all values wave-uniform):
+//   uint32_t chunks, nmat, ng;            units per matrix row, matrices per job, groups/row
+//   TileRef tref(uint32_t j, uint32_t mat)
+//   void job_begin(uint32_t j)            prepares as, hscale for job j
+//   ASrc<LDS> as; float hscale;
+//   void scales(uint32_t j, uint32_t c, float (&fs)[NT])
+//   void flush(uint32_t j, const float (&m0)[NT], const float (&m1)[NT])
+// ------------------------------------------------------------------------------------------
+
+template <uint32_t FMT, int NT, bool LDS, typename Pol>
+__device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1, const uint8_t* lds) {
+    constexpr int D = StreamDepth<FMT>::kValue;
+    if (u0 >= u1) return;
+    const uint32_t C = pol.chunks, NM = pol.nmat, UJ = C * NM;
+    // Load head: D units ahead of the processing position. Loads are issued unconditionally
+    // (past the end of the range the head stays on the last unit, an L2 hit) so that every
+    // path through the loop has the same loads outstanding and the waits before each chunk
+    // stay partial.
+    uint32_t hj = u0 / UJ, hm = (u0 - hj * UJ) / C, hc = u0 - hj * UJ - hm * C;
+    uint32_t hu = u0;
+    TileRef htr = pol.tref(hj, hm);
+    auto head_next = [&]() {
+        if (hu + 1u >= u1) return;
+        ++hu;
+        if (++hc == C) {
+            hc = 0;
+            if (++hm == NM) {
+                hm = 0;
+                ++hj;
+            }
+            htr = pol.tref(hj, hm);
+        }
+    };
+    Chunk buf[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        load_chunk<FMT>(htr, hc, pol.ng, buf[k]);
+        head_next();
+    }
+    uint32_t pj = u0 / UJ, pm = (u0 - pj * UJ) / C, pc = u0 - pj * UJ - pm * C;
+    pol.job_begin(pj);
+    float acc[NT], keep[NT], fs[NT];
+#pragma unroll
+    for (int s = 0; s < NT; ++s) acc[s] = keep[s] = 0.0f;
+    for (uint32_t u = u0; u < u1; u += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const uint32_t uu = u + k;
+            if (uu < u1) {
+                pol.scales(pj, pc, fs);
+                process_chunk<FMT, NT, LDS>(buf[k], pc, pol.ng, pol.as, lds, pol.hscale, fs, acc);
+            }
+            load_chunk<FMT>(htr, hc, pol.ng, buf[k]);
+            head_next();
+            if (uu < u1) {
+                bool job_end = false;
+                if (++pc == C) {
+                    pc = 0;
+                    if (pm + 1 < NM) {
+#pragma unroll
+                        for (int s = 0; s < NT; ++s) {
+                            keep[s] = acc[s];
+                            acc[s] = 0.0f;
+                        }
+                        ++pm;
+                    } else {
+                        job_end = true;
+                    }
+                }
+                if (job_end || uu + 1 == u1) {
+                    if (NM == 2 && pm == 1) pol.flush(pj, keep, acc);
+                    else pol.flush(pj, acc, keep);  // keep is zero here
+#pragma unroll
+                    for (int s = 0; s < NT; ++s) acc[s] = keep[s] = 0.0f;
+                    if (job_end) {
+                        ++pj;
+                        pm = 0;
+                        if (uu + 1 < u1) pol.job_begin(pj);
+                    }
+                }
+            }
+        }
+    }
+}
+
+}  // namespace vl
+
+#endif  // VL_STREAM_H

@@ -10,6 +10,10 @@ experts touched) changes every step, and layer instances rotate so that no weigh
 cache between their uses.
 
     python bench.py [--steps K] [--warmup W] [--workload iq2_moe] [--no-cpu-baseline]
+    python bench.py --copy-calibration BYTES     plain device copies of BYTES (counter scale)
+
+roofline.traffic (HBM bytes per launch of the gate/up kernel) is read from the committed
+rocprofv3 counter summary profiles/k_moe_gateup.iq2_moe.traffic.txt when it exists.
 """
 
 from __future__ import annotations
@@ -27,6 +31,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+TRAFFIC_SUMMARY = ROOT / "profiles" / "k_moe_gateup.iq2_moe.traffic.txt"
 
 
 def parse() -> argparse.Namespace:
@@ -42,7 +47,32 @@ def parse() -> argparse.Namespace:
     p.add_argument("--profile-steps", type=int, default=100)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                   help="only run 20 device-to-device copies of BYTES (no layer)")
     return p.parse_args()
+
+
+def copy_calibration(nbytes: int) -> int:
+    """Plain device copies of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 20}))
+    return 0
+
+
+def measured_traffic() -> tuple[int | None, str | None]:
+    """HBM bytes per gate/up launch from the committed counter summary, if there is one."""
+    import re
+
+    if not TRAFFIC_SUMMARY.exists():
+        return None, None
+    m = re.search(r"traffic_bytes_per_launch = (\d+)", TRAFFIC_SUMMARY.read_text())
+    return (int(m.group(1)), str(TRAFFIC_SUMMARY.relative_to(ROOT))) if m else (None, None)
 
 
 def token_pool(wl, count: int) -> np.ndarray:
@@ -157,6 +187,8 @@ def main() -> int:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this path "
               "(no multi-GPU sharding or collectives are built)", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
     import torch
 
     from vastloom_amd import ops
@@ -216,6 +248,7 @@ def main() -> int:
     gateup_bytes = n_exp * 2 * storage_bytes(wl.gate_type, F, H)
     gateup_gbs = gateup_bytes / (stage_us["gate_up"] * 1e-6) / 1e9
     down_gbs = n_exp * storage_bytes(wl.down_type, H, F) / (stage_us["down"] * 1e-6) / 1e9
+    traffic, traffic_src = measured_traffic() if wl.name == "iq2_moe" else (None, None)
 
     result = {
         "metric": "quant expert FFN effective HBM GB/s (% of peak) + us per MoE layer, 1 GPU",
@@ -243,8 +276,10 @@ def main() -> int:
         "stages_us": stage_us,
         "roofline": {"bound": "hbm", "kernel": "k_moe_gateup", "achieved": round(gateup_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gateup_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gateup_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "bytes_per_launch": gateup_bytes,
+                     "kernel_avg_us": stage_us["gate_up"],
                      "down_kernel_achieved": round(down_gbs, 1)},
         "cpu_baseline": None,
     }

@@ -19,8 +19,11 @@
 // lanes of a half-wave then touch 32 different bank pairs whatever entries they look up, which
 // removes the bank conflicts of random lookups. The table address of entry e for a lane is
 // (e << 8) | lane_off with lane_off = (l % 32) * 8, formed by one v_perm_b32 when e is a byte
-// of a payload word and by a shift and a v_and_or_b32 otherwise. The tables start at LDS byte 0,
-// so the table bases fold into the DS instructions' immediate offsets.
+// of a payload word and by a shift and a v_and_or_b32 otherwise.
+//
+// LDS is addressed by plain byte addresses: the kernels that use these tables declare no static
+// LDS (the launch code checks), so their dynamic LDS starts at address 0, the tables sit at its
+// start, and the table bases fold into the DS instructions' immediate offsets.
 #ifndef VL_DECODE_H
 #define VL_DECODE_H
 
@@ -53,9 +56,14 @@ __device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t width
     return __builtin_amdgcn_ubfe(v, off, width);
 }
 
-__device__ __forceinline__ uint64_t lds_u64(const uint8_t* lds, uint32_t addr) {
-    return *reinterpret_cast<const uint64_t*>(lds + addr);
+#define VL_LDS __attribute__((address_space(3)))
+
+// Load of type T from LDS byte address addr.
+template <typename T>
+__device__ __forceinline__ T lds_load(uint32_t addr) {
+    return *reinterpret_cast<const VL_LDS T*>((uintptr_t)addr);
 }
+__device__ __forceinline__ uint64_t lds_u64(uint32_t addr) { return lds_load<uint64_t>(addr); }
 
 // (byte k of v) << 8 | lane_off, one v_perm_b32.
 __device__ __forceinline__ uint32_t byte_entry(uint32_t v, int k, uint32_t lane_off) {
@@ -64,8 +72,7 @@ __device__ __forceinline__ uint32_t byte_entry(uint32_t v, int k, uint32_t lane_
 
 // IQ2_XXS group g of a superblock half (vl_layout.h): grid bytes in w[0..3], sign fields in
 // w[4..7]. Codes select from the palette {8, 25, 43, -8, -25, -43}.
-__device__ __forceinline__ i32x4 decode_iq2_xxs(const uint32_t (&w)[8], int g, uint32_t lane_off,
-                                                const uint8_t* lds) {
+__device__ __forceinline__ i32x4 decode_iq2_xxs(const uint32_t (&w)[8], int g, uint32_t lane_off) {
     const int q = g >> 1, odd = g & 1;
     const uint32_t gw = w[q], sw = w[4 + q];
     const uint32_t a0 = byte_entry(gw, 2 * odd, lane_off);
@@ -73,8 +80,8 @@ __device__ __forceinline__ i32x4 decode_iq2_xxs(const uint32_t (&w)[8], int g, u
     // Sign fields at bits 14*odd and 14*odd + 7, moved to bits 8..14: one shift, one and-or.
     const uint32_t b0 = ((odd ? sw >> 6 : sw << 8) & 0x7f00u) | lane_off;
     const uint32_t b1 = ((odd ? sw >> 13 : sw << 1) & 0x7f00u) | lane_off;
-    const uint64_t s0 = lds_u64(lds, kTabA + a0) | lds_u64(lds, kTabB + b0);
-    const uint64_t s1 = lds_u64(lds, kTabA + a1) | lds_u64(lds, kTabB + b1);
+    const uint64_t s0 = lds_u64(kTabA + a0) | lds_u64(kTabB + b0);
+    const uint64_t s1 = lds_u64(kTabA + a1) | lds_u64(kTabB + b1);
     i32x4 f;
     f[0] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, lo32(s0));
     f[1] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, hi32(s0));
@@ -90,23 +97,22 @@ __device__ __forceinline__ uint32_t iq2_scale_bytes(const uint32_t (&w)[8]) {
     return perm(w[5], w[4], 0x0c0c0703u) | perm(w[7], w[6], 0x07030c0cu);
 }
 
-// 2s+1 from a scale byte (nibble in bits 4..7): (byte >> 3) | 1.
-__device__ __forceinline__ int odd_scale(uint32_t bytes, int k) {
-    return (int)(bfe(bytes, 8u * (uint32_t)k + 3u, 5) | 1u);
+// 2s+1 of four scale bytes (nibbles in bits 4..7), one per byte: (byte >> 3) | 1 bytewise.
+__device__ __forceinline__ uint32_t odd_scales4(uint32_t bytes) {
+    return ((bytes >> 3) & 0x1e1e1e1eu) | 0x01010101u;
 }
 
 // IQ3_XXS group: q = the lane's four grid bytes (two per sub-block), aux = the group's sign and
 // scale word. Magnitude entries hold the four positive values in the low word and their
 // negations in the high word; sign entries select per lane.
-__device__ __forceinline__ i32x4 decode_iq3_xxs(uint32_t q, uint32_t aux, int hh,
-                                                uint32_t lane_off, const uint8_t* lds) {
+__device__ __forceinline__ i32x4 decode_iq3_xxs(uint32_t q, uint32_t aux, int hh, uint32_t lane_off) {
     const uint32_t a = aux >> (14 * hh);
-    const uint64_t sel0 = lds_u64(lds, kTabB + (((a << 8) & 0x7f00u) | lane_off));
-    const uint64_t sel1 = lds_u64(lds, kTabB + (((a << 1) & 0x7f00u) | lane_off));
-    const uint64_t g00 = lds_u64(lds, kTabA + byte_entry(q, 0, lane_off));
-    const uint64_t g01 = lds_u64(lds, kTabA + byte_entry(q, 1, lane_off));
-    const uint64_t g10 = lds_u64(lds, kTabA + byte_entry(q, 2, lane_off));
-    const uint64_t g11 = lds_u64(lds, kTabA + byte_entry(q, 3, lane_off));
+    const uint64_t sel0 = lds_u64(kTabB + (((a << 8) & 0x7f00u) | lane_off));
+    const uint64_t sel1 = lds_u64(kTabB + (((a << 1) & 0x7f00u) | lane_off));
+    const uint64_t g00 = lds_u64(kTabA + byte_entry(q, 0, lane_off));
+    const uint64_t g01 = lds_u64(kTabA + byte_entry(q, 1, lane_off));
+    const uint64_t g10 = lds_u64(kTabA + byte_entry(q, 2, lane_off));
+    const uint64_t g11 = lds_u64(kTabA + byte_entry(q, 3, lane_off));
     i32x4 f;
     f[0] = (int)perm(hi32(g00), lo32(g00), lo32(sel0));
     f[1] = (int)perm(hi32(g01), lo32(g01), hi32(sel0));
@@ -117,15 +123,13 @@ __device__ __forceinline__ i32x4 decode_iq3_xxs(uint32_t q, uint32_t aux, int hh
 
 // IQ1_S group: qs4 = low 8 bits of the four 11-bit grid indices, qh = the group's 16-bit word
 // (3 high index bits per sub-block, 3-bit scale at bit 12, delta sign at bit 15).
-__device__ __forceinline__ i32x4 decode_iq1_s(uint32_t qs4, uint32_t qh, int hh,
-                                              const uint8_t* lds) {
-    const uint64_t* codes = reinterpret_cast<const uint64_t*>(lds);
+__device__ __forceinline__ i32x4 decode_iq1_s(uint32_t qs4, uint32_t qh, int hh) {
     const int s0 = 2 * hh;
     const uint32_t i0 = ((qs4 >> (8 * s0)) & 0xffu) | (((qh >> (3 * s0)) & 7u) << 8);
     const uint32_t i1 = ((qs4 >> (8 * s0 + 8)) & 0xffu) | (((qh >> (3 * s0 + 3)) & 7u) << 8);
     const uint64_t dm = (qh & 0x8000u) ? 0x0404040404040404ull : 0ull;
-    const uint64_t c0 = codes[i0] | dm;
-    const uint64_t c1 = codes[i1] | dm;
+    const uint64_t c0 = lds_u64(i0 * 8u) | dm;
+    const uint64_t c1 = lds_u64(i1 * 8u) | dm;
     i32x4 f;
     f[0] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, lo32(c0));
     f[1] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, hi32(c0));

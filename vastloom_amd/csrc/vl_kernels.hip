@@ -36,7 +36,13 @@ hipError_t ensure_dynamic_lds(const void* kernel, uint32_t bytes) {
     static thread_local uint32_t n = 0;
     for (uint32_t i = 0; i < n; ++i)
         if (done[i] == kernel && limit[i] >= bytes) return hipSuccess;
-    const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    // The kernels address their dynamic LDS from LDS address 0 (vl_decode.h), which holds only
+    // when they declare no static LDS.
+    hipFuncAttributes attr{};
+    hipError_t e = hipFuncGetAttributes(&attr, kernel);
+    if (e != hipSuccess) return e;
+    if (attr.sharedSizeBytes != 0) return hipErrorInvalidKernelFile;
+    e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
     if (e != hipSuccess) return e;
     if (n < 128) {
         done[n] = kernel;
@@ -178,7 +184,7 @@ __global__ void __launch_bounds__(256) k_dequant(vl_tiled_layout L, const uint8_
     const uint32_t lane_off = n * 8u;
     for (int g = 0; g < 8; ++g) {
         int sc = 1;
-        const i32x4 frag = dec.group(ch, g, lane_off, hh, lds, sc);
+        const i32x4 frag = dec.group(ch, g, lane_off, hh, sc);
         float* dst = out + (uint64_t)row * L.cols + (uint64_t)c * 256u + 32u * g + 16u * hh;
         for (int e = 0; e < 16; ++e) {
             const int q = (int)(int8_t)((uint32_t)frag[e >> 2] >> (8 * (e & 3)));
@@ -280,9 +286,8 @@ struct Matvec {
 
     __device__ void scales(uint32_t, uint32_t c, float (&fs)[NT]) const {
         const uint32_t eb = FMT == VL_TYPE_Q8_0 ? c / 2u : c;
-        const float* sc = reinterpret_cast<const float*>(lds + scale_off) + 8u * eb;
 #pragma unroll
-        for (int s = 0; s < NT; ++s) fs[s] = sc[s];
+        for (int s = 0; s < NT; ++s) fs[s] = lds_load<float>(scale_off + 4u * (8u * eb + s));
     }
 
     __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&)[NT]) const {
@@ -301,14 +306,11 @@ struct Matvec {
         for (int i = 0; i < (NT + 1) / 2; ++i) {
             const uint32_t sl = 2u * i + hh;
             if (sl < tokens) {
-                float v = 0.0f;
-                for (uint32_t k = first; k <= last; ++k) {
-                    const float* rr = rec + (uint64_t)(k + j) * (NT * 64u) + sl * 64u;
-                    v += load_shared(rr + n) + load_shared(rr + 32u + n);
-                }
+                float v[1];
+                sum_records<NT, 1>(rec, NT * 64u, j, first, last, sl, n, v);
                 if (row < L.rows) {
-                    bad |= !isfinite(v);
-                    *gp(y + (uint64_t)sl * L.rows + row) = v;
+                    bad |= !isfinite(v[0]);
+                    *gp(y + (uint64_t)sl * L.rows + row) = v[0];
                 }
             }
         }
@@ -325,27 +327,27 @@ __global__ void __launch_bounds__(kStreamThreads) k_matvec(vl_tiled_layout L, co
     fill_tables<FMT>(lds);
     constexpr uint32_t TB = table_bytes<FMT>();
     const uint32_t stage_bytes = LDS ? (L.cols / 32u) * NT * 128u : 0u;
-    const uint32_t scale_off = TB + stage_bytes;
+    const uint32_t scale_off = TB + stage_bytes;  // then m.xblocks * 8 scales and the wave flags
     if (LDS) {
         const uint4* src = reinterpret_cast<const uint4*>(ws + m.off_xlimbs);
         uint4* dst = reinterpret_cast<uint4*>(lds + TB);
         for (uint32_t i = threadIdx.x; i < stage_bytes / 16u; i += blockDim.x) dst[i] = ld_u4(src + i);
     }
+    int nonfinite = 0;
     {
         const int* xe = reinterpret_cast<const int*>(ws + m.off_xexp);
-        float* sc = reinterpret_cast<float*>(lds + scale_off);
-        for (uint32_t i = threadIdx.x; i < m.xblocks * 8u; i += blockDim.x)
-            sc[i] = (i & 7u) < tokens ? __builtin_amdgcn_ldexpf(1.0f, -*gp(xe + i)) : 0.0f;
-    }
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
         const uint32_t* xf = reinterpret_cast<const uint32_t*>(ws + m.off_xflags);
-        uint32_t bits = 0;
-        for (uint32_t xb = 0; xb < m.xblocks; ++xb)
-            for (uint32_t t = 0; t < tokens; ++t)
-                if (xf[8u * xb + t]) bits = kStatusNonFiniteInput;
-        if (bits) or_bits(reinterpret_cast<uint32_t*>(ws), bits);
+        float* sc = reinterpret_cast<float*>(lds + scale_off);
+        for (uint32_t i = threadIdx.x; i < m.xblocks * 8u; i += blockDim.x) {
+            const bool live = (i & 7u) < tokens;
+            sc[i] = live ? __builtin_amdgcn_ldexpf(1.0f, -*gp(xe + i)) : 0.0f;
+            if (live && *gp(xf + i)) nonfinite = 1;
+        }
     }
-    __syncthreads();
+    const bool any_nonfinite =
+        block_any(nonfinite != 0, reinterpret_cast<uint32_t*>(lds + scale_off + m.xblocks * 32u));
+    if (blockIdx.x == 0 && threadIdx.x == 0 && any_nonfinite)
+        or_bits(reinterpret_cast<uint32_t*>(ws), kStatusNonFiniteInput);
     Matvec<FMT, NT, LDS> pol;
     pol.L = L;
     pol.W = W;
@@ -365,7 +367,7 @@ __global__ void __launch_bounds__(kStreamThreads) k_matvec(vl_tiled_layout L, co
     pol.y = y;
     pol.hscale = (threadIdx.x & 32u) ? 65536.0f : 1.0f;
     stream_range<FMT, NT, LDS>(pol, range_begin(pol.wid, pol.NW, pol.TU),
-                               range_begin(pol.wid + 1u, pol.NW, pol.TU), lds);
+                               range_begin(pol.wid + 1u, pol.NW, pol.TU));
 }
 
 // Dynamic LDS of one workgroup on gfx950 (the matvec kernel has no static LDS).
@@ -377,7 +379,7 @@ static hipError_t launch_matvec_nt(const vl_tiled_layout& L, const uint8_t* w, u
                                    hipStream_t st) {
     const uint32_t stage = (L.cols / 32u) * NT * 128u;
     const uint32_t TB = table_bytes<FMT>();
-    const uint32_t base = TB + m.xblocks * 8u * 4u;
+    const uint32_t base = TB + m.xblocks * 8u * 4u + kStreamWaves * 4u;  // tables, scales, flags
     if (base + stage <= kMatvecLdsBudget) {
         const uint32_t shm = base + stage;
         const hipError_t e = ensure_dynamic_lds((const void*)k_matvec<FMT, NT, true>, shm);

@@ -429,9 +429,10 @@ __device__ __forceinline__ void route_token_wave(const MoeShape& s, const MoeInp
 
 // After route_token_wave for every token (and a barrier), the whole block builds the active-expert
 // list: distinct experts in ascending id, each with its tokens in ascending order, and every
-// token's combine order. publish also writes them (and the routes) to the workspace.
+// token's combine order. publish also writes them (and the routes) to the workspace, and raises
+// the status bits of refused routes and of non-finite activations (x_nonfinite).
 __device__ __forceinline__ void build_active(const MoeShape& s, const MoeWorkspace& w, bool publish,
-                                            RouteLds& rt) {
+                                            bool x_nonfinite, RouteLds& rt) {
     const uint32_t K = s.top_k, E = s.experts, P = s.tokens * K;
     const uint32_t p = threadIdx.x;
     if (p < P) {
@@ -498,11 +499,7 @@ __device__ __forceinline__ void build_active(const MoeShape& s, const MoeWorkspa
         if (publish) {
             MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
             *gp(&hdr->n_active) = rt.n_active;
-            uint32_t bits = bad ? kStatusBadRoute : 0u;
-            const uint32_t* xf = ws_ptr<uint32_t>(w, w.off_xflags);
-            for (uint32_t xb = 0; xb < w.xblocks; ++xb)
-                for (uint32_t t = 0; t < s.tokens; ++t)
-                    if (*gp(xf + 8u * xb + t)) bits |= kStatusNonFiniteInput;
+            const uint32_t bits = (bad ? kStatusBadRoute : 0u) | (x_nonfinite ? kStatusNonFiniteInput : 0u);
             if (bits) or_bits(&hdr->status, bits);
         }
     }
@@ -552,40 +549,24 @@ __device__ __forceinline__ float swiglu(uint32_t sem, float g, float u, float li
 // Stream policies.
 // ------------------------------------------------------------------------------------------
 
-// Sum of a job's records for (matrix mat, slot s, row n): records first..last in order, each
-// record's two lane halves in order.
-template <int NT>
-__device__ __forceinline__ float sum_records(const float* rec, uint32_t rec_floats, uint32_t j,
-                                             uint32_t first, uint32_t last, uint32_t mat,
-                                             uint32_t s, uint32_t n) {
-    float v = 0.0f;
-    for (uint32_t k = first; k <= last; ++k) {
-        const float* r = rec + (uint64_t)(k + j) * rec_floats + (mat * NT + s) * 64u;
-        v += load_shared(r + n) + load_shared(r + 32u + n);
-    }
-    return v;
-}
-
 // Tile epilogues run out of line: they are rare, and inlined into the streaming loop their
-// float64 code would compete with the in-flight weight buffers for registers.
+// float64 code would compete with the in-flight weight buffers for registers. Their arguments are
+// plain scalars (a structure argument would be passed through scratch memory).
 
-// Last wave of gate/up tile job j: gate/up sums, SwiGLU, the tile's h rows, and the maxima of |h|
-// per 256-row block and slot (the down kernel's limb exponents).
-struct GateUpFixup {
-    const float* rec;  // gate/up records
-    float* h;          // [A][NT][inter]
-    uint32_t* hmax;    // [A][hblocks][8]
-    uint32_t* status;
-    uint32_t j, first, last, tiles, hblocks, inter, semantics;
-    ActiveExpert ae;   // the tile's expert
-};
-
+// Last wave of gate/up tile job j: gate/up sums, SwiGLU, the tile's h rows ([A][NT][inter]), and
+// the maxima of |h| per 256-row block and slot (hmax [A][hblocks][8], the down kernel's limb
+// exponents). The active-expert list is the RouteLds at LDS byte route_off.
 template <int NT>
-__device__ __attribute__((noinline)) void gateup_fixup(GateUpFixup f) {
-    const uint32_t a = f.j / f.tiles, t = f.j - a * f.tiles;
-    const ActiveExpert& ae = f.ae;
+__device__ __attribute__((noinline)) void gateup_fixup(const float* rec, float* hout, uint32_t* hmax,
+                                                       uint32_t* status, uint32_t j, uint32_t first,
+                                                       uint32_t last, uint32_t tiles, uint32_t hblocks,
+                                                       uint32_t inter, uint32_t semantics,
+                                                       uint32_t route_off) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t a = j / tiles, t = j - a * tiles;
+    const ActiveExpert& ae = reinterpret_cast<const RouteLds*>(lds + route_off)->act[a];
     const uint32_t lane = threadIdx.x & 63u, n = lane & 31u, hh = lane >> 5;
-    const uint32_t row = t * 32u + n, sb = t / 8u, F = f.inter;
+    const uint32_t row = t * 32u + n, sb = t / 8u, F = inter;
     const uint32_t nt = uni(ae.ntok);
     bool bad = false;
 #pragma unroll
@@ -593,21 +574,21 @@ __device__ __attribute__((noinline)) void gateup_fixup(GateUpFixup f) {
         const uint32_t sl = 2u * i + hh;
         float hmag = 0.0f;
         if (sl < nt) {
-            const float g = sum_records<NT>(f.rec, 2u * NT * 64u, f.j, f.first, f.last, 0, sl, n);
-            const float u = sum_records<NT>(f.rec, 2u * NT * 64u, f.j, f.first, f.last, 1, sl, n);
+            float gu[2];
+            sum_records<NT, 2>(rec, 2u * NT * 64u, j, first, last, sl, n, gu);
             if (row < F) {
-                const float h = swiglu(f.semantics, g, u, ae.limit, ae.apply_w != 0, ae.route_w[sl]);
-                bad |= !isfinite(g) || !isfinite(u) || !isfinite(h);
-                *gp(f.h + ((uint64_t)a * NT + sl) * F + row) = h;
+                const float h = swiglu(semantics, gu[0], gu[1], ae.limit, ae.apply_w != 0, ae.route_w[sl]);
+                bad |= !isfinite(gu[0]) || !isfinite(gu[1]) || !isfinite(h);
+                *gp(hout + ((uint64_t)a * NT + sl) * F + row) = h;
                 hmag = isfinite(h) ? fabsf(h) : 0.0f;
             }
         }
         for (int o = 16; o > 0; o >>= 1) hmag = fmaxf(hmag, __shfl_xor(hmag, o));
         if (n == 0 && sl < nt)
-            __hip_atomic_fetch_max(gp(f.hmax + ((uint64_t)a * f.hblocks + sb) * 8u + sl),
+            __hip_atomic_fetch_max(gp(hmax + ((uint64_t)a * hblocks + sb) * 8u + sl),
                                    __float_as_uint(hmag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (__any(bad) && lane == 0) or_bits(f.status, kStatusNonFiniteOutput);
+    if (__any(bad) && lane == 0) or_bits(status, kStatusNonFiniteOutput);
 }
 
 // Gate and up projections: job j = (active expert a, tile t) = (j / tiles, j % tiles), two
@@ -624,7 +605,7 @@ struct GateUp {
     MoeWorkspace w;
     vl_tiled_layout L;
     uint32_t tiles, UJ, TU, NW, wid;
-    uint32_t stage_off, scale_off;
+    uint32_t stage_off, scale_off, route_off;
     const uint8_t* lds;
     const RouteLds* rt;
     const uint8_t* const* wptr;  // [a][2] gate, up
@@ -652,9 +633,9 @@ struct GateUp {
 
     __device__ void scales(uint32_t, uint32_t c, float (&fs)[NT]) const {
         const uint32_t eb = FMT == VL_TYPE_Q8_0 ? c / 2u : c;
-        const float* sc = reinterpret_cast<const float*>(lds + scale_off) + 8u * eb;
 #pragma unroll
-        for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? sc[tok[s2]] : 0.0f;
+        for (int s2 = 0; s2 < NT; ++s2)
+            fs[s2] = (uint32_t)s2 < ntok ? lds_load<float>(scale_off + 4u * (8u * eb + tok[s2])) : 0.0f;
     }
 
     __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&m1)[NT]) const {
@@ -671,34 +652,25 @@ struct GateUp {
         const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
         const MoeCounters cn = counters_of(w);
         if (!arrive(cn.gu + j, last - first + 1u)) return;
-        GateUpFixup f;
-        f.ae = rt->act[j / tiles];
-        f.rec = rec;
-        f.h = ws_ptr<float>(w, w.off_h);
-        f.hmax = cn.hmax;
-        f.status = &ws_ptr<MoeHeader>(w, w.off_header)->status;
-        f.j = j;
-        f.first = first;
-        f.last = last;
-        f.tiles = tiles;
-        f.hblocks = w.hblocks;
-        f.inter = s.inter;
-        f.semantics = s.semantics;
-        gateup_fixup<NT>(f);
+        gateup_fixup<NT>(rec, ws_ptr<float>(w, w.off_h), cn.hmax,
+                         &ws_ptr<MoeHeader>(w, w.off_header)->status, j, first, last, tiles,
+                         w.hblocks, s.inter, s.semantics, route_off);
     }
 };
 
 // Dynamic LDS of the gate/up kernel, from byte 0: decode tables, staged activation limbs (LDS
-// path), the 2^-e scales of the activation blocks, the routing state and the weight pointers.
+// path), the 2^-e scales of the activation blocks, per-wave flags, the routing state and the
+// weight pointers.
 struct GateUpLds {
-    uint32_t stage, scale, route, wptr, bytes;
+    uint32_t stage, scale, flags, route, wptr, bytes;
 };
 __host__ __device__ inline GateUpLds gateup_lds(uint32_t table_bytes, uint32_t stage_bytes,
                                                 uint32_t xblocks) {
     GateUpLds l;
     l.stage = table_bytes;
     l.scale = l.stage + stage_bytes;
-    l.route = (l.scale + xblocks * 8u * 4u + 15u) & ~15u;
+    l.flags = l.scale + xblocks * 8u * 4u;
+    l.route = (l.flags + kStreamWaves * 4u + 15u) & ~15u;
     l.wptr = (l.route + (uint32_t)sizeof(RouteLds) + 15u) & ~15u;
     l.bytes = l.wptr + kMaxActive * 2u * 8u;
     return l;
@@ -714,6 +686,7 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_gateup(const MoeShape s,
     RouteLds& rt = *reinterpret_cast<RouteLds*>(lds + lay.route);
     const uint8_t** wptr = reinterpret_cast<const uint8_t**>(lds + lay.wptr);
     const uint32_t wave = threadIdx.x >> 6;
+    int nonfinite = 0;
     if (wave < s.tokens) {
         // Waves 0..tokens-1 route; the others fill the decode tables and stage the activations.
         route_token_wave(s, in, w, wave, rt);
@@ -726,12 +699,16 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_gateup(const MoeShape s,
             for (uint32_t i = tid; i < stage_bytes / 16u; i += nthr) dst[i] = ld_u4(src + i);
         }
         const int* xe = ws_ptr<const int>(w, w.off_xexp);
+        const uint32_t* xf = ws_ptr<const uint32_t>(w, w.off_xflags);
         float* sc = reinterpret_cast<float*>(lds + lay.scale);
-        for (uint32_t i = tid; i < w.xblocks * 8u; i += nthr)
-            sc[i] = (i & 7u) < s.tokens ? __builtin_amdgcn_ldexpf(1.0f, -*gp(xe + i)) : 0.0f;
+        for (uint32_t i = tid; i < w.xblocks * 8u; i += nthr) {
+            const bool live = (i & 7u) < s.tokens;
+            sc[i] = live ? __builtin_amdgcn_ldexpf(1.0f, -*gp(xe + i)) : 0.0f;
+            if (live && *gp(xf + i)) nonfinite = 1;
+        }
     }
-    __syncthreads();
-    build_active(s, w, blockIdx.x == 0, rt);
+    const bool any_nonfinite = block_any(nonfinite != 0, reinterpret_cast<uint32_t*>(lds + lay.flags));
+    build_active(s, w, blockIdx.x == 0, any_nonfinite, rt);
     for (uint32_t i = threadIdx.x; i < 2u * rt.n_active; i += blockDim.x) {
         const MoeExpert& ex = in.experts[rt.act[i / 2u].expert];
         wptr[i] = (i % 2u) ? ex.up : ex.gate;
@@ -752,60 +729,71 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_gateup(const MoeShape s,
     pol.wid = blockIdx.x * kStreamWaves + uni(threadIdx.x >> 6);
     pol.stage_off = lay.stage;
     pol.scale_off = lay.scale;
+    pol.route_off = lay.route;
     pol.lds = lds;
     pol.rt = &rt;
     pol.wptr = wptr;
     pol.hscale = (threadIdx.x & 32u) ? 65536.0f : 1.0f;
     pol.ntok = 0;
     stream_range<FMT, NT, LDS>(pol, range_begin(pol.wid, pol.NW, pol.TU),
-                               range_begin(pol.wid + 1u, pol.NW, pol.TU), lds);
+                               range_begin(pol.wid + 1u, pol.NW, pol.TU));
 }
 
-// Last wave of down job j: the expert's output rows of tile t; the last expert of tile t then
-// combines the layer output rows in each token's combine order.
-struct DownFixup {
-    const float* rec;  // down records
-    float* ypart;      // [A][NT][width]
-    float* out;        // [tokens][width]
-    const CombineEntry* comb;
-    uint32_t* tile_cnt;
-    uint32_t* status;
-    uint32_t j, first, last, tiles, n_active, width, tokens, top_k, has_shared, semantics, ntok;
-};
-
+// Last wave of down job j: the expert's output rows of tile t (ypart [A][NT][width]); the last
+// expert of tile t then combines the layer output rows in each token's combine order (the
+// CombineEntry table [tokens][top_k + 1] at LDS byte comb_off).
 template <int NT>
-__device__ __attribute__((noinline)) void down_fixup(DownFixup f) {
-    const uint32_t a = f.j / f.tiles, t = f.j - a * f.tiles;
+__device__ __attribute__((noinline)) void down_fixup(const float* rec, float* ypart, float* out,
+                                                     uint32_t* tile_cnt, uint32_t* status, uint32_t j,
+                                                     uint32_t first, uint32_t last, uint32_t tiles,
+                                                     uint32_t n_active, uint32_t width, uint32_t tokens,
+                                                     uint32_t top_k, uint32_t has_shared,
+                                                     uint32_t semantics, uint32_t ntok,
+                                                     uint32_t comb_off) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t a = j / tiles, t = j - a * tiles;
     const uint32_t lane = threadIdx.x & 63u, n = lane & 31u, hh = lane >> 5;
-    const uint32_t row = t * 32u + n, H = f.width;
-    const uint32_t nt = f.ntok;
+    const uint32_t row = t * 32u + n, H = width;
 #pragma unroll
     for (int i = 0; i < (NT + 1) / 2; ++i) {
         const uint32_t sl = 2u * i + hh;
-        if (sl < nt) {
-            const float y = sum_records<NT>(f.rec, NT * 64u, f.j, f.first, f.last, 0, sl, n);
-            if (row < H) store_shared(f.ypart + ((uint64_t)a * NT + sl) * H + row, y);
+        if (sl < ntok) {
+            float y[1];
+            sum_records<NT, 1>(rec, NT * 64u, j, first, last, sl, n, y);
+            if (row < H) store_shared(ypart + ((uint64_t)a * NT + sl) * H + row, y[0]);
         }
     }
-    if (!arrive(f.tile_cnt + t, f.n_active)) return;
-    const uint32_t K = f.top_k, nent = K + (f.has_shared ? 1u : 0u);
+    if (!arrive(tile_cnt + t, n_active)) return;
+    const CombineEntry* comb = reinterpret_cast<const CombineEntry*>(lds + comb_off);
+    const uint32_t K = top_k, nent = K + (has_shared ? 1u : 0u);
+    constexpr uint32_t kMaxEnt = kMoeMaxTopK + 1u;
     bool bad = false;
-    for (uint32_t idx = lane; idx < f.tokens * 32u; idx += 64u) {
+    for (uint32_t idx = lane; idx < tokens * 32u; idx += 64u) {
         const uint32_t tk = idx / 32u, r = t * 32u + idx % 32u;
         if (r >= H) continue;
+        // All of the row's expert outputs are loaded before the first is added.
+        float y[kMaxEnt];
+#pragma unroll
+        for (uint32_t k = 0; k < kMaxEnt; ++k) {
+            y[k] = 0.0f;
+            if (k < nent) {
+                const uint32_t src = comb[tk * (K + 1u) + k].src;
+                y[k] = load_shared(ypart + ((uint64_t)(src >> 3) * NT + (src & 7u)) * H + r);
+            }
+        }
         float acc = 0.0f;
-        for (uint32_t k = 0; k < nent; ++k) {
-            const uint32_t* ce = reinterpret_cast<const uint32_t*>(f.comb + tk * (K + 1u) + k);
-            const uint32_t src = *gp(ce);
-            const float wt = __uint_as_float(*gp(ce + 1));
-            const float y = load_shared(f.ypart + ((uint64_t)(src >> 3) * NT + (src & 7u)) * H + r);
-            acc = (f.semantics == kSemQwen && k < K) ? __fadd_rn(acc, __fmul_rn(y, wt))
-                                                    : __fadd_rn(acc, y);
+#pragma unroll
+        for (uint32_t k = 0; k < kMaxEnt; ++k) {
+            if (k < nent) {
+                const float wt = comb[tk * (K + 1u) + k].w;
+                acc = (semantics == kSemQwen && k < K) ? __fadd_rn(acc, __fmul_rn(y[k], wt))
+                                                       : __fadd_rn(acc, y[k]);
+            }
         }
         bad |= !isfinite(acc);
-        *gp(f.out + (uint64_t)tk * H + r) = acc;
+        *gp(out + (uint64_t)tk * H + r) = acc;
     }
-    if (__any(bad) && lane == 0) or_bits(f.status, kStatusNonFiniteOutput);
+    if (__any(bad) && lane == 0) or_bits(status, kStatusNonFiniteOutput);
 }
 
 // Down projection: job j = (active expert a, tile t of the output rows). The block turns the h of
@@ -822,7 +810,7 @@ struct Down {
     uint32_t n_active;
     vl_tiled_layout L;
     uint32_t tiles, UJ, TU, NW, wid;
-    uint32_t a0, expert_bytes, stage_off, scale_off;
+    uint32_t a0, expert_bytes, stage_off, scale_off, comb_off;
     const int8_t* slab;
     const uint8_t* lds;
     const ActiveExpert* act;
@@ -846,9 +834,9 @@ struct Down {
 
     __device__ void scales(uint32_t, uint32_t c, float (&fs)[NT]) const {
         const uint32_t eb = FMT == VL_TYPE_Q8_0 ? c / 2u : c;
-        const float* sc = reinterpret_cast<const float*>(lds + scale_off) + ((cur_a - a0) * w.hblocks + eb) * 8u;
+        const uint32_t sc = scale_off + 32u * ((cur_a - a0) * w.hblocks + eb);
 #pragma unroll
-        for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? sc[s2] : 0.0f;
+        for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? lds_load<float>(sc + 4u * s2) : 0.0f;
     }
 
     __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&)[NT]) const {
@@ -862,25 +850,10 @@ struct Down {
         const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
         const MoeCounters cn = counters_of(w);
         if (!arrive(cn.dn + j, last - first + 1u)) return;
-        DownFixup f;
-        f.rec = rec;
-        f.ypart = ws_ptr<float>(w, w.off_ypart);
-        f.out = in.out;
-        f.comb = ws_ptr<const CombineEntry>(w, w.off_combine);
-        f.tile_cnt = cn.tile;
-        f.status = &ws_ptr<MoeHeader>(w, w.off_header)->status;
-        f.j = j;
-        f.first = first;
-        f.last = last;
-        f.tiles = tiles;
-        f.n_active = n_active;
-        f.width = s.width;
-        f.tokens = s.tokens;
-        f.top_k = s.top_k;
-        f.has_shared = s.has_shared;
-        f.semantics = s.semantics;
-        f.ntok = uni(act[j / tiles].ntok);
-        down_fixup<NT>(f);
+        down_fixup<NT>(rec, ws_ptr<float>(w, w.off_ypart), in.out, cn.tile,
+                       &ws_ptr<MoeHeader>(w, w.off_header)->status, j, first, last, tiles, n_active,
+                       s.width, s.tokens, s.top_k, s.has_shared, s.semantics,
+                       uni(act[j / tiles].ntok), comb_off);
     }
 };
 
@@ -916,9 +889,10 @@ __device__ __forceinline__ void convert_h(const MoeWorkspace& w, uint32_t inter,
 }
 
 // Dynamic LDS of the down kernel, from byte 0: decode tables, staged h limbs (LDS path), the 2^-e
-// scales of the staged experts' h blocks, the active list and the down weight pointers.
+// scales of the staged experts' h blocks, the active list, the down weight pointers and the
+// combine table.
 struct DownLds {
-    uint32_t stage, scale, act, wptr, bytes;
+    uint32_t stage, scale, act, wptr, comb, bytes;
 };
 __host__ __device__ inline DownLds down_lds(uint32_t table_bytes, uint32_t stage_bytes,
                                             uint32_t stage, uint32_t hblocks) {
@@ -927,7 +901,8 @@ __host__ __device__ inline DownLds down_lds(uint32_t table_bytes, uint32_t stage
     l.scale = l.stage + stage_bytes;
     l.act = (l.scale + stage * hblocks * 8u * 4u + 15u) & ~15u;
     l.wptr = l.act + kMaxActive * (uint32_t)sizeof(ActiveExpert);
-    l.bytes = l.wptr + kMaxActive * 8u;
+    l.comb = l.wptr + kMaxActive * 8u;
+    l.bytes = l.comb + kMoeMaxTokens * (kMoeMaxTopK + 1u) * (uint32_t)sizeof(CombineEntry);
     return l;
 }
 
@@ -956,6 +931,10 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_down(const MoeShape s, c
         const uint32_t* src = ws_ptr<const uint32_t>(w, w.off_active);
         uint32_t* dst = reinterpret_cast<uint32_t*>(act);
         for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) dst[i] = *gp(src + i);
+        const uint32_t cwords = s.tokens * (s.top_k + 1u) * 2u;
+        const uint32_t* csrc = ws_ptr<const uint32_t>(w, w.off_combine);
+        uint32_t* cdst = reinterpret_cast<uint32_t*>(lds + lay.comb);
+        for (uint32_t i = threadIdx.x; i < cwords; i += blockDim.x) cdst[i] = *gp(csrc + i);
     }
     fill_tables<FMT>(lds);
     __syncthreads();
@@ -988,6 +967,7 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_down(const MoeShape s, c
     pol.expert_bytes = eb;
     pol.stage_off = lay.stage;
     pol.scale_off = lay.scale;
+    pol.comb_off = lay.comb;
     pol.slab = slab;
     pol.lds = lds;
     pol.act = act;
@@ -995,7 +975,7 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_down(const MoeShape s, c
     pol.hscale = (threadIdx.x & 32u) ? 65536.0f : 1.0f;
     pol.cur_a = 0;
     pol.ntok = 0;
-    stream_range<FMT, NT, LDS>(pol, range_begin(pol.wid, NW, TU), range_begin(pol.wid + 1u, NW, TU), lds);
+    stream_range<FMT, NT, LDS>(pol, range_begin(pol.wid, NW, TU), range_begin(pol.wid + 1u, NW, TU));
 }
 
 // ------------------------------------------------------------------------------------------

@@ -234,33 +234,33 @@ __device__ __forceinline__ float unit_factor() {
 template <uint32_t FMT>
 struct ChunkDecoder {
     uint32_t w[8];
-    uint32_t sc_lo, sc_hi;  // IQ2_XXS: scale bytes of groups 0..3 and 4..7
+    uint32_t sc_lo, sc_hi;  // IQ2_XXS: 2s+1 of groups 0..3 and 4..7, one per byte
     __device__ __forceinline__ void init(const Chunk& ch) {
         if (FMT == VL_TYPE_IQ2_XXS) {
             iq2_words(ch, w);
             const uint32_t own = iq2_scale_bytes(w);
             const uint32_t other = (uint32_t)__shfl_xor((int)own, 32);
             const bool hi_half = (threadIdx.x & 32u) != 0;
-            sc_lo = hi_half ? other : own;
-            sc_hi = hi_half ? own : other;
+            sc_lo = odd_scales4(hi_half ? other : own);
+            sc_hi = odd_scales4(hi_half ? own : other);
         }
     }
     __device__ __forceinline__ i32x4 group(const Chunk& ch, int g, uint32_t lane_off, int hh,
-                                           const uint8_t* lds, int& sc) const {
+                                           int& sc) const {
         if (FMT == VL_TYPE_IQ2_XXS) {
-            sc = odd_scale(g < 4 ? sc_lo : sc_hi, g & 3);
-            return decode_iq2_xxs(w, g, lane_off, lds);
+            sc = (int)bfe(g < 4 ? sc_lo : sc_hi, 8u * (uint32_t)(g & 3), 8);
+            return decode_iq2_xxs(w, g, lane_off);
         } else if (FMT == VL_TYPE_IQ3_XXS) {
             const uint4& q = g < 2 ? ch.q0 : g < 4 ? ch.q1 : g < 6 ? ch.q2 : ch.q3;
             const uint32_t qs = word(q, 2 * (g & 1) + hh);
             const uint32_t aux = word(g < 4 ? ch.a0 : ch.a1, g & 3);
             sc = 2 * (int)(aux >> 28) + 1;
-            return decode_iq3_xxs(qs, aux, hh, lane_off, lds);
+            return decode_iq3_xxs(qs, aux, hh, lane_off);
         } else {  // IQ1_S
             const uint32_t qs4 = word(g < 4 ? ch.q0 : ch.q1, g & 3);
             const uint32_t qh = (word(ch.q2, g >> 1) >> (16 * (g & 1))) & 0xffffu;
             sc = 2 * (int)((qh >> 12) & 7u) + 1;
-            return decode_iq1_s(qs4, qh, hh, lds);
+            return decode_iq1_s(qs4, qh, hh);
         }
     }
 };
@@ -280,9 +280,9 @@ __device__ __forceinline__ uint32_t a_limb(uint32_t m) { return 2u * ((m / 4u) %
 template <bool LDS, uint32_t STRIDE>
 struct ASrc {
     const int8_t* ptr;  // global source (LDS == false)
-    uint32_t off;       // LDS byte offset (LDS == true)
-    __device__ __forceinline__ i32x4 load(const uint8_t* lds, uint32_t G) const {
-        if (LDS) return *reinterpret_cast<const i32x4*>(lds + off + G * STRIDE);
+    uint32_t off;       // LDS byte address (LDS == true)
+    __device__ __forceinline__ i32x4 load(uint32_t G) const {
+        if (LDS) return lds_load<i32x4>(off + G * STRIDE);
         return *gp(reinterpret_cast<const i32x4*>(ptr + (uint64_t)G * STRIDE));
     }
 };
@@ -295,7 +295,7 @@ struct ASrc {
 // the high-limb half); fs[s]: 2^-e of slot s for the unit's exponent block.
 template <uint32_t FMT, int NT, bool LDS>
 __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint32_t ng,
-                                              const ASrc<LDS, NT * 128u>& as, const uint8_t* lds,
+                                              const ASrc<LDS, NT * 128u>& as,
                                               float hscale, const float (&fs)[NT], float (&accf)[NT]) {
     const uint32_t lane = threadIdx.x & 63u;
     const int hh = (int)(lane >> 5);
@@ -306,7 +306,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint3
         for (int b = 0; b < 4; ++b) {
             const uint32_t G = 4u * c + b;
             if (G >= ng) break;
-            const i32x4 afr = as.load(lds, G);
+            const i32x4 afr = as.load(G);
             const uint4& q = b == 0 ? ch.q0 : b == 1 ? ch.q1 : b == 2 ? ch.q2 : ch.q3;
             i32x4 bfr;
             bfr[0] = (int)q.x; bfr[1] = (int)q.y; bfr[2] = (int)q.z; bfr[3] = (int)q.w;
@@ -321,7 +321,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint3
     }
     i32x4 afr[8];
 #pragma unroll
-    for (int g = 0; g < 8; ++g) afr[g] = as.load(lds, 8u * c + g);
+    for (int g = 0; g < 8; ++g) afr[g] = as.load(8u * c + g);
     ChunkDecoder<FMT> dec;
     dec.init(ch);
     int acc[2 * NT];
@@ -330,7 +330,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint3
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
         int sc;
-        const i32x4 bfr = dec.group(ch, g, lane_off, hh, lds, sc);
+        const i32x4 bfr = dec.group(ch, g, lane_off, hh, sc);
         const i32x16 r = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[g], bfr, zero16, 0, 0, 0);
         // |r| < 2^18 and sc <= 31: the 24-bit multiply is exact; the superblock sum stays
         // below 2^27.
@@ -381,6 +381,47 @@ __device__ __forceinline__ void store_shared_u32(uint32_t* p, uint32_t v) {
 }
 __device__ __forceinline__ uint32_t load_shared_u32(const uint32_t* p) {
     return __hip_atomic_load(gp(const_cast<uint32_t*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sums of a job's records for (slot s, row n) of matrices 0..NM-1: records first..last in order,
+// each record's two lane halves added first. The loads of four records are issued before any of
+// them is used, so a fixup waits about one memory latency per four records.
+template <int NT, int NM>
+__device__ __forceinline__ void sum_records(const float* rec, uint32_t rec_floats, uint32_t j,
+                                            uint32_t first, uint32_t last, uint32_t s, uint32_t n,
+                                            float (&out)[NM]) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) out[m] = 0.0f;
+    for (uint32_t k0 = first; k0 <= last; k0 += 4u) {
+        float v[4][NM][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t k = k0 + i <= last ? k0 + i : last;  // clamped loads are not added
+            const float* r = rec + (uint64_t)(k + j) * rec_floats + s * 64u + n;
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                v[i][m][0] = load_shared(r + m * NT * 64u);
+                v[i][m][1] = load_shared(r + m * NT * 64u + 32u);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (k0 + i <= last)
+#pragma unroll
+                for (int m = 0; m < NM; ++m) out[m] += v[i][m][0] + v[i][m][1];
+    }
+}
+
+// OR of a predicate over the block, through one LDS word per wave (slots[kStreamWaves], no
+// initialisation needed: every wave writes its own word). Contains a block barrier.
+__device__ __forceinline__ bool block_any(bool v, uint32_t* slots) {
+    const bool w = __any(v);
+    if ((threadIdx.x & 63u) == 0) slots[threadIdx.x >> 6] = w ? 1u : 0u;
+    __syncthreads();
+    uint32_t r = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kStreamWaves; ++i) r |= slots[i];
+    return r != 0;
 }
 
 // Publishes this wave's record stores and counts the wave in; returns true in every lane of
@@ -480,7 +521,7 @@ __device__ __forceinline__ void prep_x_block(const float* __restrict__ x, uint64
 // ------------------------------------------------------------------------------------------
 
 template <uint32_t FMT, int NT, bool LDS, typename Pol>
-__device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1, const uint8_t* lds) {
+__device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1) {
     constexpr int D = StreamDepth<FMT>::kValue;
     if (u0 >= u1) return;
     const uint32_t C = pol.chunks, NM = pol.nmat, UJ = C * NM;
@@ -520,7 +561,7 @@ __device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1,
             const uint32_t uu = u + k;
             if (uu < u1) {
                 pol.scales(pj, pc, fs);
-                process_chunk<FMT, NT, LDS>(buf[k], pc, pol.ng, pol.as, lds, pol.hscale, fs, acc);
+                process_chunk<FMT, NT, LDS>(buf[k], pc, pol.ng, pol.as, pol.hscale, fs, acc);
             }
             load_chunk<FMT>(htr, hc, pol.ng, buf[k]);
             head_next();

@@ -130,6 +130,16 @@ struct TileRef {
     const uint8_t* p2;
 };
 
+// Target of the loads a wave issues past the end of its range (they keep every path through the
+// stream loop the same; their data is never used). One small buffer that stays in L2, instead of
+// re-reading the range's last unit from HBM. 4 KiB covers the widest unit read (four Q8_0 groups).
+static __device__ __align__(4096) uint8_t g_idle_unit[4096];
+
+__device__ __forceinline__ TileRef idle_tile() {
+    const uint8_t* p = g_idle_unit;
+    return TileRef{p, p, p};
+}
+
 template <uint32_t FMT>
 __device__ __forceinline__ TileRef tile_ref(const vl_tiled_layout& L, const uint8_t* w, uint32_t t) {
     const uint64_t NB = L.superblocks, NG = L.groups;
@@ -526,14 +536,18 @@ __device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1)
     if (u0 >= u1) return;
     const uint32_t C = pol.chunks, NM = pol.nmat, UJ = C * NM;
     // Load head: D units ahead of the processing position. Loads are issued unconditionally
-    // (past the end of the range the head stays on the last unit, an L2 hit) so that every
+    // (past the end of the range the head moves to the idle unit, an L2 hit) so that every
     // path through the loop has the same loads outstanding and the waits before each chunk
     // stay partial.
     uint32_t hj = u0 / UJ, hm = (u0 - hj * UJ) / C, hc = u0 - hj * UJ - hm * C;
     uint32_t hu = u0;
     TileRef htr = pol.tref(hj, hm);
     auto head_next = [&]() {
-        if (hu + 1u >= u1) return;
+        if (hu + 1u >= u1) {
+            htr = idle_tile();
+            hc = 0;
+            return;
+        }
         ++hu;
         if (++hc == C) {
             hc = 0;

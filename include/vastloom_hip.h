@@ -4,9 +4,9 @@
  * CudaDriver/CudaDriverBackend launch entries and the CudaMatvecAccelerator seam) for the
  * GGUF storage types Q8_0, IQ2_XXS, IQ3_XXS and IQ1_S. Every entry point takes plain pointers
  * and sizes; device pointers are HIP device addresses, streams are hipStream_t passed as void*
- * (NULL = the default stream). Nothing here allocates behind the caller's back except the
- * governed entry points (vl_device_alloc, the accelerator), which reserve with the Safety
- * Governor first.
+ * (NULL = the default stream). Nothing here allocates device or pinned memory behind the
+ * caller's back: the governed entry points (vl_buffer_alloc, the accelerator) reserve every
+ * byte with a Safety Governor before allocating it.
  *
  * Status codes: 0 is success, 1..10 are 1 + the reference's vastloom::ErrorCode
  * (include/vastloom/core/status.hpp:10-21), and VL_DECLINED is the accelerator seam's
@@ -206,6 +206,179 @@ int vl_moe_layer_profiled(const vl_moe_config* config, const vl_moe_inputs* inpu
 
 /* Milliseconds of each stage of a recorded call (the events must have completed). */
 int vl_timeline_stage_ms(vl_timeline* timeline, uint32_t call, float* ms /* [VL_STAGE_COUNT] */);
+
+/* ---- Safety Governor ------------------------------------------------------------------------
+ * A native counterpart of safety::ResourceGovernor (src/safety/resource_governor.cpp:19-214,
+ * include/vastloom/safety/resource_governor.hpp:15-117): per-kind hard budgets, an optional
+ * aggregate host-memory budget, and a safety state that refuses new reservations when critical
+ * or emergency. The allocating entry points below see a Governor only through vl_governor_ops,
+ * so a caller that owns its own ResourceGovernor passes that instead (INTEGRATION.md shows the
+ * adapter). */
+
+#define VL_KIND_RAM 0u      /* ResourceKind::ram */
+#define VL_KIND_VRAM 1u     /* ResourceKind::vram: device memory */
+#define VL_KIND_STAGING 2u  /* ResourceKind::staging: pinned host memory */
+#define VL_KIND_SCRATCH 3u  /* ResourceKind::scratch */
+
+#define VL_STATE_NORMAL 0u
+#define VL_STATE_PRESSURE 1u
+#define VL_STATE_CRITICAL 2u
+#define VL_STATE_EMERGENCY 3u
+
+typedef struct vl_resource_limits { /* ResourceLimits (resource_governor.hpp:29-42) */
+    uint64_t host_memory_hard_limit;  /* 0 = per-kind budgets only */
+    uint64_t ram_hard_limit;
+    uint64_t vram_hard_limit;
+    uint64_t staging_hard_limit;
+    uint64_t scratch_hard_limit;
+    uint64_t minimum_system_ram_available;
+    uint64_t minimum_storage_available;
+    double pressure_ratio;  /* clamped to [0.10, 0.99] */
+    double critical_ratio;  /* clamped to [pressure_ratio + 0.01, 1.0] */
+    uint32_t recovery_samples;
+} vl_resource_limits;
+
+typedef struct vl_runtime_pressure { /* RuntimePressure (resource_governor.hpp:44-48) */
+    uint64_t system_ram_available;
+    uint64_t gpu_vram_available;
+    uint64_t storage_available;
+} vl_runtime_pressure;
+
+typedef struct vl_governor_snapshot {
+    uint32_t state;
+    uint32_t recovery_counter;
+    uint64_t reserved[4]; /* by VL_KIND_* */
+} vl_governor_snapshot;
+
+typedef struct vl_governor vl_governor;
+
+/* The reference's ResourceLimits defaults (2 GiB RAM and 20 GiB storage reserves, ratios 0.82 and
+ * 0.93, 3 recovery samples) with every hard budget 0, i.e. nothing may be reserved yet. */
+void vl_resource_limits_default(vl_resource_limits* limits);
+int vl_governor_create(const vl_resource_limits* limits, vl_governor** out);
+void vl_governor_destroy(vl_governor* governor);
+/* ResourceGovernor::try_reserve (resource_governor.cpp:64-105): zero bytes is invalid_argument;
+ * the critical and emergency states, a zero or exceeded kind budget and an exceeded aggregate
+ * host budget are resource_exhausted. On success *reservation is a non-zero id. */
+int vl_governor_try_reserve(vl_governor* governor, uint32_t kind, uint64_t bytes, const char* tag,
+                            uint64_t* reservation);
+/* Reservation::release: the bytes return to the budget. */
+int vl_governor_release(vl_governor* governor, uint64_t reservation);
+/* Reservation::abandon_accounting_on_external_release_failure: the id is dropped and its bytes
+ * stay charged (memory that could not be freed must not be handed out again). */
+int vl_governor_abandon(vl_governor* governor, uint64_t reservation);
+/* ResourceGovernor::update_pressure (resource_governor.cpp:107-196). */
+int vl_governor_update_pressure(vl_governor* governor, const vl_runtime_pressure* pressure,
+                                uint32_t* state);
+int vl_governor_snapshot_get(const vl_governor* governor, vl_governor_snapshot* out);
+
+/* A Governor as the allocating entry points see it. */
+typedef struct vl_governor_ops {
+    void* ctx;
+    /* Returns a vl_status; on VL_OK *reservation is a non-zero id. */
+    int (*try_reserve)(void* ctx, uint32_t kind, uint64_t bytes, const char* tag,
+                       uint64_t* reservation);
+    void (*release)(void* ctx, uint64_t reservation);
+    void (*abandon)(void* ctx, uint64_t reservation);
+} vl_governor_ops;
+
+/* The ops of a native Governor (valid while the Governor lives). */
+vl_governor_ops vl_governor_as_ops(vl_governor* governor);
+
+/* ---- Governed allocations -------------------------------------------------------------------
+ * CudaDriver::allocate / CudaAllocation (src/cuda/cuda_driver.cpp:2881-3010): reserve with the
+ * Governor, check that the device keeps min_free_after bytes free after the allocation, then
+ * allocate; release frees and returns the bytes, and a failed free keeps the bytes charged and
+ * quarantines the handle. */
+
+typedef struct vl_buffer vl_buffer;
+
+/* kind VL_KIND_VRAM: device memory on `device`; VL_KIND_STAGING: pinned host memory (hipHostMalloc).
+ * Refusals (the Governor's, or too little free device memory) return VL_RESOURCE_EXHAUSTED. */
+int vl_buffer_alloc(const vl_governor_ops* governor, uint32_t kind, int device, uint64_t bytes,
+                    uint64_t min_free_after, const char* tag, vl_buffer** out);
+void* vl_buffer_ptr(const vl_buffer* buffer);
+uint64_t vl_buffer_bytes(const vl_buffer* buffer);
+int vl_buffer_free(vl_buffer* buffer);
+
+/* ---- Matvec accelerator with device residency -------------------------------------------------
+ * The DeepseekV4MatvecAccelerator seam (include/vastloom/inference/deepseek_v4_reference.hpp:
+ * 437-451) as CudaMatvecAccelerator implements it (src/cuda/cuda_matvec_accelerator.cpp:102-314,
+ * include/vastloom/cuda/cuda_matvec_accelerator.hpp:17-113): matrices become resident on first
+ * use, keyed by cache identity; matrices that will not recur are evicted first, then the least
+ * recently used; anything this cannot take is declined (VL_DECLINED, output untouched). Uploads
+ * go through Governor-reserved pinned staging and hipMemcpyAsync on a copy stream, in row
+ * ranges, each range packed into the resident tiled form on the compute stream. */
+
+typedef struct vl_packed_matrix { /* DeepseekV4PackedMatrix (deepseek_v4_reference.hpp:104-141) */
+    uint32_t ggml_type;
+    uint32_t recurring;           /* the next pass asks for these weights again */
+    uint64_t rows;
+    uint64_t logical_columns;
+    uint64_t storage_columns;
+    const void* encoded;          /* host GGUF bytes (the descriptor's payload) */
+    uint64_t encoded_bytes;
+    uint64_t cache_identity;      /* 0 = do not cache: declined */
+} vl_packed_matrix;
+
+typedef struct vl_accel_options { /* CudaMatvecAcceleratorOptions (.hpp:17-30) */
+    int device_ordinal;
+    uint32_t experts_only;            /* decline recurring matrices */
+    uint64_t minimum_free_vram_after; /* default 1 GiB */
+    uint64_t maximum_resident_bytes;  /* default 6 GiB */
+    uint64_t maximum_matrices;        /* default 512 */
+    uint64_t staging_bytes;           /* pinned staging for uploads, two slots; default 64 MiB */
+} vl_accel_options;
+
+#define VL_ACCEL_TYPE_SLOTS 8u
+
+typedef struct vl_accel_stats { /* CudaMatvecAcceleratorStats (.hpp:32-54) */
+    uint64_t offered, accelerated, declined, evicted, declined_recurring;
+    uint64_t resident_matrices, resident_bytes, uploaded_bytes;
+    uint32_t declined_type[VL_ACCEL_TYPE_SLOTS];     /* storage types declined for having no kernel */
+    uint64_t declined_by_type[VL_ACCEL_TYPE_SLOTS];  /* ... and how often (first 8 types seen) */
+    double kernel_ms, upload_ms;
+} vl_accel_stats;
+
+/* Device operations of an accelerator: the default is HIP on options->device_ordinal. A test can
+ * pass its own (CudaDriver::from_backend_for_testing, src/cuda/cuda_driver.cpp:2909-2916). Every
+ * function returns a vl_status. */
+typedef struct vl_accel_backend {
+    void* ctx;
+    int (*free_memory)(void* ctx, int device, uint64_t* free_bytes);
+    int (*allocate)(void* ctx, uint32_t kind, int device, uint64_t bytes, void** ptr);
+    int (*release)(void* ctx, uint32_t kind, void* ptr);
+    /* GGUF host bytes -> tiled resident form at `tiled`, through `staging` (pinned, two slots of
+     * staging_bytes / 2) and `scratch` (device, two slots of the same size). */
+    int (*upload)(void* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void* gguf,
+                  void* tiled, void* staging, void* scratch, uint64_t staging_bytes);
+    /* Device bytes matvec needs for x, y and its workspace at this shape. */
+    int (*io_bytes)(void* ctx, uint32_t type, uint64_t rows, uint64_t cols, uint64_t* bytes);
+    /* y = W x with host x and y, through the device buffer io (io_bytes long); synchronous. A
+     * non-finite x or y is VL_INVALID_ARGUMENT, as the reference's matvec refuses it. */
+    int (*matvec)(void* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void* tiled,
+                  const float* x, float* y, void* io, uint64_t io_bytes);
+} vl_accel_backend;
+
+typedef struct vl_accel vl_accel;
+
+void vl_accel_options_default(vl_accel_options* options);
+/* backend may be NULL (HIP). Reserves and allocates the staging buffers. */
+int vl_accel_create(const vl_accel_options* options, const vl_governor_ops* governor,
+                    const vl_accel_backend* backend, vl_accel** out);
+/* Releases every resident matrix and the staging buffers. */
+int vl_accel_destroy(vl_accel* accel);
+/* DeepseekV4MatvecAccelerator::matvec: input has storage_columns floats, output rows floats,
+ * both host memory. VL_OK: output written; VL_DECLINED: output untouched; else an error. */
+int vl_accel_matvec(vl_accel* accel, const vl_packed_matrix* matrix, const float* input,
+                    uint64_t input_len, float* output, uint64_t output_len);
+/* Makes the matrix resident without multiplying (upload on first sight). VL_OK or VL_DECLINED. */
+int vl_accel_prefetch(vl_accel* accel, const vl_packed_matrix* matrix);
+/* 1 when these weights are resident now, else 0 (CudaMatvecAccelerator::holds). */
+int vl_accel_holds(const vl_accel* accel, uint64_t cache_identity);
+/* Device address of a resident matrix's tiled form (for vl_expert_weights), or VL_NOT_FOUND. */
+int vl_accel_resident_matrix(const vl_accel* accel, uint64_t cache_identity, const void** tiled);
+int vl_accel_stats_get(const vl_accel* accel, vl_accel_stats* out);
 
 #ifdef __cplusplus
 }

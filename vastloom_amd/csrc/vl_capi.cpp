@@ -9,15 +9,16 @@
 #include <vector>
 
 #include "../../include/vastloom_hip.h"
+#include "vl_error.h"
 #include "vl_kernels.h"
 #include "vl_layout.h"
 #include "vl_moe.h"
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
 
-int fail(int code, const char* fmt, ...) {
+int vl::fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -26,6 +27,10 @@ int fail(int code, const char* fmt, ...) {
     g_last_error = buf;
     return code;
 }
+
+namespace {
+
+using vl::fail;
 
 int hip_fail(hipError_t e, const char* what) {
     return fail(VL_INTERNAL_ERROR, "%s: %s", what, hipGetErrorString(e));

@@ -33,6 +33,10 @@ hipError_t ensure_dynamic_lds(const void* kernel, uint32_t bytes);
 
 hipError_t launch_pack(const vl_tiled_layout& L, const uint8_t* gguf, uint8_t* tiled,
                        hipStream_t stream);
+// Rows [row0, row1) of the padded matrix (row1 <= rows_padded); gguf_row0 holds the GGUF bytes
+// of rows row0 .. min(row1, rows) - 1.
+hipError_t launch_pack_rows(const vl_tiled_layout& L, const uint8_t* gguf_row0, uint8_t* tiled,
+                            uint32_t row0, uint32_t row1, hipStream_t stream);
 hipError_t launch_dequant(const vl_tiled_layout& L, const uint8_t* tiled, float* out,
                           hipStream_t stream);
 

@@ -64,17 +64,18 @@ __device__ __forceinline__ uint32_t ld_u32_bytes(const uint8_t* p) {
     return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
 
+// Rows [row0, row1) of the padded matrix; gguf points at the GGUF bytes of row row0.
 __global__ void k_pack(vl_tiled_layout L, const uint8_t* __restrict__ gguf,
-                       uint8_t* __restrict__ out) {
+                       uint8_t* __restrict__ out, uint32_t row0, uint32_t row1) {
     const uint64_t id = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const bool q8 = L.type == VL_TYPE_Q8_0;
     const uint32_t units = q8 ? L.groups : L.superblocks;  // blocks per row
-    if (id >= (uint64_t)L.rows_padded * units) return;
-    const uint32_t r = (uint32_t)(id / units), b = (uint32_t)(id % units);
+    if (id >= (uint64_t)(row1 - row0) * units) return;
+    const uint32_t r = row0 + (uint32_t)(id / units), b = (uint32_t)(id % units);
     const uint32_t t = r / 32u, j = r % 32u;
     const bool pad = r >= L.rows;
     // Padded rows read nothing; their source pointer stays on the first block.
-    const uint8_t* src = pad ? gguf : gguf + ((uint64_t)r * units + b) * L.block_bytes;
+    const uint8_t* src = pad ? gguf : gguf + ((uint64_t)(r - row0) * units + b) * L.block_bytes;
     const uint32_t NG = L.groups, NB = L.superblocks;
     uint8_t* S = out + L.plane2;
     switch (L.type) {
@@ -131,13 +132,20 @@ __global__ void k_pack(vl_tiled_layout L, const uint8_t* __restrict__ gguf,
     }
 }
 
-hipError_t launch_pack(const vl_tiled_layout& L, const uint8_t* gguf, uint8_t* tiled,
-                       hipStream_t stream) {
-    const uint64_t units = (uint64_t)L.rows_padded * (L.type == VL_TYPE_Q8_0 ? L.groups : L.superblocks);
+hipError_t launch_pack_rows(const vl_tiled_layout& L, const uint8_t* gguf_row0, uint8_t* tiled,
+                            uint32_t row0, uint32_t row1, hipStream_t stream) {
+    if (row0 >= row1 || row1 > L.rows_padded) return hipErrorInvalidValue;
+    const uint64_t units = (uint64_t)(row1 - row0) * (L.type == VL_TYPE_Q8_0 ? L.groups : L.superblocks);
     const uint32_t block = 256;
     const uint64_t grid = (units + block - 1) / block;
-    hipLaunchKernelGGL(k_pack, dim3((uint32_t)grid), dim3(block), 0, stream, L, gguf, tiled);
+    hipLaunchKernelGGL(k_pack, dim3((uint32_t)grid), dim3(block), 0, stream, L, gguf_row0, tiled,
+                       row0, row1);
     return hipGetLastError();
+}
+
+hipError_t launch_pack(const vl_tiled_layout& L, const uint8_t* gguf, uint8_t* tiled,
+                       hipStream_t stream) {
+    return launch_pack_rows(L, gguf, tiled, 0u, L.rows_padded, stream);
 }
 
 // ------------------------------------------------------------------------------------------

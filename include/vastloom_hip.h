@@ -139,7 +139,8 @@ typedef struct vl_expert_weights {
 #define VL_SCORE_SIGMOID 1u
 
 typedef struct vl_moe_config {
-    uint32_t tokens;        /* 1..8 */
+    uint32_t tokens;        /* 1..1024; above 8 the grouped path (at most 16384 token-expert
+                             * assignments and 1792 groups of up to 8 tokens) */
     uint32_t width;         /* model width H (multiple of 256) */
     uint32_t intermediate;  /* expert width F */
     uint32_t experts;       /* routed experts E (<= 1024) */
@@ -171,7 +172,10 @@ typedef struct vl_moe_inputs {
 int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes);
 
 /* One MoE layer: router logits (float64 accumulation), routing, the selected experts' SwiGLU
- * FFNs and the combine, all on the stream with no host synchronisation. The status word of the
+ * FFNs and the combine, all on the stream with no host synchronisation. Up to 8 tokens share
+ * each expert's weight pass; more tokens take the grouped path, which splits each selected
+ * expert's tokens, in ascending order, into groups of up to 8 and streams the expert's weights
+ * once per group (moe_forward's per-expert token batches, deepseek_v4_graph.cpp:2211-2229). The status word of the
  * workspace (vl_read_status) reports non-finite values and invalid routes (an out-of-range or
  * repeated expert id); the output is then not meaningful, as the reference would have refused
  * the layer. Replaces the per-matvec device calls of moe_forward / qwen38_moe_block. */

@@ -104,7 +104,9 @@ def _device_layer(ops, lib, wl, experts, shared, sem, routing, router=None, bias
 
 def _check_layer(ops, lib, oracle, wl, experts, shared, sem, routing_name, routing, x,
                  score_fn=SCORE_SIGMOID, bias=None, table=None, route_scale=1.0,
-                 routed_limit=0.0, shared_limit=0.0):
+                 routed_limit=0.0, shared_limit=0.0, sample=None):
+    """Routes of every token must equal the oracle's; outputs are checked for every token, or
+    for the tokens in `sample` (each token's output depends on its own routes only)."""
     H, F = wl.width, wl.intermediate
     router = wl.router()
     layer = _device_layer(ops, lib, wl, experts, shared, sem, routing, router, bias, score_fn,
@@ -118,6 +120,9 @@ def _check_layer(ops, lib, oracle, wl, experts, shared, sem, routing_name, routi
                            route_scale)
     assert np.array_equal(ids_dev, ids), (ids_dev, ids)
     assert np.allclose(w_dev, w, rtol=1e-6, atol=0)
+    if sample is not None:
+        sample = np.asarray(sample)
+        got, x, ids, w = got[sample], x[sample], ids[sample], w[sample]
     if sem == "qwen":
         want = np.stack([oracle.moe_qwen(x[t], ids[t], w[t], experts, shared, H, F, threads=8)
                          for t in range(x.shape[0])])
@@ -199,3 +204,55 @@ def test_workload_deepseek_layers(ops, lib, oracle, name):
     experts, shared = _workload_case(wl)
     _check_layer(ops, lib, oracle, wl, experts, shared, "deepseek", "learned", lib.ROUTE_LEARNED,
                  wl.x(), SCORE_SIGMOID)
+
+
+# -- Grouped path: more than 8 tokens -------------------------------------------------------------
+
+@pytest.mark.parametrize("routing_name,tokens,gt,dt", [
+    ("learned", 9, IQ2_XXS, IQ2_XXS), ("table", 37, IQ2_XXS, IQ2_XXS),
+    ("softmax", 100, Q8_0, Q8_0), ("learned", 64, IQ1_S, IQ3_XXS)])
+def test_grouped_layers(ops, lib, oracle, routing_name, tokens, gt, dt):
+    print(f"[moe grouped] {routing_name} tokens={tokens} types={gt},{dt}", flush=True)
+    rng = np.random.default_rng(tokens)
+    from vastloom_amd.workloads import MoeWorkload
+    sem = "qwen" if routing_name == "softmax" else "deepseek"
+    E, K, H, F = 24, 4, 512, 256
+    wl = MoeWorkload("grouped_small", 13, H, F, E, K, tokens, gt, dt, 0.01, sem)
+    experts = [make_expert(rng, gt, dt, H, F) for _ in range(E)]
+    shared = make_expert(rng, gt, dt, H, F)
+    x = rng.standard_normal((tokens, H)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32) if routing_name == "learned" else None
+    table = (np.stack([rng.choice(E, K, replace=False) for _ in range(tokens)])
+             if routing_name == "table" else None)
+    routing = {"learned": lib.ROUTE_LEARNED, "table": lib.ROUTE_TABLE,
+               "softmax": lib.ROUTE_SOFTMAX}[routing_name]
+    _check_layer(ops, lib, oracle, wl, experts, shared, sem, routing_name, routing, x,
+                 SCORE_SIGMOID, bias, table, route_scale=1.5 if sem == "deepseek" else 1.0,
+                 routed_limit=0.3 if sem == "deepseek" else 0.0,
+                 shared_limit=0.2 if sem == "deepseek" else 0.0)
+
+
+def test_grouped_bad_route_is_refused(ops, lib, oracle):
+    rng = np.random.default_rng(2)
+    from vastloom_amd.workloads import MoeWorkload
+    wl = MoeWorkload("grouped_bad", 14, 256, 256, 6, 2, 20, IQ2_XXS, IQ2_XXS, 0.01, "deepseek")
+    experts = [make_expert(rng, IQ2_XXS, IQ2_XXS, 256, 256) for _ in range(6)]
+    layer = _device_layer(ops, lib, wl, experts, None, "deepseek", lib.ROUTE_TABLE, wl.router())
+    x = torch.from_numpy(rng.standard_normal((20, 256)).astype(np.float32)).cuda()
+    table = np.stack([rng.choice(6, 2, replace=False) for _ in range(20)]).astype(np.int32)
+    ok = layer.forward(x, table_ids=torch.from_numpy(table).cuda())
+    assert torch.isfinite(ok).all()
+    table[13] = [4, 4]
+    with pytest.raises(ops.VlError):
+        layer.forward(x, table_ids=torch.from_numpy(table).cuda())
+
+
+def test_workload_grouped_moe(ops, lib, oracle):
+    """512 tokens, Zipf(1.1) table routing over 256 IQ2_XXS experts plus the shared expert:
+    every token's routes, and the outputs of a sample of tokens, against the oracle."""
+    wl = workload("grouped_moe")
+    print("[workload] grouped_moe", flush=True)
+    experts, shared = _workload_case(wl)
+    _check_layer(ops, lib, oracle, wl, experts, shared, "deepseek", "table", lib.ROUTE_TABLE,
+                 wl.x(), SCORE_SIGMOID, table=wl.zipf_table(),
+                 sample=[0, 1, 77, 255, 256, 400, 511])

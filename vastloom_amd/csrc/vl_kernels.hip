@@ -263,7 +263,7 @@ __global__ void __launch_bounds__(256) k_prep_x(const float* __restrict__ x, uin
         uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + m.off_counters);
         for (uint32_t i = threadIdx.x; i < m.tiles; i += blockDim.x) cnt[i] = 0;
     }
-    prep_x_block(x, cols, cols, tokens, m.slots, blockIdx.x,
+    prep_x_block(x, cols, cols, 0u, tokens, m.slots, 8u, blockIdx.x,
                  reinterpret_cast<int8_t*>(ws + m.off_xlimbs), reinterpret_cast<int*>(ws + m.off_xexp),
                  reinterpret_cast<uint32_t*>(ws + m.off_xflags));
 }

@@ -37,8 +37,13 @@ enum MoeRouting : uint32_t {
 
 enum MoeScore : uint32_t { kScoreSqrtSoftplus = 0, kScoreSigmoid = 1 };
 
+// Token slots of one MFMA job; more tokens take the grouped path (up to kMoeMaxTokensGrouped
+// tokens, with at most kMoeMaxGroupAssign token-expert assignments and kMoeMaxGroups groups).
 constexpr uint32_t kMoeMaxTokens = 8;
 constexpr uint32_t kMoeMaxTopK = 16;
+constexpr uint32_t kMoeMaxTokensGrouped = 1024;
+constexpr uint32_t kMoeMaxGroupAssign = 16384;
+constexpr uint32_t kMoeMaxGroups = 1792;
 
 struct MoeShape {
     uint32_t tokens, width, inter, experts, top_k;
@@ -67,8 +72,10 @@ struct MoeWorkspace {
     uint64_t bytes;
     uint64_t off_header, off_logits, off_scores, off_keys, off_route_idx, off_route_w, off_active, off_combine,
         off_xexp, off_xflags, off_xlimbs, off_counters, off_rec_gu, off_rec_dn, off_h,
-        off_hslab, off_ypart;
-    uint32_t max_active, slots, waves, blocks;
+        off_hslab, off_ypart, off_gweights;
+    uint32_t grouped;                                 // more than kMoeMaxTokens tokens
+    uint32_t max_active, slots, waves, blocks;        // slots: MFMA token slots of a job
+    uint32_t xslots, estride;                         // token strides of the limb and exponent arrays
     uint32_t tiles_gu, tiles_dn, hblocks, xblocks;  // gate/up and down tiles, h and x exponent blocks
     uint32_t counters;                                // u32 words at off_counters
     uint32_t stage;                                   // experts one down block converts h for

@@ -49,10 +49,21 @@ constexpr uint32_t kMaxActive = kMoeMaxTokens * kMoeMaxTopK + 1;
 
 static inline uint64_t align256(uint64_t v) { return (v + 255u) & ~uint64_t(255); }
 
+// Groups of the grouped path, at most: each selected expert's tokens in groups of
+// kMoeMaxTokens (a partial group per expert at most), then the shared expert's.
+static uint64_t max_groups(const MoeShape& s) {
+    const uint64_t assign = (uint64_t)s.tokens * s.top_k;
+    const uint64_t used = assign < s.experts ? assign : s.experts;
+    return assign / kMoeMaxTokens + used + (s.has_shared ? (s.tokens + kMoeMaxTokens - 1u) / kMoeMaxTokens : 0u);
+}
+
 bool moe_shape_ok(const MoeShape& s) {
     uint32_t be = 0, bb = 0;
-    if (s.tokens == 0 || s.tokens > kMoeMaxTokens || s.top_k == 0 || s.top_k > kMoeMaxTopK ||
+    if (s.tokens == 0 || s.tokens > kMoeMaxTokensGrouped || s.top_k == 0 || s.top_k > kMoeMaxTopK ||
         s.experts == 0 || s.experts > 1024 || s.top_k > s.experts)
+        return false;
+    if (s.tokens > kMoeMaxTokens &&
+        ((uint64_t)s.tokens * s.top_k > kMoeMaxGroupAssign || max_groups(s) > kMoeMaxGroups))
         return false;
     if (!vl_block_shape(s.gate_type, &be, &bb) || s.width % be || s.width % 256u) return false;
     if (!vl_block_shape(s.down_type, &be, &bb) || s.inter % be || s.inter % 32u) return false;
@@ -73,8 +84,11 @@ __host__ __device__ inline uint32_t down_expert_bytes(uint32_t inter, uint32_t s
 MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base) {
     MoeWorkspace w{};
     w.base = static_cast<uint8_t*>(base);
-    w.max_active = max_active(s);
-    w.slots = limb_slots(s.tokens);
+    w.grouped = s.tokens > kMoeMaxTokens ? 1u : 0u;
+    w.max_active = w.grouped ? (uint32_t)max_groups(s) : max_active(s);
+    w.slots = w.grouped ? kMoeMaxTokens : limb_slots(s.tokens);
+    w.xslots = w.grouped ? s.tokens : w.slots;
+    w.estride = w.grouped ? s.tokens : 8u;
     w.blocks = blocks;
     w.waves = blocks * kStreamWaves;
     w.tiles_gu = (s.inter + 31u) / 32u;
@@ -97,15 +111,16 @@ MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base
     w.off_route_w = o; o = align256(o + T * K * 4u);
     w.off_active = o; o = align256(o + A * sizeof(ActiveExpert));
     w.off_combine = o; o = align256(o + T * (K + 1) * sizeof(CombineEntry));
-    w.off_xexp = o; o = align256(o + (uint64_t)w.xblocks * 8u * 4u);
-    w.off_xflags = o; o = align256(o + (uint64_t)w.xblocks * 8u * 4u);
-    w.off_xlimbs = o; o = align256(o + (uint64_t)(s.width / 32u) * NT * 128u);
+    w.off_xexp = o; o = align256(o + (uint64_t)w.xblocks * w.estride * 4u);
+    w.off_xflags = o; o = align256(o + (uint64_t)w.xblocks * w.estride * 4u);
+    w.off_xlimbs = o; o = align256(o + (uint64_t)(s.width / 32u) * w.xslots * 128u);
     w.off_counters = o; o = align256(o + (uint64_t)w.counters * 4u);
     w.off_rec_gu = o; o = align256(o + (w.waves + A * w.tiles_gu) * 2u * NT * 64u * 4u);
     w.off_rec_dn = o; o = align256(o + (w.waves + A * w.tiles_dn) * NT * 64u * 4u);
     w.off_h = o; o = align256(o + A * NT * s.inter * 4u);
     w.off_hslab = o; o = align256(o + (uint64_t)blocks * w.stage * down_expert_bytes(s.inter, w.slots));
     w.off_ypart = o; o = align256(o + A * NT * (uint64_t)s.width * 4u);
+    w.off_gweights = o; o = align256(o + (w.grouped ? A * sizeof(MoeExpert) : 0u));
     w.bytes = o;
     return w;
 }
@@ -170,22 +185,29 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
-// Block b: expert row b's logits (four waves take interleaved quarters of the row with every
-// lane's float4 loads in flight; partial sums added in wave order), then the limbs of column
-// block b of every token. Block 0 also zeroes the status word and the handoff counters.
+// Block (b, g): expert row b's logits for the tokens of group g (tokens 8g .. 8g + 7; four waves
+// take interleaved quarters of the row with every lane's float4 loads in flight; partial sums
+// added in wave order), then the limbs of column block b of the group's tokens. Block (0, 0)
+// zeroes the status word; all blocks together zero the handoff counters.
 __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeInputs in,
                                                     const MoeWorkspace w) {
     __shared__ double red[kMoeMaxTokens][4];
     const uint32_t b = blockIdx.x;
-    if (b == 0) {
+    const uint32_t t0 = blockIdx.y * kMoeMaxTokens;
+    const uint32_t t1 = t0 + kMoeMaxTokens < s.tokens ? t0 + kMoeMaxTokens : s.tokens;
+    if (b == 0 && blockIdx.y == 0 && threadIdx.x < 2) {
         MoeHeader* h = ws_ptr<MoeHeader>(w, w.off_header);
-        if (threadIdx.x < 2) (&h->status)[threadIdx.x] = 0;
+        (&h->status)[threadIdx.x] = 0;
+    }
+    {
         uint32_t* cnt = ws_ptr<uint32_t>(w, w.off_counters);
-        for (uint32_t i = threadIdx.x; i < w.counters; i += blockDim.x) cnt[i] = 0;
+        const uint32_t nb = gridDim.x * gridDim.y, lb = blockIdx.y * gridDim.x + b;
+        for (uint32_t i = lb * blockDim.x + threadIdx.x; i < w.counters; i += nb * blockDim.x) cnt[i] = 0;
     }
     if (b < w.xblocks)
-        prep_x_block(in.x, s.width, s.width, s.tokens, w.slots, b, ws_ptr<int8_t>(w, w.off_xlimbs),
-                     ws_ptr<int>(w, w.off_xexp), ws_ptr<uint32_t>(w, w.off_xflags));
+        prep_x_block(in.x, s.width, s.width, t0, t1, w.xslots, w.estride, b,
+                     ws_ptr<int8_t>(w, w.off_xlimbs), ws_ptr<int>(w, w.off_xexp),
+                     ws_ptr<uint32_t>(w, w.off_xflags));
     if (s.routing == kRouteGiven || b >= s.experts) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float4* row = reinterpret_cast<const float4*>(in.router + (uint64_t)b * s.width);
@@ -197,7 +219,7 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
         const uint32_t i = threadIdx.x + 256u * j;
         if (i < n4) { wv[j] = row[i]; nv = j + 1; }
     }
-    for (uint32_t t = 0; t < s.tokens; ++t) {
+    for (uint32_t t = t0; t < t1; ++t) {
         const float4* xr = reinterpret_cast<const float4*>(in.x + (uint64_t)t * s.width);
         double acc = 0.0;
 #pragma unroll
@@ -219,15 +241,15 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
             acc += (double)a.w * (double)c.w;
         }
         acc = wave_sum_f64(acc);
-        if (lane == 0) red[t][wave] = acc;
+        if (lane == 0) red[t - t0][wave] = acc;
     }
     __syncthreads();
-    if (threadIdx.x < s.tokens) {
+    if (threadIdx.x < t1 - t0) {
         // Logit, score and selection key: learned routing ranks score + bias (the reference's
         // float keys), softmax routing ranks probabilities, which order as the logits do.
-        const uint32_t t = threadIdx.x;
+        const uint32_t t = t0 + threadIdx.x, r = threadIdx.x;
         const uint64_t i = (uint64_t)t * s.experts + b;
-        const float logit = (float)(((red[t][0] + red[t][1]) + red[t][2]) + red[t][3]);
+        const float logit = (float)(((red[r][0] + red[r][1]) + red[r][2]) + red[r][3]);
         float score = 0.0f;
         uint32_t key;
         if (s.routing == kRouteSoftmax) {
@@ -370,9 +392,11 @@ struct RouteLds {
 };
 
 
-// Routing of token t by one wave: ids and weights into rt.idx/wt, refusal into rt.bad[t].
-__device__ __forceinline__ void route_token_wave(const MoeShape& s, const MoeInputs& in,
-                                                 const MoeWorkspace& w, uint32_t t, RouteLds& rt) {
+// Routing of token t by one wave: its K ids and weights into idx/wt (LDS, in the token's rank
+// order); returns true in every lane when the token is refused.
+__device__ __forceinline__ bool route_token(const MoeShape& s, const MoeInputs& in,
+                                            const MoeWorkspace& w, uint32_t t, TopKLds& tk,
+                                            uint32_t* idx, float* wt) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t K = s.top_k, E = s.experts;
     const uint64_t base = (uint64_t)t * E;
@@ -383,48 +407,53 @@ __device__ __forceinline__ void route_token_wave(const MoeShape& s, const MoeInp
             if (s.routing == kRouteGiven) id = in.given_ids ? *gp(in.given_ids + t * K + k) : 0u;
             else id = *gp(in.table_ids + t * K + k);
             if (id >= E) { bad = true; id = 0; }
-            rt.idx[t * K + k] = id;
+            idx[k] = id;
         }
         __builtin_amdgcn_wave_barrier();
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         // Duplicate experts within one token are refused.
         for (uint32_t k = lane; k < K; k += 64)
             for (uint32_t j = 0; j < k; ++j)
-                if (rt.idx[t * K + j] == rt.idx[t * K + k]) bad = true;
+                if (idx[j] == idx[k]) bad = true;
         if (s.routing == kRouteGiven) {
             for (uint32_t k = lane; k < K; k += 64)
-                rt.wt[t * K + k] = in.given_weights ? *gp(in.given_weights + t * K + k) : 1.0f;
+                wt[k] = in.given_weights ? *gp(in.given_weights + t * K + k) : 1.0f;
         } else if (lane == 0) {
             const float* lg = ws_ptr<const float>(w, w.off_logits) + base;
             const float* scr = ws_ptr<const float>(w, w.off_scores) + base;
             double sum = 0.0;
             float sc[kMoeMaxTopK];
             for (uint32_t k = 0; k < K; ++k) {
-                const uint32_t e = rt.idx[t * K + k];
+                const uint32_t e = idx[k];
                 bad |= !isfinite(*gp(lg + e));
                 sc[k] = *gp(scr + e);
                 sum += (double)sc[k];
             }
             if (!(sum > 0.0) || isinf(sum)) bad = true;
             for (uint32_t k = 0; k < K; ++k)
-                rt.wt[t * K + k] = (float)((double)sc[k] / sum * (double)s.route_scale);
+                wt[k] = (float)((double)sc[k] / sum * (double)s.route_scale);
         }
     } else {
         const float* lg = ws_ptr<const float>(w, w.off_logits) + base;
         const float* scr = ws_ptr<const float>(w, w.off_scores) + base;
         const uint32_t* keys = ws_ptr<const uint32_t>(w, w.off_keys) + base;
         const bool softmax = s.routing == kRouteSoftmax;
-        TopKLds& tk = rt.topk[t];
-        uint32_t* si = rt.idx + t * K;
-        float* sw = rt.wt + t * K;
-        if (E <= 64) bad = route_topk<1>(lg, scr, keys, E, K, softmax, s, tk, si, sw);
-        else if (E <= 128) bad = route_topk<2>(lg, scr, keys, E, K, softmax, s, tk, si, sw);
-        else if (E <= 256) bad = route_topk<4>(lg, scr, keys, E, K, softmax, s, tk, si, sw);
-        else if (E <= 512) bad = route_topk<8>(lg, scr, keys, E, K, softmax, s, tk, si, sw);
-        else bad = route_topk<16>(lg, scr, keys, E, K, softmax, s, tk, si, sw);
+        if (E <= 64) bad = route_topk<1>(lg, scr, keys, E, K, softmax, s, tk, idx, wt);
+        else if (E <= 128) bad = route_topk<2>(lg, scr, keys, E, K, softmax, s, tk, idx, wt);
+        else if (E <= 256) bad = route_topk<4>(lg, scr, keys, E, K, softmax, s, tk, idx, wt);
+        else if (E <= 512) bad = route_topk<8>(lg, scr, keys, E, K, softmax, s, tk, idx, wt);
+        else bad = route_topk<16>(lg, scr, keys, E, K, softmax, s, tk, idx, wt);
     }
-    bad = __any(bad);
-    if (lane == 0) rt.bad[t] = bad ? 1u : 0u;
+    return __any(bad);
+}
+
+// Routing of token t by one wave of a gate/up block: ids and weights into rt.idx/wt, refusal into
+// rt.bad[t].
+__device__ __forceinline__ void route_token_wave(const MoeShape& s, const MoeInputs& in,
+                                                 const MoeWorkspace& w, uint32_t t, RouteLds& rt) {
+    const uint32_t K = s.top_k;
+    const bool bad = route_token(s, in, w, t, rt.topk[t], rt.idx + t * K, rt.wt + t * K);
+    if ((threadIdx.x & 63u) == 0) rt.bad[t] = bad ? 1u : 0u;
 }
 
 // After route_token_wave for every token (and a barrier), the whole block builds the active-expert
@@ -556,15 +585,18 @@ __device__ __forceinline__ float swiglu(uint32_t sem, float g, float u, float li
 // Last wave of gate/up tile job j: gate/up sums, SwiGLU, the tile's h rows ([A][NT][inter]), and
 // the maxima of |h| per 256-row block and slot (hmax [A][hblocks][8], the down kernel's limb
 // exponents). The active-expert list is the RouteLds at LDS byte route_off.
+// With entries == nullptr the active list is the RouteLds at LDS byte route_off (per-block
+// routing); otherwise it is the grouped path's list in global memory.
 template <int NT>
 __device__ __attribute__((noinline)) void gateup_fixup(const float* rec, float* hout, uint32_t* hmax,
                                                        uint32_t* status, uint32_t j, uint32_t first,
                                                        uint32_t last, uint32_t tiles, uint32_t hblocks,
                                                        uint32_t inter, uint32_t semantics,
-                                                       uint32_t route_off) {
+                                                       uint32_t route_off, const ActiveExpert* entries) {
     extern __shared__ __align__(16) uint8_t lds[];
     const uint32_t a = j / tiles, t = j - a * tiles;
-    const ActiveExpert& ae = reinterpret_cast<const RouteLds*>(lds + route_off)->act[a];
+    const ActiveExpert& ae =
+        entries ? entries[a] : reinterpret_cast<const RouteLds*>(lds + route_off)->act[a];
     const uint32_t lane = threadIdx.x & 63u, n = lane & 31u, hh = lane >> 5;
     const uint32_t row = t * 32u + n, sb = t / 8u, F = inter;
     const uint32_t nt = uni(ae.ntok);
@@ -654,7 +686,7 @@ struct GateUp {
         if (!arrive(cn.gu + j, last - first + 1u)) return;
         gateup_fixup<NT>(rec, ws_ptr<float>(w, w.off_h), cn.hmax,
                          &ws_ptr<MoeHeader>(w, w.off_header)->status, j, first, last, tiles,
-                         w.hblocks, s.inter, s.semantics, route_off);
+                         w.hblocks, s.inter, s.semantics, route_off, nullptr);
     }
 };
 
@@ -739,9 +771,9 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_gateup(const MoeShape s,
                                range_begin(pol.wid + 1u, pol.NW, pol.TU));
 }
 
-// Last wave of down job j: the expert's output rows of tile t (ypart [A][NT][width]); the last
-// expert of tile t then combines the layer output rows in each token's combine order (the
-// CombineEntry table [tokens][top_k + 1] at LDS byte comb_off).
+// Last wave of down job j: the expert's output rows of tile t (ypart [A][NT][width]); unless
+// tile_cnt is null, the last expert of tile t then combines the layer output rows in each token's
+// combine order (the CombineEntry table [tokens][top_k + 1] at LDS byte comb_off).
 template <int NT>
 __device__ __attribute__((noinline)) void down_fixup(const float* rec, float* ypart, float* out,
                                                      uint32_t* tile_cnt, uint32_t* status, uint32_t j,
@@ -763,7 +795,7 @@ __device__ __attribute__((noinline)) void down_fixup(const float* rec, float* yp
             if (row < H) store_shared(ypart + ((uint64_t)a * NT + sl) * H + row, y[0]);
         }
     }
-    if (!arrive(tile_cnt + t, n_active)) return;
+    if (!tile_cnt || !arrive(tile_cnt + t, n_active)) return;  // grouped path: combined later
     const CombineEntry* comb = reinterpret_cast<const CombineEntry*>(lds + comb_off);
     const uint32_t K = top_k, nent = K + (has_shared ? 1u : 0u);
     constexpr uint32_t kMaxEnt = kMoeMaxTopK + 1u;
@@ -861,8 +893,8 @@ struct Down {
 // 256-row block and slot from the gate/up kernel's maxima; scale[(a - a0)][block][8] = 2^-e.
 template <int NT>
 __device__ __forceinline__ void convert_h(const MoeWorkspace& w, uint32_t inter, uint32_t a0,
-                                          uint32_t a1, const ActiveExpert* act, int8_t* dst,
-                                          float* scale) {
+                                          uint32_t a1, const uint32_t* ntok, uint32_t ntok_stride,
+                                          int8_t* dst, float* scale) {
     const uint32_t* hmax = counters_of(w).hmax;
     const float* h = ws_ptr<const float>(w, w.off_h);
     const uint32_t na = a1 - a0 + 1u;
@@ -874,7 +906,7 @@ __device__ __forceinline__ void convert_h(const MoeWorkspace& w, uint32_t inter,
     for (uint32_t i = threadIdx.x; i < na * NT * quads; i += blockDim.x) {
         const uint32_t q = i % quads, sl = (i / quads) % NT, al = i / (quads * NT);
         const uint32_t a = a0 + al, col = 4u * q;
-        if (sl >= act[a].ntok) continue;
+        if (sl >= ntok[a * ntok_stride]) continue;
         const uint32_t m = *gp(hmax + ((uint64_t)a * w.hblocks + col / 256u) * 8u + sl);
         const int e = limb_exponent(__uint_as_float(m));
         const float4 f4 = ld_f4(h + ((uint64_t)a * NT + sl) * inter + col);
@@ -941,7 +973,8 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_down(const MoeShape s, c
     for (uint32_t i = threadIdx.x; i < n_active; i += blockDim.x)
         wptr[i] = in.experts[act[i].expert].down;
     if (ub0 < ub1)
-        convert_h<NT>(w, s.inter, a0, a1, act, LDS ? reinterpret_cast<int8_t*>(lds + lay.stage) : slab,
+        convert_h<NT>(w, s.inter, a0, a1, &act[0].ntok, (uint32_t)(sizeof(ActiveExpert) / 4u),
+                      LDS ? reinterpret_cast<int8_t*>(lds + lay.stage) : slab,
                       reinterpret_cast<float*>(lds + lay.scale));
     __syncthreads();
     if (n_active == 0) {
@@ -976,6 +1009,409 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_down(const MoeShape s, c
     pol.cur_a = 0;
     pol.ntok = 0;
     stream_range<FMT, NT, LDS>(pol, range_begin(pol.wid, NW, TU), range_begin(pol.wid + 1u, NW, TU));
+}
+
+// ------------------------------------------------------------------------------------------
+// Grouped path: more than kMoeMaxTokens tokens.
+//
+// k_moe_route_many routes every token (one wave each) into the workspace's route arrays.
+// k_moe_plan splits each selected expert's tokens, in ascending token order, into groups of up
+// to kMoeMaxTokens (one job's MFMA token slots), appends the shared expert's groups (tokens in
+// order) and writes every token's combine order. The gate/up and down kernels then stream the
+// (group, tile) jobs of that list, and k_moe_combine adds each token's expert rows in its
+// combine order. An expert's weights are read once per group of its tokens.
+// ------------------------------------------------------------------------------------------
+
+struct RouteWaveLds {
+    TopKLds tk;
+    uint32_t idx[kMoeMaxTopK];
+    float wt[kMoeMaxTopK];
+};
+
+__global__ void __launch_bounds__(kStreamThreads) k_moe_route_many(const MoeShape s, const MoeInputs in,
+                                                                   const MoeWorkspace w) {
+    __shared__ RouteWaveLds r[kStreamWaves];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t t = blockIdx.x * kStreamWaves + wave;
+    if (t >= s.tokens) return;
+    RouteWaveLds& rw = r[wave];
+    const bool bad = route_token(s, in, w, t, rw.tk, rw.idx, rw.wt);
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const uint32_t K = s.top_k;
+    if (lane < K) {
+        *gp(ws_ptr<uint32_t>(w, w.off_route_idx) + (uint64_t)t * K + lane) = rw.idx[lane];
+        *gp(ws_ptr<float>(w, w.off_route_w) + (uint64_t)t * K + lane) = rw.wt[lane];
+    }
+    if (bad && lane == 0) or_bits(&ws_ptr<MoeHeader>(w, w.off_header)->status, kStatusBadRoute);
+}
+
+// Dynamic LDS bytes of k_moe_plan: expert counts, group bases, the staged route ids, wave flags.
+__host__ __device__ inline uint32_t plan_lds_bytes(const MoeShape& s) {
+    return (2u * s.experts + 1u + s.tokens * s.top_k + kStreamWaves) * 4u;
+}
+
+// One block: the grouped path's group list (ActiveExpert entries), their weight pointers, every
+// token's combine entries, the group count and the status bits of refused routes and non-finite
+// activations.
+__global__ void __launch_bounds__(kStreamThreads) k_moe_plan(const MoeShape s, const MoeInputs in,
+                                                             const MoeWorkspace w) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const uint32_t T = s.tokens, K = s.top_k, E = s.experts, P = T * K;
+    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(lds);
+    uint32_t* base = cnt + E;
+    uint32_t* ids = base + E + 1u;
+    uint32_t* flags = ids + P;
+    MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
+    const uint32_t* ridx = ws_ptr<const uint32_t>(w, w.off_route_idx);
+    const float* rwt = ws_ptr<const float>(w, w.off_route_w);
+    for (uint32_t i = tid; i < P; i += nth) ids[i] = *gp(ridx + i);
+    for (uint32_t e = tid; e < E; e += nth) cnt[e] = 0;
+    bool nonfinite = false;
+    const uint32_t* xf = ws_ptr<const uint32_t>(w, w.off_xflags);
+    for (uint32_t i = tid; i < w.xblocks * w.estride; i += nth) nonfinite |= *gp(xf + i) != 0u;
+    const bool any_nonfinite = block_any(nonfinite, flags);
+    for (uint32_t i = tid; i < P; i += nth)
+        __hip_atomic_fetch_add(&cnt[ids[i]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t acc = 0;
+        for (uint32_t e = 0; e < E; ++e) {
+            base[e] = acc;
+            acc += (cnt[e] + kMoeMaxTokens - 1u) / kMoeMaxTokens;
+        }
+        base[E] = acc;
+    }
+    __syncthreads();
+    ActiveExpert* ent = ws_ptr<ActiveExpert>(w, w.off_active);
+    MoeExpert* gw = ws_ptr<MoeExpert>(w, w.off_gweights);
+    CombineEntry* comb = ws_ptr<CombineEntry>(w, w.off_combine);
+    const bool deepseek = s.semantics == kSemDeepseek, qwen = s.semantics == kSemQwen;
+    // One thread per expert walks the assignments in order: ranks follow ascending tokens.
+    for (uint32_t e = tid; e < E; e += nth) {
+        const uint32_t n = cnt[e];
+        if (n == 0) continue;
+        const MoeExpert ex = in.experts[e];
+        uint32_t r = 0;
+        for (uint32_t p = 0; p < P && r < n; ++p) {
+            if (ids[p] != e) continue;
+            const uint32_t t = p / K, k = p - t * K;
+            const uint32_t a = base[e] + r / kMoeMaxTokens, sl = r % kMoeMaxTokens;
+            ActiveExpert* A = ent + a;
+            const float wt = *gp(rwt + p);
+            *gp(&A->tok[sl]) = t;
+            *gp(&A->route_w[sl]) = wt;
+            if (sl == 0) {
+                *gp(&A->expert) = e;
+                *gp(&A->ntok) = n - r < kMoeMaxTokens ? n - r : kMoeMaxTokens;
+                *gp(&A->apply_w) = deepseek ? 1u : 0u;
+                *gp(&A->limit) = s.routed_limit;
+                gw[a] = ex;
+            }
+            uint32_t at = k;
+            if (deepseek) {
+                at = 0;
+                for (uint32_t k2 = 0; k2 < K; ++k2) at += ids[t * K + k2] < e ? 1u : 0u;
+            }
+            uint32_t* ce = reinterpret_cast<uint32_t*>(comb + (uint64_t)t * (K + 1u) + at);
+            *gp(ce) = (a << 3) | sl;
+            *gp(ce + 1) = __float_as_uint(qwen ? wt : 1.0f);
+            ++r;
+        }
+    }
+    const uint32_t routed_groups = base[E];
+    if (s.has_shared) {
+        const MoeExpert ex = in.experts[E];
+        for (uint32_t t = tid; t < T; t += nth) {
+            const uint32_t a = routed_groups + t / kMoeMaxTokens, sl = t % kMoeMaxTokens;
+            ActiveExpert* A = ent + a;
+            *gp(&A->tok[sl]) = t;
+            *gp(&A->route_w[sl]) = 1.0f;
+            if (sl == 0) {
+                *gp(&A->expert) = E;
+                *gp(&A->ntok) = T - t < kMoeMaxTokens ? T - t : kMoeMaxTokens;
+                *gp(&A->apply_w) = 0u;
+                *gp(&A->limit) = s.shared_limit;
+                gw[a] = ex;
+            }
+            uint32_t* ce = reinterpret_cast<uint32_t*>(comb + (uint64_t)t * (K + 1u) + K);
+            *gp(ce) = (a << 3) | sl;
+            *gp(ce + 1) = __float_as_uint(1.0f);
+        }
+    }
+    if (tid == 0) {
+        const bool bad = (load_shared_u32(&hdr->status) & kStatusBadRoute) != 0;
+        const uint32_t total = routed_groups + (s.has_shared ? (T + kMoeMaxTokens - 1u) / kMoeMaxTokens : 0u);
+        *gp(&hdr->n_active) = bad ? 0u : total;
+        if (any_nonfinite) or_bits(&hdr->status, kStatusNonFiniteInput);
+    }
+}
+
+// Dynamic LDS of the grouped stream kernels, from byte 0: decode tables, then per group the
+// weight pointers (nptr of them), the token ids (u16 x kMoeMaxTokens) and the token count, then
+// (down) the 2^-e scales of the staged groups' h blocks.
+struct GroupLds {
+    uint32_t wptr, tok, ntok, scale, bytes;
+};
+__host__ __device__ inline GroupLds group_lds(uint32_t table_bytes, uint32_t groups, uint32_t nptr,
+                                              uint32_t scale_bytes) {
+    GroupLds l;
+    l.wptr = (table_bytes + 15u) & ~15u;
+    l.tok = l.wptr + groups * nptr * 8u;
+    l.ntok = l.tok + groups * kMoeMaxTokens * 2u;
+    l.scale = (l.ntok + groups * 4u + 15u) & ~15u;
+    l.bytes = l.scale + scale_bytes;
+    return l;
+}
+
+// Copies the group list's pointers (gate/up or down), token ids and counts into LDS.
+__device__ __forceinline__ void stage_groups(const MoeWorkspace& w, uint32_t n, const GroupLds& lay,
+                                             bool down, uint8_t* lds) {
+    const ActiveExpert* ent = ws_ptr<const ActiveExpert>(w, w.off_active);
+    const MoeExpert* gw = ws_ptr<const MoeExpert>(w, w.off_gweights);
+    uint64_t* wp = reinterpret_cast<uint64_t*>(lds + lay.wptr);
+    uint16_t* tok = reinterpret_cast<uint16_t*>(lds + lay.tok);
+    uint32_t* ntok = reinterpret_cast<uint32_t*>(lds + lay.ntok);
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const MoeExpert ex = gw[i];
+        if (down) {
+            wp[i] = reinterpret_cast<uint64_t>(ex.down);
+        } else {
+            wp[2u * i] = reinterpret_cast<uint64_t>(ex.gate);
+            wp[2u * i + 1u] = reinterpret_cast<uint64_t>(ex.up);
+        }
+        const uint32_t nt = *gp(&ent[i].ntok);
+        ntok[i] = nt;
+        for (uint32_t k = 0; k < kMoeMaxTokens; ++k)
+            tok[i * kMoeMaxTokens + k] = (uint16_t)(k < nt ? *gp(&ent[i].tok[k]) : 0u);
+    }
+}
+
+template <uint32_t FMT>
+struct GateUpGrouped {
+    static constexpr int NT = kMoeMaxTokens;
+    uint32_t chunks, nmat, ng;
+    ASrc<false, 0> as;
+    float hscale;
+    MoeShape s;
+    MoeWorkspace w;
+    vl_tiled_layout L;
+    uint32_t tiles, UJ, TU, NW, wid;
+    uint32_t wptr_off, tok_off, ntok_off;
+    uint32_t ntok;
+    uint32_t tok[NT];
+
+    __device__ TileRef tref(uint32_t j, uint32_t mat) const {
+        const uint32_t a = j / tiles, t = j - a * tiles;
+        const uint64_t p = lds_load<uint64_t>(wptr_off + (2u * a + mat) * 8u);
+        return tile_ref<FMT>(L, uni_ptr(reinterpret_cast<const uint8_t*>(p)), t);
+    }
+
+    __device__ void job_begin(uint32_t j) {
+        const uint32_t a = j / tiles;
+        ntok = uni(lds_load<uint32_t>(ntok_off + 4u * a));
+        const uint32_t tb = tok_off + 2u * NT * a;
+#pragma unroll
+        for (int s2 = 0; s2 < NT; ++s2) tok[s2] = uni(lds_load<uint16_t>(tb + 2u * s2));
+        const uint32_t m = threadIdx.x & 31u, kh = (threadIdx.x >> 5) & 1u;
+        const uint32_t sl = a_slot(m), limb = a_limb(m);
+        const uint32_t tk = lds_load<uint16_t>(tb + 2u * (sl < ntok ? sl : 0u));
+        as.ptr = ws_ptr<int8_t>(w, w.off_xlimbs) + (uint64_t)tk * 128u + limb * 32u + 16u * kh;
+    }
+
+    __device__ void scales(uint32_t, uint32_t c, float (&fs)[NT]) const {
+        const uint32_t eb = FMT == VL_TYPE_Q8_0 ? c / 2u : c;
+        const int* xe = ws_ptr<const int>(w, w.off_xexp) + (uint64_t)eb * w.estride;
+#pragma unroll
+        for (int s2 = 0; s2 < NT; ++s2)
+            fs[s2] = (uint32_t)s2 < ntok ? __builtin_amdgcn_ldexpf(1.0f, -*gp(xe + tok[s2])) : 0.0f;
+    }
+
+    __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&m1)[NT]) const {
+        const uint32_t lane = threadIdx.x & 63u;
+        constexpr uint32_t RF = 2u * NT * 64u;
+        float* rec = ws_ptr<float>(w, w.off_rec_gu);
+        float* r = rec + (uint64_t)(wid + j) * RF;
+#pragma unroll
+        for (int s2 = 0; s2 < NT; ++s2) {
+            store_shared(r + s2 * 64u + lane, m0[s2]);
+            store_shared(r + (NT + s2) * 64u + lane, m1[s2]);
+        }
+        const uint32_t first = wave_of_unit(j * UJ, NW, TU);
+        const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
+        const MoeCounters cn = counters_of(w);
+        if (!arrive(cn.gu + j, last - first + 1u)) return;
+        gateup_fixup<NT>(rec, ws_ptr<float>(w, w.off_h), cn.hmax,
+                         &ws_ptr<MoeHeader>(w, w.off_header)->status, j, first, last, tiles,
+                         w.hblocks, s.inter, s.semantics, 0u, ws_ptr<const ActiveExpert>(w, w.off_active));
+    }
+};
+
+template <uint32_t FMT>
+__global__ void __launch_bounds__(kStreamThreads) k_moe_gateup_grouped(const MoeShape s, const MoeInputs in,
+                                                                       const MoeWorkspace w) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int NT = kMoeMaxTokens;
+    const uint32_t n = uni(*gp(&ws_ptr<const MoeHeader>(w, w.off_header)->n_active));
+    const GroupLds lay = group_lds(table_bytes<FMT>(), w.max_active, 2u, 0u);
+    fill_tables<FMT>(lds);
+    stage_groups(w, n, lay, false, lds);
+    __syncthreads();
+    if (n == 0) return;
+    GateUpGrouped<FMT> pol;
+    pol.s = s;
+    pol.w = w;
+    vl_make_layout(FMT, s.inter, s.width, &pol.L);
+    pol.chunks = units_per_row(FMT, s.width);
+    pol.nmat = 2;
+    pol.ng = pol.L.groups;
+    pol.tiles = w.tiles_gu;
+    pol.UJ = 2u * pol.chunks;
+    pol.TU = n * w.tiles_gu * pol.UJ;
+    pol.NW = active_waves(gridDim.x * kStreamWaves, pol.TU);
+    pol.wid = blockIdx.x * kStreamWaves + uni(threadIdx.x >> 6);
+    pol.wptr_off = lay.wptr;
+    pol.tok_off = lay.tok;
+    pol.ntok_off = lay.ntok;
+    pol.as.stride = w.xslots * 128u;
+    pol.hscale = (threadIdx.x & 32u) ? 65536.0f : 1.0f;
+    pol.ntok = 0;
+    stream_range<FMT, NT, false>(pol, range_begin(pol.wid, pol.NW, pol.TU),
+                                 range_begin(pol.wid + 1u, pol.NW, pol.TU));
+}
+
+template <uint32_t FMT>
+struct DownGrouped {
+    static constexpr int NT = kMoeMaxTokens;
+    uint32_t chunks, nmat, ng;
+    ASrc<false, NT * 128u> as;
+    float hscale;
+    MoeShape s;
+    MoeInputs in;
+    MoeWorkspace w;
+    uint32_t n_active;
+    vl_tiled_layout L;
+    uint32_t tiles, UJ, TU, NW, wid;
+    uint32_t a0, expert_bytes, scale_off, wptr_off, ntok_off;
+    const int8_t* slab;
+    uint32_t cur_a, ntok;
+
+    __device__ TileRef tref(uint32_t j, uint32_t) const {
+        const uint32_t a = j / tiles, t = j - a * tiles;
+        const uint64_t p = lds_load<uint64_t>(wptr_off + 8u * a);
+        return tile_ref<FMT>(L, uni_ptr(reinterpret_cast<const uint8_t*>(p)), t);
+    }
+
+    __device__ void job_begin(uint32_t j) {
+        cur_a = j / tiles;
+        ntok = uni(lds_load<uint32_t>(ntok_off + 4u * cur_a));
+        const uint32_t m = threadIdx.x & 31u, kh = (threadIdx.x >> 5) & 1u;
+        const uint32_t sl = a_slot(m), limb = a_limb(m);
+        as.ptr = slab + (uint64_t)(cur_a - a0) * expert_bytes + (sl < ntok ? sl : 0u) * 128u + limb * 32u + 16u * kh;
+    }
+
+    __device__ void scales(uint32_t, uint32_t c, float (&fs)[NT]) const {
+        const uint32_t eb = FMT == VL_TYPE_Q8_0 ? c / 2u : c;
+        const uint32_t sc = scale_off + 32u * ((cur_a - a0) * w.hblocks + eb);
+#pragma unroll
+        for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? lds_load<float>(sc + 4u * s2) : 0.0f;
+    }
+
+    __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&)[NT]) const {
+        const uint32_t lane = threadIdx.x & 63u;
+        constexpr uint32_t RF = NT * 64u;
+        float* rec = ws_ptr<float>(w, w.off_rec_dn);
+        float* r = rec + (uint64_t)(wid + j) * RF;
+#pragma unroll
+        for (int s2 = 0; s2 < NT; ++s2) store_shared(r + s2 * 64u + lane, m0[s2]);
+        const uint32_t first = wave_of_unit(j * UJ, NW, TU);
+        const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
+        const MoeCounters cn = counters_of(w);
+        if (!arrive(cn.dn + j, last - first + 1u)) return;
+        down_fixup<NT>(rec, ws_ptr<float>(w, w.off_ypart), in.out, nullptr,
+                       &ws_ptr<MoeHeader>(w, w.off_header)->status, j, first, last, tiles, n_active,
+                       s.width, s.tokens, s.top_k, s.has_shared, s.semantics,
+                       uni(lds_load<uint32_t>(ntok_off + 4u * (j / tiles))), 0u);
+    }
+};
+
+template <uint32_t FMT>
+__global__ void __launch_bounds__(kStreamThreads) k_moe_down_grouped(const MoeShape s, const MoeInputs in,
+                                                                     const MoeWorkspace w) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int NT = kMoeMaxTokens;
+    const uint32_t n_active = uni(*gp(&ws_ptr<const MoeHeader>(w, w.off_header)->n_active));
+    const uint32_t tiles = w.tiles_dn, UJ = units_per_row(FMT, s.inter);
+    const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * kStreamWaves, TU);
+    const uint32_t ub0 = range_begin(blockIdx.x * kStreamWaves, NW, TU);
+    const uint32_t ub1 = range_begin((blockIdx.x + 1u) * kStreamWaves, NW, TU);
+    const uint32_t a0 = ub0 < ub1 ? (ub0 / UJ) / tiles : 0u;
+    const uint32_t a1 = ub0 < ub1 ? ((ub1 - 1u) / UJ) / tiles : 0u;
+    const uint32_t eb = down_expert_bytes(s.inter, NT);
+    const GroupLds lay = group_lds(table_bytes<FMT>(), w.max_active, 1u, w.stage * w.hblocks * 32u);
+    int8_t* slab = ws_ptr<int8_t>(w, w.off_hslab) + (uint64_t)blockIdx.x * w.stage * eb;
+    fill_tables<FMT>(lds);
+    stage_groups(w, n_active, lay, true, lds);
+    __syncthreads();
+    if (ub0 < ub1)
+        convert_h<NT>(w, s.inter, a0, a1, reinterpret_cast<const uint32_t*>(lds + lay.ntok), 1u, slab,
+                      reinterpret_cast<float*>(lds + lay.scale));
+    __syncthreads();
+    if (n_active == 0) return;
+    DownGrouped<FMT> pol;
+    pol.s = s;
+    pol.in = in;
+    pol.w = w;
+    pol.n_active = n_active;
+    vl_make_layout(FMT, s.width, s.inter, &pol.L);
+    pol.chunks = UJ;
+    pol.nmat = 1;
+    pol.ng = pol.L.groups;
+    pol.tiles = tiles;
+    pol.UJ = UJ;
+    pol.TU = TU;
+    pol.NW = NW;
+    pol.wid = blockIdx.x * kStreamWaves + uni(threadIdx.x >> 6);
+    pol.a0 = a0;
+    pol.expert_bytes = eb;
+    pol.scale_off = lay.scale;
+    pol.wptr_off = lay.wptr;
+    pol.ntok_off = lay.ntok;
+    pol.slab = slab;
+    pol.hscale = (threadIdx.x & 32u) ? 65536.0f : 1.0f;
+    pol.cur_a = 0;
+    pol.ntok = 0;
+    stream_range<FMT, NT, false>(pol, range_begin(pol.wid, NW, TU), range_begin(pol.wid + 1u, NW, TU));
+}
+
+// out[t][r]: token t's expert rows added in its combine order (zero when the layer was refused).
+__global__ void __launch_bounds__(256) k_moe_combine(const MoeShape s, const MoeInputs in,
+                                                     const MoeWorkspace w) {
+    constexpr uint32_t NT = kMoeMaxTokens;
+    const uint32_t H = s.width, K = s.top_k, nent = K + (s.has_shared ? 1u : 0u);
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const MoeHeader* hdr = ws_ptr<const MoeHeader>(w, w.off_header);
+    const uint32_t n_active = *gp(&hdr->n_active);
+    bool bad = false;
+    if (i < (uint64_t)s.tokens * H) {
+        const uint32_t t = (uint32_t)(i / H), r = (uint32_t)(i - (uint64_t)t * H);
+        float acc = 0.0f;
+        if (n_active) {
+            const CombineEntry* ce = ws_ptr<const CombineEntry>(w, w.off_combine) + (uint64_t)t * (K + 1u);
+            const float* yp = ws_ptr<const float>(w, w.off_ypart);
+            for (uint32_t k = 0; k < nent; ++k) {
+                const uint32_t src = *gp(&ce[k].src);
+                const float y = *gp(yp + ((uint64_t)(src >> 3) * NT + (src & 7u)) * H + r);
+                acc = (s.semantics == kSemQwen && k < K) ? __fadd_rn(acc, __fmul_rn(y, *gp(&ce[k].w)))
+                                                         : __fadd_rn(acc, y);
+            }
+        }
+        bad = !isfinite(acc);
+        *gp(in.out + i) = acc;
+    }
+    if (__any(bad) && (threadIdx.x & 63u) == 0)
+        or_bits(&ws_ptr<MoeHeader>(w, w.off_header)->status, kStatusNonFiniteOutput);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1038,9 +1474,71 @@ static hipError_t launch_down_fmt(const MoeShape& s, const MoeInputs& in, const 
     }
 }
 
+template <uint32_t FMT>
+static hipError_t launch_gateup_grouped(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
+                                        hipStream_t st) {
+    const GroupLds lay = group_lds(table_bytes<FMT>(), w.max_active, 2u, 0u);
+    if (lay.bytes > kLdsBudget) return hipErrorInvalidValue;
+    return launch_stream(k_moe_gateup_grouped<FMT>, w.blocks, lay.bytes, st, s, in, w);
+}
+
+template <uint32_t FMT>
+static hipError_t launch_down_grouped(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
+                                      hipStream_t st) {
+    const GroupLds lay = group_lds(table_bytes<FMT>(), w.max_active, 1u, w.stage * w.hblocks * 32u);
+    if (lay.bytes > kLdsBudget) return hipErrorInvalidValue;
+    return launch_stream(k_moe_down_grouped<FMT>, w.blocks, lay.bytes, st, s, in, w);
+}
+
+// Routing, planning, gate/up, down and combine of the grouped path.
+static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
+                                     hipStream_t st, hipEvent_t* ev) {
+    auto mark = [&](uint32_t stage) {
+        if (ev) (void)hipEventRecord(ev[stage], st);
+    };
+    mark(kStageRouter);
+    const uint32_t router_blocks = s.routing == kRouteGiven ? 1u : s.experts;
+    const uint32_t groups = (s.tokens + kMoeMaxTokens - 1u) / kMoeMaxTokens;
+    hipLaunchKernelGGL(k_moe_router, dim3(router_blocks > w.xblocks ? router_blocks : w.xblocks, groups),
+                       dim3(256), 0, st, s, in, w);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_moe_route_many, dim3((s.tokens + kStreamWaves - 1u) / kStreamWaves),
+                       dim3(kStreamThreads), 0, st, s, in, w);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const uint32_t plan_shm = plan_lds_bytes(s);
+    if ((e = ensure_dynamic_lds((const void*)k_moe_plan, plan_shm)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(kStreamThreads), plan_shm, st, s, in, w);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    mark(kStageGateUp);
+    switch (s.gate_type) {
+        case VL_TYPE_IQ2_XXS: e = launch_gateup_grouped<VL_TYPE_IQ2_XXS>(s, in, w, st); break;
+        case VL_TYPE_IQ3_XXS: e = launch_gateup_grouped<VL_TYPE_IQ3_XXS>(s, in, w, st); break;
+        case VL_TYPE_IQ1_S: e = launch_gateup_grouped<VL_TYPE_IQ1_S>(s, in, w, st); break;
+        case VL_TYPE_Q8_0: e = launch_gateup_grouped<VL_TYPE_Q8_0>(s, in, w, st); break;
+        default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+    mark(kStageDown);
+    switch (s.down_type) {
+        case VL_TYPE_IQ2_XXS: e = launch_down_grouped<VL_TYPE_IQ2_XXS>(s, in, w, st); break;
+        case VL_TYPE_IQ3_XXS: e = launch_down_grouped<VL_TYPE_IQ3_XXS>(s, in, w, st); break;
+        case VL_TYPE_IQ1_S: e = launch_down_grouped<VL_TYPE_IQ1_S>(s, in, w, st); break;
+        case VL_TYPE_Q8_0: e = launch_down_grouped<VL_TYPE_Q8_0>(s, in, w, st); break;
+        default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+    const uint64_t outs = (uint64_t)s.tokens * s.width;
+    hipLaunchKernelGGL(k_moe_combine, dim3((uint32_t)((outs + 255u) / 256u)), dim3(256), 0, st, s, in, w);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    mark(kStageCount);
+    return hipSuccess;
+}
+
 hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
                       hipStream_t st, hipEvent_t* ev) {
     if (!moe_shape_ok(s) || w.blocks == 0) return hipErrorInvalidValue;
+    if (w.grouped) return launch_moe_grouped(s, in, w, st, ev);
     auto mark = [&](uint32_t stage) {
         if (ev) (void)hipEventRecord(ev[stage], st);
     };

@@ -284,16 +284,19 @@ __device__ __forceinline__ uint32_t a_slot(uint32_t m) { return 2u * (m / 8u) + 
 __device__ __forceinline__ uint32_t a_limb(uint32_t m) { return 2u * ((m / 4u) % 2u) + m % 2u; }
 
 // Limb source of one lane: activation limbs are stored [group][slot][4 limbs][32 columns], so
-// consecutive groups of one (slot, limb) row are STRIDE = slots * 128 bytes apart. Lanes whose
-// token slot is unused read slot 0's row: their products land in result registers of unused
-// slots (scaled by 0) or in registers that are never read, so every lane has the same stride.
+// consecutive groups of one (slot, limb) row are STRIDE = slots * 128 bytes apart (STRIDE 0:
+// the run-time `stride`, for token counts known only at launch). Lanes whose token slot is
+// unused read slot 0's row: their products land in result registers of unused slots (scaled by
+// 0) or in registers that are never read, so every lane has the same stride.
 template <bool LDS, uint32_t STRIDE>
 struct ASrc {
     const int8_t* ptr;  // global source (LDS == false)
     uint32_t off;       // LDS byte address (LDS == true)
+    uint32_t stride;    // bytes between groups when STRIDE == 0
     __device__ __forceinline__ i32x4 load(uint32_t G) const {
-        if (LDS) return lds_load<i32x4>(off + G * STRIDE);
-        return *gp(reinterpret_cast<const i32x4*>(ptr + (uint64_t)G * STRIDE));
+        const uint32_t st = STRIDE ? STRIDE : stride;
+        if (LDS) return lds_load<i32x4>(off + G * st);
+        return *gp(reinterpret_cast<const i32x4*>(ptr + (uint64_t)G * st));
     }
 };
 
@@ -303,9 +306,8 @@ struct ASrc {
 
 // df: weight factor of the lane's row for the unit (d times the format factor, times 65536 in
 // the high-limb half); fs[s]: 2^-e of slot s for the unit's exponent block.
-template <uint32_t FMT, int NT, bool LDS>
-__device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint32_t ng,
-                                              const ASrc<LDS, NT * 128u>& as,
+template <uint32_t FMT, int NT, typename AS>
+__device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint32_t ng, const AS& as,
                                               float hscale, const float (&fs)[NT], float (&accf)[NT]) {
     const uint32_t lane = threadIdx.x & 63u;
     const int hh = (int)(lane >> 5);
@@ -478,20 +480,20 @@ __device__ __forceinline__ int limb_exponent(float m) {
     return m > 0.0f ? 30 - q : 0;
 }
 
-// One wave per token: limbs of columns [256 xb, 256 xb + 256) of token t of x ([tokens][cols],
-// token stride x_stride) into xl ([cols/32][slots][4][32]), the block's exponent into
-// xe[8 xb + t] and a non-finite flag into flags[8 xb + t] (written whatever its value).
-// cols is a multiple of 32.
+// One wave per token t in [t0, t1): limbs of columns [256 xb, 256 xb + 256) of token t of x
+// ([tokens][cols], token stride x_stride) into xl ([cols/32][slots][4][32]), the block's exponent
+// into xe[estride xb + t] and a non-finite flag into flags[estride xb + t] (written whatever its
+// value). cols is a multiple of 32.
 __device__ __forceinline__ void prep_x_block(const float* __restrict__ x, uint64_t x_stride,
-                                             uint32_t cols, uint32_t tokens, uint32_t slots,
-                                             uint32_t xb, int8_t* __restrict__ xl,
+                                             uint32_t cols, uint32_t t0, uint32_t t1, uint32_t slots,
+                                             uint32_t estride, uint32_t xb, int8_t* __restrict__ xl,
                                              int* __restrict__ xe, uint32_t* __restrict__ flags) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const uint32_t col = xb * 256u + lane * 4u;
-    for (uint32_t t = wave; t < tokens; t += nwaves) {
+    for (uint32_t t = t0 + wave; t < t1; t += nwaves) {
         float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (col < cols) {
-            const float4 f = ld_f4(x + t * x_stride + col);
+            const float4 f = ld_f4(x + (uint64_t)t * x_stride + col);
             v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
         }
         bool finite = true;
@@ -505,8 +507,8 @@ __device__ __forceinline__ void prep_x_block(const float* __restrict__ x, uint64
         const bool all_finite = __all(finite);
         const int e = limb_exponent(m);
         if (lane == 0) {
-            *gp(xe + 8u * xb + t) = e;
-            *gp(flags + 8u * xb + t) = all_finite ? 0u : 1u;
+            *gp(xe + estride * xb + t) = e;
+            *gp(flags + estride * xb + t) = all_finite ? 0u : 1u;
         }
         if (col < cols) {
             uint32_t packed[4];
@@ -575,7 +577,7 @@ __device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1)
             const uint32_t uu = u + k;
             if (uu < u1) {
                 pol.scales(pj, pc, fs);
-                process_chunk<FMT, NT, LDS>(buf[k], pc, pol.ng, pol.as, pol.hscale, fs, acc);
+                process_chunk<FMT, NT>(buf[k], pc, pol.ng, pol.as, pol.hscale, fs, acc);
             }
             load_chunk<FMT>(htr, hc, pol.ng, buf[k]);
             head_next();

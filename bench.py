@@ -40,9 +40,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--workload", default="iq2_moe",
-                   choices=["q8_expert", "q8_moe", "iq2_moe", "mixed_moe"])
-    p.add_argument("--layers", type=int, default=6,
-                   help="layer instances rotated between steps (defeats caching of weights)")
+                   choices=["q8_expert", "q8_moe", "iq2_moe", "grouped_moe"])
+    p.add_argument("--layers", type=int, default=None,
+                   help="layer instances rotated between steps (defeats caching of weights); "
+                        "default 6, or 2 for the grouped workload")
     p.add_argument("--token-pool", type=int, default=64)
     p.add_argument("--profile-steps", type=int, default=100)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -79,7 +80,7 @@ def token_pool(wl, count: int) -> np.ndarray:
     """The workload's own tokens first, then further seeded N(0, 1) tokens."""
     base = wl.x()
     rng = np.random.Generator(np.random.PCG64(np.random.SeedSequence([wl.seed, 2, 1])))
-    extra = rng.standard_normal((max(0, count - base.shape[0]) * wl.tokens, wl.width))
+    extra = rng.standard_normal((max(0, count * wl.tokens - base.shape[0]), wl.width))
     pool = np.concatenate([base, extra.astype(np.float32)])
     return pool[: count * wl.tokens].reshape(count, wl.tokens, wl.width)
 
@@ -92,8 +93,8 @@ def build_layers(wl, instances: int):
     experts = [wl.expert(e) for e in range(wl.experts)]
     shared = wl.shared()
     sem = _lib.SEM_QWEN if wl.semantics == "qwen" else _lib.SEM_DEEPSEEK
-    routing = {"softmax": _lib.ROUTE_SOFTMAX, "single": _lib.ROUTE_GIVEN}.get(
-        wl.routing, _lib.ROUTE_LEARNED)
+    routing = {"softmax": _lib.ROUTE_SOFTMAX, "single": _lib.ROUTE_GIVEN,
+               "zipf_table": _lib.ROUTE_TABLE}.get(wl.routing, _lib.ROUTE_LEARNED)
     router = torch.from_numpy(wl.router())
     layers = []
     for _ in range(instances):
@@ -142,17 +143,24 @@ def cpu_baseline(wl, experts, shared, pool, seconds: float) -> dict:
             h = h.astype(np.float32)
         return matvec(e.down_type, e.down, H, F, h)
 
+    table = wl.zipf_table() if wl.routing == "zipf_table" else None
+    # Tokens are independent: the sample is whole tokens of the layer, and the time per layer
+    # is the time per token times the layer's tokens.
     done, t0 = 0, time.perf_counter()
     while True:
-        x = pool[done % len(pool)]
-        for t in range(wl.tokens):
-            xt = x[t]
-            if wl.routing == "single":
-                expert(experts[0], xt, None)
-                continue
+        batch = done // wl.tokens
+        t = done % wl.tokens
+        xt = pool[batch % len(pool)][t]
+        if wl.routing == "single":
+            expert(experts[0], xt, None)
+        else:
             logits = orc.linear_f64(router, xt, wl.experts)
             if wl.routing == "softmax":
                 ids, w = orc.route_softmax(logits[0], wl.top_k, True)
+            elif table is not None:
+                ids, w = orc.route_hash(logits, np.zeros(1, np.uint32), table[t:t + 1],
+                                        wl.top_k, wl.route_scale, wl.score_fn)
+                ids, w = ids[0], w[0]
             else:
                 ids, w = orc.route_learned(logits, None, wl.top_k, 1.0, wl.score_fn)
                 ids, w = ids[0], w[0]
@@ -163,22 +171,31 @@ def cpu_baseline(wl, experts, shared, pool, seconds: float) -> dict:
             if shared is not None:
                 out += expert(shared, xt, None)
         done += 1
-        if time.perf_counter() - t0 >= seconds:
+        if time.perf_counter() - t0 >= seconds and done % min(wl.tokens, 8) == 0:
             break
     elapsed = time.perf_counter() - t0
+    per_layer = elapsed / done * wl.tokens
     layer_bytes = layer_weight_bytes(wl)
-    return {"value": round(layer_bytes * done / elapsed / 1e9, 4), "unit": "GB/s",
+    return {"value": round(layer_bytes / per_layer / 1e9, 4), "unit": "GB/s",
             "cores": threads, "kind": kind,
-            "us_per_layer": round(elapsed / done * 1e6, 1),
-            "sample": f"{done} layer(s) of the {wl.name} workload, {wl.tokens} token(s) each, "
+            "us_per_layer": round(per_layer * 1e6, 1),
+            "sample": f"{done} token(s) of the {wl.name} workload ({wl.tokens} per layer), "
                       f"{elapsed:.1f} s on {threads} thread(s) of {os.cpu_count()} logical CPUs"}
 
 
+def routed_experts(wl) -> int:
+    """Distinct routed experts one layer call reads."""
+    if wl.routing == "single":
+        return 1
+    if wl.tokens == 1:
+        return wl.top_k
+    if wl.routing == "zipf_table":
+        return int(np.unique(wl.zipf_table()).size)
+    raise ValueError("per-layer bytes depend on the activations for this multi-token workload")
+
+
 def layer_weight_bytes(wl) -> int:
-    routed = 1 if wl.routing == "single" else min(wl.experts, wl.tokens * wl.top_k)
-    if wl.tokens > 1:
-        raise ValueError("per-layer bytes depend on routing for multi-token workloads")
-    return (routed + (1 if wl.has_shared else 0)) * wl.expert_bytes()
+    return (routed_experts(wl) + (1 if wl.has_shared else 0)) * wl.expert_bytes()
 
 
 def main() -> int:
@@ -195,14 +212,20 @@ def main() -> int:
     from vastloom_amd.workloads import workload
 
     wl = workload(args.workload)
-    if wl.tokens != 1:
-        print("bench.py times single-token layers; use the parity tests for multi-token workloads",
+    if wl.tokens != 1 and wl.routing != "zipf_table":
+        print("bench.py times single-token layers and the table-routed grouped workload",
               file=sys.stderr)
         return 2
+    if args.layers is None:
+        args.layers = 6 if wl.tokens == 1 else 2
+    if wl.tokens > 1:
+        args.token_pool = min(args.token_pool, 4)
     t_build = time.perf_counter()
     experts, shared, layers = build_layers(wl, args.layers)
     pool_host = token_pool(wl, args.token_pool)
     pool = torch.from_numpy(pool_host).cuda()
+    table = (torch.from_numpy(np.ascontiguousarray(wl.zipf_table(), np.uint32)).cuda()
+             if wl.routing == "zipf_table" else None)
     outs = [torch.empty((wl.tokens, wl.width), dtype=torch.float32, device="cuda")
             for _ in range(2)]
     print(f"# built {args.layers} layer instance(s) of {wl.name} in "
@@ -210,7 +233,7 @@ def main() -> int:
 
     def step(i, **kw):
         layer = layers[i % len(layers)]
-        return layer.forward(pool[i % len(pool)], outs[i % 2], check=False, **kw)
+        return layer.forward(pool[i % len(pool)], outs[i % 2], check=False, table_ids=table, **kw)
 
     for i in range(args.warmup):
         step(i)
@@ -242,7 +265,7 @@ def main() -> int:
     layer_bytes = layer_weight_bytes(wl)
     gbs = layer_bytes / (ms_per_step * 1e-3) / 1e9
     # Dominant kernel: the gate/up pass, which reads two matrices of every selected expert.
-    n_exp = (1 if wl.routing == "single" else wl.top_k) + (1 if wl.has_shared else 0)
+    n_exp = routed_experts(wl) + (1 if wl.has_shared else 0)
     H, F = wl.width, wl.intermediate
     from vastloom_amd.workloads import storage_bytes
     gateup_bytes = n_exp * 2 * storage_bytes(wl.gate_type, F, H)
@@ -268,13 +291,17 @@ def main() -> int:
                 "fp16 scales, N(0,0.02) router, N(0,1) tokens)",
         "config": {"workload": f"{wl.name}: DeepSeek-class MoE layer, width {wl.width}, expert "
                                f"width {wl.intermediate}, {wl.experts} routed experts top-"
-                               f"{wl.top_k} + {int(wl.has_shared)} shared, 1 token, sigmoid "
-                               f"router, {TYPE(wl.gate_type)} gate/up, {TYPE(wl.down_type)} down",
+                               f"{wl.top_k} + {int(wl.has_shared)} shared, {wl.tokens} token(s), "
+                               f"{ROUTER_NAME[wl.routing]} router, {TYPE(wl.gate_type)} gate/up, "
+                               f"{TYPE(wl.down_type)} down",
+                   "tokens": wl.tokens, "selected_experts": n_exp,
+                   "tokens_per_s": round(wl.tokens / (ms_per_step * 1e-3), 1),
                    "quantized_bytes_per_layer": layer_bytes,
                    "router_bytes_per_layer": wl.router_bytes(),
                    "layer_instances": args.layers, "token_pool": args.token_pool},
         "stages_us": stage_us,
-        "roofline": {"bound": "hbm", "kernel": "k_moe_gateup", "achieved": round(gateup_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": "k_moe_gateup" if wl.tokens <= 8 else "k_moe_gateup_grouped",
+                     "achieved": round(gateup_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gateup_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
@@ -287,6 +314,10 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(wl, experts, shared, pool_host, args.cpu_seconds)
     print(json.dumps(result))
     return 0
+
+
+ROUTER_NAME = {"learned": "sigmoid", "softmax": "softmax", "single": "no",
+               "zipf_table": "Zipf(1.1) table"}
 
 
 def TYPE(t: int) -> str:

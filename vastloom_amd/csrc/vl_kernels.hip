@@ -328,7 +328,7 @@ struct Matvec {
 };
 
 template <uint32_t FMT, int NT, bool LDS>
-__global__ void __launch_bounds__(kStreamThreads) k_matvec(vl_tiled_layout L, const uint8_t* W,
+__global__ void __launch_bounds__(stream_threads<NT>()) k_matvec(vl_tiled_layout L, const uint8_t* W,
                                                            uint32_t tokens, float* y, uint8_t* ws,
                                                            MatvecWs m) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -365,8 +365,8 @@ __global__ void __launch_bounds__(kStreamThreads) k_matvec(vl_tiled_layout L, co
     pol.ng = L.groups;
     pol.UJ = pol.chunks;
     pol.TU = L.tiles * pol.UJ;
-    pol.NW = active_waves(gridDim.x * kStreamWaves, pol.TU);
-    pol.wid = blockIdx.x * kStreamWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    pol.NW = active_waves(gridDim.x * stream_waves<NT>(), pol.TU);
+    pol.wid = blockIdx.x * stream_waves<NT>() + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     pol.stage_off = TB;
     pol.scale_off = scale_off;
     pol.lds = lds;
@@ -392,13 +392,13 @@ static hipError_t launch_matvec_nt(const vl_tiled_layout& L, const uint8_t* w, u
         const uint32_t shm = base + stage;
         const hipError_t e = ensure_dynamic_lds((const void*)k_matvec<FMT, NT, true>, shm);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((k_matvec<FMT, NT, true>), dim3(blocks), dim3(kStreamThreads), shm, st,
+        hipLaunchKernelGGL((k_matvec<FMT, NT, true>), dim3(blocks), dim3(stream_threads<NT>()), shm, st,
                            L, w, tokens, y, ws, m);
     } else {
         const uint32_t shm = base;
         const hipError_t e = ensure_dynamic_lds((const void*)k_matvec<FMT, NT, false>, shm);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((k_matvec<FMT, NT, false>), dim3(blocks), dim3(kStreamThreads), shm, st,
+        hipLaunchKernelGGL((k_matvec<FMT, NT, false>), dim3(blocks), dim3(stream_threads<NT>()), shm, st,
                            L, w, tokens, y, ws, m);
     }
     return hipGetLastError();

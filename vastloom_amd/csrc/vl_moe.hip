@@ -709,7 +709,7 @@ __host__ __device__ inline GateUpLds gateup_lds(uint32_t table_bytes, uint32_t s
 }
 
 template <uint32_t FMT, int NT, bool LDS>
-__global__ void __launch_bounds__(kStreamThreads) k_moe_gateup(const MoeShape s, const MoeInputs in,
+__global__ void __launch_bounds__(stream_threads<NT>()) k_moe_gateup(const MoeShape s, const MoeInputs in,
                                                                const MoeWorkspace w) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t TB = table_bytes<FMT>();
@@ -717,13 +717,16 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_gateup(const MoeShape s,
     const GateUpLds lay = gateup_lds(TB, stage_bytes, w.xblocks);
     RouteLds& rt = *reinterpret_cast<RouteLds*>(lds + lay.route);
     const uint8_t** wptr = reinterpret_cast<const uint8_t**>(lds + lay.wptr);
-    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     int nonfinite = 0;
-    if (wave < s.tokens) {
-        // Waves 0..tokens-1 route; the others fill the decode tables and stage the activations.
-        route_token_wave(s, in, w, wave, rt);
-    } else {
-        const uint32_t tid = threadIdx.x - 64u * s.tokens, nthr = blockDim.x - 64u * s.tokens;
+    // Waves 0..tokens-1 route; the others fill the decode tables and stage the activations, or,
+    // when every wave routes, the whole block does so afterwards.
+    const bool fillers = s.tokens < nwaves;
+    if (wave < s.tokens) route_token_wave(s, in, w, wave, rt);
+    if (!fillers) __syncthreads();
+    if (!fillers || wave >= s.tokens) {
+        const uint32_t first = fillers ? s.tokens : 0u;
+        const uint32_t tid = threadIdx.x - 64u * first, nthr = blockDim.x - 64u * first;
         fill_tables<FMT>(lds, tid, nthr);
         if (LDS) {
             const uint4* src = ws_ptr<const uint4>(w, w.off_xlimbs);
@@ -757,8 +760,8 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_gateup(const MoeShape s,
     pol.tiles = w.tiles_gu;
     pol.UJ = 2u * pol.chunks;
     pol.TU = uni(rt.n_active) * w.tiles_gu * pol.UJ;
-    pol.NW = active_waves(gridDim.x * kStreamWaves, pol.TU);
-    pol.wid = blockIdx.x * kStreamWaves + uni(threadIdx.x >> 6);
+    pol.NW = active_waves(gridDim.x * stream_waves<NT>(), pol.TU);
+    pol.wid = blockIdx.x * stream_waves<NT>() + uni(threadIdx.x >> 6);
     pol.stage_off = lay.stage;
     pol.scale_off = lay.scale;
     pol.route_off = lay.route;
@@ -939,16 +942,17 @@ __host__ __device__ inline DownLds down_lds(uint32_t table_bytes, uint32_t stage
 }
 
 template <uint32_t FMT, int NT, bool LDS>
-__global__ void __launch_bounds__(kStreamThreads) k_moe_down(const MoeShape s, const MoeInputs in,
+__global__ void __launch_bounds__(stream_threads<NT>()) k_moe_down(const MoeShape s, const MoeInputs in,
                                                              const MoeWorkspace w) {
     extern __shared__ __align__(16) uint8_t lds[];
     const MoeHeader* hdr = ws_ptr<const MoeHeader>(w, w.off_header);
     const uint32_t n_active = uni(*gp(&hdr->n_active));
     const uint32_t tiles = w.tiles_dn, UJ = units_per_row(FMT, s.inter);
-    const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * kStreamWaves, TU);
+    constexpr uint32_t WV = stream_waves<NT>();
+    const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * WV, TU);
     // Experts this block's units touch.
-    const uint32_t ub0 = range_begin(blockIdx.x * kStreamWaves, NW, TU);
-    const uint32_t ub1 = range_begin((blockIdx.x + 1u) * kStreamWaves, NW, TU);
+    const uint32_t ub0 = range_begin(blockIdx.x * WV, NW, TU);
+    const uint32_t ub1 = range_begin((blockIdx.x + 1u) * WV, NW, TU);
     const uint32_t a0 = ub0 < ub1 ? (ub0 / UJ) / tiles : 0u;
     const uint32_t a1 = ub0 < ub1 ? ((ub1 - 1u) / UJ) / tiles : 0u;
     constexpr uint32_t TB = table_bytes<FMT>();
@@ -995,7 +999,7 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_down(const MoeShape s, c
     pol.UJ = UJ;
     pol.TU = TU;
     pol.NW = NW;
-    pol.wid = blockIdx.x * kStreamWaves + uni(threadIdx.x >> 6);
+    pol.wid = blockIdx.x * WV + uni(threadIdx.x >> 6);
     pol.a0 = a0;
     pol.expert_bytes = eb;
     pol.stage_off = lay.stage;
@@ -1046,9 +1050,10 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_route_many(const MoeShap
     if (bad && lane == 0) or_bits(&ws_ptr<MoeHeader>(w, w.off_header)->status, kStatusBadRoute);
 }
 
-// Dynamic LDS bytes of k_moe_plan: expert counts, group bases, the staged route ids, wave flags.
+// Dynamic LDS bytes of k_moe_plan: expert counts, group bases, the staged route ids, wave flags
+// and one per-expert counter row per wave.
 __host__ __device__ inline uint32_t plan_lds_bytes(const MoeShape& s) {
-    return (2u * s.experts + 1u + s.tokens * s.top_k + kStreamWaves) * 4u;
+    return (2u * s.experts + 1u + s.tokens * s.top_k + kStreamWaves + kStreamWaves * s.experts) * 4u;
 }
 
 // One block: the grouped path's group list (ActiveExpert entries), their weight pointers, every
@@ -1063,17 +1068,35 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_plan(const MoeShape s, c
     uint32_t* base = cnt + E;
     uint32_t* ids = base + E + 1u;
     uint32_t* flags = ids + P;
+    uint32_t* hist = flags + kStreamWaves;  // [wave][E]
+    const uint32_t wave = tid >> 6, lane = tid & 63u, nw = nth >> 6;
+    // Wave w takes tokens [tw0, tw1) in order.
+    const uint32_t tw0 = (uint32_t)((uint64_t)wave * T / nw), tw1 = (uint32_t)((uint64_t)(wave + 1u) * T / nw);
     MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
     const uint32_t* ridx = ws_ptr<const uint32_t>(w, w.off_route_idx);
     const float* rwt = ws_ptr<const float>(w, w.off_route_w);
     for (uint32_t i = tid; i < P; i += nth) ids[i] = *gp(ridx + i);
-    for (uint32_t e = tid; e < E; e += nth) cnt[e] = 0;
+    for (uint32_t i = tid; i < nw * E; i += nth) hist[i] = 0;
     bool nonfinite = false;
     const uint32_t* xf = ws_ptr<const uint32_t>(w, w.off_xflags);
     for (uint32_t i = tid; i < w.xblocks * w.estride; i += nth) nonfinite |= *gp(xf + i) != 0u;
     const bool any_nonfinite = block_any(nonfinite, flags);
-    for (uint32_t i = tid; i < P; i += nth)
-        __hip_atomic_fetch_add(&cnt[ids[i]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    // 1. Per-wave counts of each expert over the wave's tokens (a token's experts are distinct;
+    //    the duplicates of a refused token can only lose increments, which keeps ranks in range).
+    uint32_t* mine = hist + wave * E;
+    for (uint32_t t = tw0; t < tw1; ++t)
+        for (uint32_t k = lane; k < K; k += 64u) ++mine[ids[t * K + k]];
+    __syncthreads();
+    // 2. Per expert: the waves' counts become exclusive offsets; the total is the expert's count.
+    for (uint32_t e = tid; e < E; e += nth) {
+        uint32_t run = 0;
+        for (uint32_t v = 0; v < nw; ++v) {
+            const uint32_t h = hist[v * E + e];
+            hist[v * E + e] = run;
+            run += h;
+        }
+        cnt[e] = run;
+    }
     __syncthreads();
     if (tid == 0) {
         uint32_t acc = 0;
@@ -1088,26 +1111,23 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_plan(const MoeShape s, c
     MoeExpert* gw = ws_ptr<MoeExpert>(w, w.off_gweights);
     CombineEntry* comb = ws_ptr<CombineEntry>(w, w.off_combine);
     const bool deepseek = s.semantics == kSemDeepseek, qwen = s.semantics == kSemQwen;
-    // One thread per expert walks the assignments in order: ranks follow ascending tokens.
-    for (uint32_t e = tid; e < E; e += nth) {
-        const uint32_t n = cnt[e];
-        if (n == 0) continue;
-        const MoeExpert ex = in.experts[e];
-        uint32_t r = 0;
-        for (uint32_t p = 0; p < P && r < n; ++p) {
-            if (ids[p] != e) continue;
-            const uint32_t t = p / K, k = p - t * K;
+    // 3. Each wave walks its tokens in order again: an expert's ranks ascend with the tokens.
+    for (uint32_t t = tw0; t < tw1; ++t) {
+        for (uint32_t k = lane; k < K; k += 64u) {
+            const uint32_t p = t * K + k, e = ids[p];
+            const uint32_t r = mine[e]++;
             const uint32_t a = base[e] + r / kMoeMaxTokens, sl = r % kMoeMaxTokens;
             ActiveExpert* A = ent + a;
             const float wt = *gp(rwt + p);
             *gp(&A->tok[sl]) = t;
             *gp(&A->route_w[sl]) = wt;
             if (sl == 0) {
+                const uint32_t n = cnt[e];
                 *gp(&A->expert) = e;
                 *gp(&A->ntok) = n - r < kMoeMaxTokens ? n - r : kMoeMaxTokens;
                 *gp(&A->apply_w) = deepseek ? 1u : 0u;
                 *gp(&A->limit) = s.routed_limit;
-                gw[a] = ex;
+                gw[a] = in.experts[e];
             }
             uint32_t at = k;
             if (deepseek) {
@@ -1117,7 +1137,6 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_plan(const MoeShape s, c
             uint32_t* ce = reinterpret_cast<uint32_t*>(comb + (uint64_t)t * (K + 1u) + at);
             *gp(ce) = (a << 3) | sl;
             *gp(ce + 1) = __float_as_uint(qwen ? wt : 1.0f);
-            ++r;
         }
     }
     const uint32_t routed_groups = base[E];
@@ -1249,7 +1268,7 @@ struct GateUpGrouped {
 };
 
 template <uint32_t FMT>
-__global__ void __launch_bounds__(kStreamThreads) k_moe_gateup_grouped(const MoeShape s, const MoeInputs in,
+__global__ void __launch_bounds__(stream_threads<kMoeMaxTokens>()) k_moe_gateup_grouped(const MoeShape s, const MoeInputs in,
                                                                        const MoeWorkspace w) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int NT = kMoeMaxTokens;
@@ -1269,8 +1288,8 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_gateup_grouped(const Moe
     pol.tiles = w.tiles_gu;
     pol.UJ = 2u * pol.chunks;
     pol.TU = n * w.tiles_gu * pol.UJ;
-    pol.NW = active_waves(gridDim.x * kStreamWaves, pol.TU);
-    pol.wid = blockIdx.x * kStreamWaves + uni(threadIdx.x >> 6);
+    pol.NW = active_waves(gridDim.x * stream_waves<NT>(), pol.TU);
+    pol.wid = blockIdx.x * stream_waves<NT>() + uni(threadIdx.x >> 6);
     pol.wptr_off = lay.wptr;
     pol.tok_off = lay.tok;
     pol.ntok_off = lay.ntok;
@@ -1337,15 +1356,16 @@ struct DownGrouped {
 };
 
 template <uint32_t FMT>
-__global__ void __launch_bounds__(kStreamThreads) k_moe_down_grouped(const MoeShape s, const MoeInputs in,
+__global__ void __launch_bounds__(stream_threads<kMoeMaxTokens>()) k_moe_down_grouped(const MoeShape s, const MoeInputs in,
                                                                      const MoeWorkspace w) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int NT = kMoeMaxTokens;
     const uint32_t n_active = uni(*gp(&ws_ptr<const MoeHeader>(w, w.off_header)->n_active));
     const uint32_t tiles = w.tiles_dn, UJ = units_per_row(FMT, s.inter);
-    const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * kStreamWaves, TU);
-    const uint32_t ub0 = range_begin(blockIdx.x * kStreamWaves, NW, TU);
-    const uint32_t ub1 = range_begin((blockIdx.x + 1u) * kStreamWaves, NW, TU);
+    constexpr uint32_t WV = stream_waves<NT>();
+    const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * WV, TU);
+    const uint32_t ub0 = range_begin(blockIdx.x * WV, NW, TU);
+    const uint32_t ub1 = range_begin((blockIdx.x + 1u) * WV, NW, TU);
     const uint32_t a0 = ub0 < ub1 ? (ub0 / UJ) / tiles : 0u;
     const uint32_t a1 = ub0 < ub1 ? ((ub1 - 1u) / UJ) / tiles : 0u;
     const uint32_t eb = down_expert_bytes(s.inter, NT);
@@ -1372,7 +1392,7 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_down_grouped(const MoeSh
     pol.UJ = UJ;
     pol.TU = TU;
     pol.NW = NW;
-    pol.wid = blockIdx.x * kStreamWaves + uni(threadIdx.x >> 6);
+    pol.wid = blockIdx.x * WV + uni(threadIdx.x >> 6);
     pol.a0 = a0;
     pol.expert_bytes = eb;
     pol.scale_off = lay.scale;
@@ -1422,11 +1442,11 @@ __global__ void __launch_bounds__(256) k_moe_combine(const MoeShape s, const Moe
 constexpr uint32_t kLdsBudget = 160u * 1024u;
 
 template <typename K, typename... Args>
-static hipError_t launch_stream(K kernel, uint32_t blocks, uint32_t shm, hipStream_t st,
-                                Args... args) {
+static hipError_t launch_stream(K kernel, uint32_t blocks, uint32_t threads, uint32_t shm,
+                                hipStream_t st, Args... args) {
     const hipError_t e = ensure_dynamic_lds((const void*)kernel, shm);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kStreamThreads), shm, st, args...);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(threads), shm, st, args...);
     return hipGetLastError();
 }
 
@@ -1436,9 +1456,9 @@ static hipError_t launch_gateup_nt(const MoeShape& s, const MoeInputs& in, const
     const uint32_t stage = (s.width / 32u) * NT * 128u;
     const GateUpLds staged = gateup_lds(table_bytes<FMT>(), stage, w.xblocks);
     if (staged.bytes <= kLdsBudget)
-        return launch_stream(k_moe_gateup<FMT, NT, true>, w.blocks, staged.bytes, st, s, in, w);
+        return launch_stream(k_moe_gateup<FMT, NT, true>, w.blocks, stream_threads<NT>(), staged.bytes, st, s, in, w);
     const GateUpLds plain = gateup_lds(table_bytes<FMT>(), 0u, w.xblocks);
-    return launch_stream(k_moe_gateup<FMT, NT, false>, w.blocks, plain.bytes, st, s, in, w);
+    return launch_stream(k_moe_gateup<FMT, NT, false>, w.blocks, stream_threads<NT>(), plain.bytes, st, s, in, w);
 }
 
 template <uint32_t FMT>
@@ -1458,9 +1478,9 @@ static hipError_t launch_down_nt(const MoeShape& s, const MoeInputs& in, const M
     const DownLds staged = down_lds(table_bytes<FMT>(), w.stage * down_expert_bytes(s.inter, NT),
                                     w.stage, w.hblocks);
     if (staged.bytes <= kLdsBudget)
-        return launch_stream(k_moe_down<FMT, NT, true>, w.blocks, staged.bytes, st, s, in, w);
+        return launch_stream(k_moe_down<FMT, NT, true>, w.blocks, stream_threads<NT>(), staged.bytes, st, s, in, w);
     const DownLds plain = down_lds(table_bytes<FMT>(), 0u, w.stage, w.hblocks);
-    return launch_stream(k_moe_down<FMT, NT, false>, w.blocks, plain.bytes, st, s, in, w);
+    return launch_stream(k_moe_down<FMT, NT, false>, w.blocks, stream_threads<NT>(), plain.bytes, st, s, in, w);
 }
 
 template <uint32_t FMT>
@@ -1479,7 +1499,7 @@ static hipError_t launch_gateup_grouped(const MoeShape& s, const MoeInputs& in, 
                                         hipStream_t st) {
     const GroupLds lay = group_lds(table_bytes<FMT>(), w.max_active, 2u, 0u);
     if (lay.bytes > kLdsBudget) return hipErrorInvalidValue;
-    return launch_stream(k_moe_gateup_grouped<FMT>, w.blocks, lay.bytes, st, s, in, w);
+    return launch_stream(k_moe_gateup_grouped<FMT>, w.blocks, stream_threads<kMoeMaxTokens>(), lay.bytes, st, s, in, w);
 }
 
 template <uint32_t FMT>
@@ -1487,7 +1507,7 @@ static hipError_t launch_down_grouped(const MoeShape& s, const MoeInputs& in, co
                                       hipStream_t st) {
     const GroupLds lay = group_lds(table_bytes<FMT>(), w.max_active, 1u, w.stage * w.hblocks * 32u);
     if (lay.bytes > kLdsBudget) return hipErrorInvalidValue;
-    return launch_stream(k_moe_down_grouped<FMT>, w.blocks, lay.bytes, st, s, in, w);
+    return launch_stream(k_moe_down_grouped<FMT>, w.blocks, stream_threads<kMoeMaxTokens>(), lay.bytes, st, s, in, w);
 }
 
 // Routing, planning, gate/up, down and combine of the grouped path.

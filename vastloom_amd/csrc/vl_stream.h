@@ -69,9 +69,19 @@ __device__ __forceinline__ T* uni_ptr(T* p) {
     return reinterpret_cast<T*>((hi << 32) | lo);
 }
 
-// Waves per persistent block, and blocks per CU.
+// Waves per persistent block (one block per CU), at most. Kernels with four or more token
+// slots per job run 8 waves per block, so that each wave has 256 registers for its slots'
+// accumulators and MFMA results; the others run 16 waves of 128 registers.
 constexpr uint32_t kStreamWaves = 16;
 constexpr uint32_t kStreamThreads = kStreamWaves * 64;
+template <int NT>
+__host__ __device__ constexpr uint32_t stream_waves() {
+    return NT >= 4 ? 8u : 16u;
+}
+template <int NT>
+__host__ __device__ constexpr uint32_t stream_threads() {
+    return stream_waves<NT>() * 64u;
+}
 
 template <uint32_t FMT>
 __host__ __device__ constexpr uint32_t table_bytes() {
@@ -431,8 +441,7 @@ __device__ __forceinline__ bool block_any(bool v, uint32_t* slots) {
     if ((threadIdx.x & 63u) == 0) slots[threadIdx.x >> 6] = w ? 1u : 0u;
     __syncthreads();
     uint32_t r = 0;
-#pragma unroll
-    for (uint32_t i = 0; i < kStreamWaves; ++i) r |= slots[i];
+    for (uint32_t i = 0; i < (blockDim.x >> 6); ++i) r |= slots[i];
     return r != 0;
 }
 

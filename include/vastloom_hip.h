@@ -50,6 +50,7 @@ typedef enum vl_status {
 #define VL_STATUS_NONFINITE_INPUT 1u
 #define VL_STATUS_NONFINITE_OUTPUT 2u
 #define VL_STATUS_BAD_ROUTE 4u
+#define VL_STATUS_INTERNAL 8u /* a bounded wait inside a single-launch layer timed out */
 
 /* Thread-local message describing the last non-zero status returned on this thread. */
 const char* vl_last_error(void);
@@ -181,6 +182,12 @@ int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes);
  * the layer. Replaces the per-matvec device calls of moe_forward / qwen38_moe_block. */
 int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
                  uint64_t workspace_bytes, void* stream);
+
+/* Whether vl_moe_layer may run a layer as one cooperative launch where that applies (one or two
+ * tokens, one storage type for gate/up and down); process-wide, off by default (on MI355X the
+ * three-kernel sequence is faster). Both ways give bit-identical outputs; the switch exists for
+ * comparison and measurement. No counterpart in the reference. */
+int vl_moe_set_fused(int enabled);
 
 /* Routing chosen by the last vl_moe_layer on this workspace: ids and weights [tokens][top_k]
  * copied to host memory (synchronizes the stream). */

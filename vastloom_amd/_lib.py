@@ -16,7 +16,7 @@ STATUS_NAMES = {
     5: "io_error", 6: "integrity_error", 7: "unsafe_path", 8: "unsupported",
     9: "resource_exhausted", 10: "internal_error", 100: "declined",
 }
-STATUS_NONFINITE_INPUT, STATUS_NONFINITE_OUTPUT, STATUS_BAD_ROUTE = 1, 2, 4
+STATUS_NONFINITE_INPUT, STATUS_NONFINITE_OUTPUT, STATUS_BAD_ROUTE, STATUS_INTERNAL = 1, 2, 4, 8
 
 _lib: C.CDLL | None = None
 
@@ -43,6 +43,7 @@ _SIGNATURES = {
     "vl_moe_workspace": [_P, C.POINTER(_U64)],
     "vl_moe_layer": [_P, _P, _P, _U64, _P],
     "vl_moe_read_routes": [_P, _P, _P, _P, _P],
+    "vl_moe_set_fused": [_I32],
     "vl_timeline_create": [_U32, C.POINTER(C.c_void_p)],
     "vl_timeline_destroy": [_P],
     "vl_moe_layer_profiled": [_P, _P, _P, _U64, _P, _P, _U32],

@@ -149,6 +149,11 @@ int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes) {
     return VL_OK;
 }
 
+int vl_moe_set_fused(int enabled) {
+    vl::set_moe_fused(enabled != 0);
+    return VL_OK;
+}
+
 int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
                  uint64_t workspace_bytes, void* stream) {
     vl::MoeShape s;

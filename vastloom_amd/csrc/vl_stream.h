@@ -489,17 +489,18 @@ __device__ __forceinline__ int limb_exponent(float m) {
     return m > 0.0f ? 30 - q : 0;
 }
 
-// One wave per token t in [t0, t1): limbs of columns [256 xb, 256 xb + 256) of token t of x
-// ([tokens][cols], token stride x_stride) into xl ([cols/32][slots][4][32]), the block's exponent
-// into xe[estride xb + t] and a non-finite flag into flags[estride xb + t] (written whatever its
-// value). cols is a multiple of 32.
-__device__ __forceinline__ void prep_x_block(const float* __restrict__ x, uint64_t x_stride,
-                                             uint32_t cols, uint32_t t0, uint32_t t1, uint32_t slots,
+// One wave: limbs of columns [256 xb, 256 xb + 256) of token t of x ([tokens][cols], token
+// stride x_stride) into xl ([cols/32][slots][4][32]), the block's exponent into xe[estride xb + t]
+// and a non-finite flag into flags[estride xb + t] (written whatever its value). cols is a
+// multiple of 32. The stores are agent-scope (written through to memory), so that blocks of the
+// same launch on other XCDs can read them after a grid barrier.
+__device__ __forceinline__ void prep_x_token(const float* __restrict__ x, uint64_t x_stride,
+                                             uint32_t cols, uint32_t t, uint32_t slots,
                                              uint32_t estride, uint32_t xb, int8_t* __restrict__ xl,
                                              int* __restrict__ xe, uint32_t* __restrict__ flags) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t col = xb * 256u + lane * 4u;
-    for (uint32_t t = t0 + wave; t < t1; t += nwaves) {
+    {
         float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (col < cols) {
             const float4 f = ld_f4(x + (uint64_t)t * x_stride + col);
@@ -516,17 +517,27 @@ __device__ __forceinline__ void prep_x_block(const float* __restrict__ x, uint64
         const bool all_finite = __all(finite);
         const int e = limb_exponent(m);
         if (lane == 0) {
-            *gp(xe + estride * xb + t) = e;
-            *gp(flags + estride * xb + t) = all_finite ? 0u : 1u;
+            store_shared_u32(reinterpret_cast<uint32_t*>(xe + estride * xb + t), (uint32_t)e);
+            store_shared_u32(flags + estride * xb + t, all_finite ? 0u : 1u);
         }
         if (col < cols) {
             uint32_t packed[4];
             limbs4(v, e, packed);
             const uint64_t base = ((uint64_t)(col / 32u) * slots + t) * 128u + (col % 32u);
 #pragma unroll
-            for (int l = 0; l < 4; ++l) *gp(reinterpret_cast<uint32_t*>(xl + base + 32u * l)) = packed[l];
+            for (int l = 0; l < 4; ++l) store_shared_u32(reinterpret_cast<uint32_t*>(xl + base + 32u * l), packed[l]);
         }
     }
+}
+
+// One wave per token t in [t0, t1) of the block: prep_x_token.
+__device__ __forceinline__ void prep_x_block(const float* __restrict__ x, uint64_t x_stride,
+                                             uint32_t cols, uint32_t t0, uint32_t t1, uint32_t slots,
+                                             uint32_t estride, uint32_t xb, int8_t* __restrict__ xl,
+                                             int* __restrict__ xe, uint32_t* __restrict__ flags) {
+    const uint32_t wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    for (uint32_t t = t0 + wave; t < t1; t += nwaves)
+        prep_x_token(x, x_stride, cols, t, slots, estride, xb, xl, xe, flags);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -298,16 +298,21 @@ struct Matvec {
         for (int s = 0; s < NT; ++s) fs[s] = lds_load<float>(scale_off + 4u * (8u * eb + s));
     }
 
-    __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&)[NT]) const {
+    __device__ uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&)[NT], uint32_t& kc) const {
         const uint32_t lane = threadIdx.x & 63u;
         float* rec = reinterpret_cast<float*>(const_cast<uint8_t*>(ws) + m.off_rec);
         float* r = rec + (uint64_t)(wid + j) * (NT * 64u);
 #pragma unroll
         for (int s = 0; s < NT; ++s) store_shared(r + s * 64u + lane, m0[s]);
+        kc = wave_of_unit(j * UJ + UJ - 1u, NW, TU) - wave_of_unit(j * UJ, NW, TU) + 1u;
+        return reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(ws) + m.off_counters) + j;
+    }
+
+    __device__ void fixup(uint32_t j) const {
+        const uint32_t lane = threadIdx.x & 63u;
+        const float* rec = reinterpret_cast<const float*>(ws + m.off_rec);
         const uint32_t first = wave_of_unit(j * UJ, NW, TU);
         const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
-        uint32_t* cnt = reinterpret_cast<uint32_t*>(const_cast<uint8_t*>(ws) + m.off_counters);
-        if (!arrive(cnt + j, last - first + 1u)) return;
         const uint32_t n = lane & 31u, hh = lane >> 5, row = j * 32u + n;
         bool bad = false;
 #pragma unroll
@@ -339,7 +344,7 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_matvec(vl_tiled_layout
     if (LDS) {
         const uint4* src = reinterpret_cast<const uint4*>(ws + m.off_xlimbs);
         uint4* dst = reinterpret_cast<uint4*>(lds + TB);
-        for (uint32_t i = threadIdx.x; i < stage_bytes / 16u; i += blockDim.x) dst[i] = ld_u4(src + i);
+        copy_to_lds(dst, src, stage_bytes / 16u, threadIdx.x, blockDim.x);
     }
     int nonfinite = 0;
     {

@@ -389,6 +389,7 @@ __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* ke
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (lane < K) {
         double sel_sum = 0.0;
+#pragma unroll 8
         for (uint32_t q = 0; q < K; ++q) sel_sum += tk.p[q];
         float wk;
         if (!softmax) {
@@ -488,13 +489,18 @@ __device__ __forceinline__ void build_active(const MoeShape& s, const MoeWorkspa
                                             CombineEntry* comb_lds = nullptr) {
     const uint32_t K = s.top_k, E = s.experts, P = s.tokens * K;
     const uint32_t p = threadIdx.x;
+    // The loops below read LDS words whose loads are independent; unrolling lets several be in
+    // flight at once instead of one latency per word.
     if (p < P) {
         uint32_t first = 1;
-        for (uint32_t q = 0; q < p; ++q) first &= rt.idx[q] != rt.idx[p] ? 1u : 0u;
+        const uint32_t ep = rt.idx[p];
+#pragma unroll 8
+        for (uint32_t q = 0; q < p; ++q) first &= rt.idx[q] != ep ? 1u : 0u;
         rt.first[p] = first;
     }
     __syncthreads();
     bool bad = false;
+#pragma unroll 8
     for (uint32_t t = 0; t < s.tokens; ++t) bad |= rt.bad[t] != 0;
     CombineEntry* comb = ws_ptr<CombineEntry>(w, w.off_combine);
     if (p < P) {
@@ -505,14 +511,14 @@ __device__ __forceinline__ void build_active(const MoeShape& s, const MoeWorkspa
             *gp(ws_ptr<float>(w, w.off_route_w) + p) = wt;
         }
         uint32_t a = 0, slot = 0, ntok = 0, pos = 0;
+#pragma unroll 8
         for (uint32_t q = 0; q < P; ++q) {
             const uint32_t eq = rt.idx[q];
             a += (rt.first[q] && eq < e) ? 1u : 0u;
-            if (eq == e) {
-                ++ntok;
-                if (q < p) ++slot;
-            }
+            ntok += eq == e ? 1u : 0u;
+            slot += (eq == e && q < p) ? 1u : 0u;
         }
+#pragma unroll 8
         for (uint32_t j = 0; j < K; ++j) pos += rt.idx[t * K + j] < e ? 1u : 0u;
         rt.act[a].tok[slot] = t;
         rt.act[a].route_w[slot] = wt;
@@ -533,6 +539,7 @@ __device__ __forceinline__ void build_active(const MoeShape& s, const MoeWorkspa
     }
     if (threadIdx.x == 0) {
         uint32_t n_routed = 0;
+#pragma unroll 8
         for (uint32_t q = 0; q < P; ++q) n_routed += rt.first[q];
         if (s.has_shared) {
             ActiveExpert& sh = rt.act[n_routed];
@@ -782,20 +789,24 @@ struct GateUp {
             fs[s2] = (uint32_t)s2 < ntok ? lds_load<float>(scale_off + 4u * (8u * eb + tok[s2])) : 0.0f;
     }
 
-    __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&m1)[NT]) const {
+    __device__ uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&m1)[NT], uint32_t& kc) const {
         const uint32_t lane = threadIdx.x & 63u;
         constexpr uint32_t RF = 2u * NT * 64u;
-        float* rec = ws_ptr<float>(w, w.off_rec_gu);
-        float* r = rec + (uint64_t)(wid + j) * RF;
+        float* r = ws_ptr<float>(w, w.off_rec_gu) + (uint64_t)(wid + j) * RF;
 #pragma unroll
         for (int s2 = 0; s2 < NT; ++s2) {
             store_shared(r + s2 * 64u + lane, m0[s2]);
             store_shared(r + (NT + s2) * 64u + lane, m1[s2]);
         }
+        kc = wave_of_unit(j * UJ + UJ - 1u, NW, TU) - wave_of_unit(j * UJ, NW, TU) + 1u;
+        return counters_of(w).gu + j;
+    }
+
+    __device__ void fixup(uint32_t j) const {
+        const float* rec = ws_ptr<const float>(w, w.off_rec_gu);
         const uint32_t first = wave_of_unit(j * UJ, NW, TU);
         const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
         const MoeCounters cn = counters_of(w);
-        if (!arrive(cn.gu + j, last - first + 1u)) return;
         gateup_fixup<NT>(rec, ws_ptr<float>(w, w.off_h), cn.hmax,
                          &ws_ptr<MoeHeader>(w, w.off_header)->status, j, first, last, tiles,
                          w.hblocks, s.inter, s.semantics, route_off, nullptr);
@@ -847,7 +858,7 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_gateup(const MoeSh
         if (LDS) {
             const uint4* src = ws_ptr<const uint4>(w, w.off_xlimbs);
             uint4* dst = reinterpret_cast<uint4*>(lds + lay.stage);
-            for (uint32_t i = tid; i < stage_bytes / 16u; i += nthr) dst[i] = ld_u4(src + i);
+            copy_to_lds(dst, src, stage_bytes / 16u, tid, nthr);
         }
         const int* xe = ws_ptr<const int>(w, w.off_xexp);
         const uint32_t* xf = ws_ptr<const uint32_t>(w, w.off_xflags);
@@ -1004,17 +1015,21 @@ struct Down {
         for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? lds_load<float>(sc + 4u * s2) : 0.0f;
     }
 
-    __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&)[NT]) const {
+    __device__ uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&)[NT], uint32_t& kc) const {
         const uint32_t lane = threadIdx.x & 63u;
         constexpr uint32_t RF = NT * 64u;
-        float* rec = ws_ptr<float>(w, w.off_rec_dn);
-        float* r = rec + (uint64_t)(wid + j) * RF;
+        float* r = ws_ptr<float>(w, w.off_rec_dn) + (uint64_t)(wid + j) * RF;
 #pragma unroll
         for (int s2 = 0; s2 < NT; ++s2) store_shared(r + s2 * 64u + lane, m0[s2]);
+        kc = wave_of_unit(j * UJ + UJ - 1u, NW, TU) - wave_of_unit(j * UJ, NW, TU) + 1u;
+        return counters_of(w).dn + j;
+    }
+
+    __device__ void fixup(uint32_t j) const {
+        const float* rec = ws_ptr<const float>(w, w.off_rec_dn);
         const uint32_t first = wave_of_unit(j * UJ, NW, TU);
         const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
         const MoeCounters cn = counters_of(w);
-        if (!arrive(cn.dn + j, last - first + 1u)) return;
         down_fixup<NT>(rec, ws_ptr<float>(w, w.off_ypart), in.out, cn.tile,
                        &ws_ptr<MoeHeader>(w, w.off_header)->status, j, first, last, tiles, n_active,
                        s.width, s.tokens, s.top_k, s.has_shared, s.semantics,
@@ -1560,20 +1575,24 @@ struct GateUpGrouped {
             fs[s2] = (uint32_t)s2 < ntok ? __builtin_amdgcn_ldexpf(1.0f, -*gp(xe + tok[s2])) : 0.0f;
     }
 
-    __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&m1)[NT]) const {
+    __device__ uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&m1)[NT], uint32_t& kc) const {
         const uint32_t lane = threadIdx.x & 63u;
         constexpr uint32_t RF = 2u * NT * 64u;
-        float* rec = ws_ptr<float>(w, w.off_rec_gu);
-        float* r = rec + (uint64_t)(wid + j) * RF;
+        float* r = ws_ptr<float>(w, w.off_rec_gu) + (uint64_t)(wid + j) * RF;
 #pragma unroll
         for (int s2 = 0; s2 < NT; ++s2) {
             store_shared(r + s2 * 64u + lane, m0[s2]);
             store_shared(r + (NT + s2) * 64u + lane, m1[s2]);
         }
+        kc = wave_of_unit(j * UJ + UJ - 1u, NW, TU) - wave_of_unit(j * UJ, NW, TU) + 1u;
+        return counters_of(w).gu + j;
+    }
+
+    __device__ void fixup(uint32_t j) const {
+        const float* rec = ws_ptr<const float>(w, w.off_rec_gu);
         const uint32_t first = wave_of_unit(j * UJ, NW, TU);
         const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
         const MoeCounters cn = counters_of(w);
-        if (!arrive(cn.gu + j, last - first + 1u)) return;
         gateup_fixup<NT>(rec, ws_ptr<float>(w, w.off_h), cn.hmax,
                          &ws_ptr<MoeHeader>(w, w.off_header)->status, j, first, last, tiles,
                          w.hblocks, s.inter, s.semantics, 0u, ws_ptr<const ActiveExpert>(w, w.off_active));
@@ -1650,17 +1669,20 @@ struct DownGrouped {
         for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? lds_load<float>(sc + 4u * s2) : 0.0f;
     }
 
-    __device__ void flush(uint32_t j, const float (&m0)[NT], const float (&)[NT]) const {
+    __device__ uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&)[NT], uint32_t& kc) const {
         const uint32_t lane = threadIdx.x & 63u;
         constexpr uint32_t RF = NT * 64u;
-        float* rec = ws_ptr<float>(w, w.off_rec_dn);
-        float* r = rec + (uint64_t)(wid + j) * RF;
+        float* r = ws_ptr<float>(w, w.off_rec_dn) + (uint64_t)(wid + j) * RF;
 #pragma unroll
         for (int s2 = 0; s2 < NT; ++s2) store_shared(r + s2 * 64u + lane, m0[s2]);
+        kc = wave_of_unit(j * UJ + UJ - 1u, NW, TU) - wave_of_unit(j * UJ, NW, TU) + 1u;
+        return counters_of(w).dn + j;
+    }
+
+    __device__ void fixup(uint32_t j) const {
+        const float* rec = ws_ptr<const float>(w, w.off_rec_dn);
         const uint32_t first = wave_of_unit(j * UJ, NW, TU);
         const uint32_t last = wave_of_unit(j * UJ + UJ - 1u, NW, TU);
-        const MoeCounters cn = counters_of(w);
-        if (!arrive(cn.dn + j, last - first + 1u)) return;
         down_fixup<NT>(rec, ws_ptr<float>(w, w.off_ypart), in.out, nullptr,
                        &ws_ptr<MoeHeader>(w, w.off_header)->status, j, first, last, tiles, n_active,
                        s.width, s.tokens, s.top_k, s.has_shared, s.semantics,

@@ -108,25 +108,65 @@ __host__ __device__ inline uint32_t exp_blocks(uint32_t cols) { return (cols + 2
 template <uint32_t FMT>
 __device__ __forceinline__ void fill_tables(uint8_t* lds, uint32_t tid0 = threadIdx.x,
                                             uint32_t nthr = blockDim.x) {
+    // Eight source loads per thread are issued before their stores, so a thread waits about one
+    // memory latency per eight stores rather than one per store.
+    constexpr int B = 8;
     if (FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_IQ3_XXS) {
         constexpr uint32_t nB = 128u * kTabCopies / 2u, nA = 256u * kTabCopies / 2u;  // uint4 stores
-        for (uint32_t i = tid0; i < nB + nA; i += nthr) {
-            uint64_t v;
-            uint32_t off;
-            if (i < nB) {
-                const uint32_t e = i / (kTabCopies / 2u);
-                v = FMT == VL_TYPE_IQ2_XXS ? g_tables.sign_sel[e] : g_tables.iq3_sel[e];
-                off = kTabB + i * 16u;
-            } else {
-                const uint32_t k = i - nB, e = k / (kTabCopies / 2u);
-                v = FMT == VL_TYPE_IQ2_XXS ? g_tables.iq2_codes[e] : g_tables.iq3_pm[e];
-                off = kTabA + k * 16u;
+        for (uint32_t i0 = tid0; i0 < nB + nA; i0 += B * nthr) {
+            uint64_t v[B];
+#pragma unroll
+            for (int j = 0; j < B; ++j) {
+                const uint32_t i = i0 + j * nthr;
+                v[j] = 0;
+                if (i < nB) v[j] = FMT == VL_TYPE_IQ2_XXS ? g_tables.sign_sel[i / (kTabCopies / 2u)]
+                                                          : g_tables.iq3_sel[i / (kTabCopies / 2u)];
+                else if (i < nB + nA)
+                    v[j] = FMT == VL_TYPE_IQ2_XXS ? g_tables.iq2_codes[(i - nB) / (kTabCopies / 2u)]
+                                                  : g_tables.iq3_pm[(i - nB) / (kTabCopies / 2u)];
             }
-            *reinterpret_cast<uint4*>(lds + off) = make_uint4(lo32(v), hi32(v), lo32(v), hi32(v));
+#pragma unroll
+            for (int j = 0; j < B; ++j) {
+                const uint32_t i = i0 + j * nthr;
+                const uint32_t off = i < nB ? kTabB + i * 16u : kTabA + (i - nB) * 16u;
+                if (i < nB + nA)
+                    *reinterpret_cast<uint4*>(lds + off) = make_uint4(lo32(v[j]), hi32(v[j]), lo32(v[j]), hi32(v[j]));
+            }
         }
     } else if (FMT == VL_TYPE_IQ1_S) {
-        for (uint32_t i = tid0; i < 2048u; i += nthr)
-            reinterpret_cast<uint64_t*>(lds)[i] = g_tables.iq1_codes[i];
+        for (uint32_t i0 = tid0; i0 < 2048u; i0 += B * nthr) {
+            uint64_t v[B];
+#pragma unroll
+            for (int j = 0; j < B; ++j) {
+                const uint32_t i = i0 + j * nthr;
+                v[j] = i < 2048u ? g_tables.iq1_codes[i] : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < B; ++j) {
+                const uint32_t i = i0 + j * nthr;
+                if (i < 2048u) reinterpret_cast<uint64_t*>(lds)[i] = v[j];
+            }
+        }
+    }
+}
+
+// dst[i] = src[i] for i < n (16-byte words, global to LDS) by threads tid0, tid0 + nthr, ...; four
+// loads per thread are in flight before their stores.
+__device__ __forceinline__ void copy_to_lds(uint4* dst, const uint4* src, uint32_t n, uint32_t tid0,
+                                            uint32_t nthr) {
+    constexpr int B = 4;
+    for (uint32_t i0 = tid0; i0 < n; i0 += B * nthr) {
+        uint4 v[B];
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+            const uint32_t i = i0 + j * nthr;
+            if (i < n) v[j] = ld_u4(src + i);
+        }
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+            const uint32_t i = i0 + j * nthr;
+            if (i < n) dst[i] = v[j];
+        }
     }
 }
 
@@ -365,10 +405,12 @@ __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint3
         accf[s] += (df * fs[s]) * ((float)acc[2 * s] + 256.0f * (float)acc[2 * s + 1]);
 }
 
-// Units in flight per wave, by the register size of a chunk.
+// Units in flight per wave. Sixteen waves per CU each with two 2 KiB IQ2_XXS units in flight keep
+// enough bytes moving; deeper rings measured slower on MI355X (more registers, and the CU's
+// oldest waves crowd out the rest), so depth is kept at two except for IQ1_S's small chunks.
 template <uint32_t FMT>
 struct StreamDepth {
-    static constexpr int kValue = FMT == VL_TYPE_IQ2_XXS ? 4 : FMT == VL_TYPE_IQ1_S ? 3 : 2;
+    static constexpr int kValue = FMT == VL_TYPE_IQ1_S ? 3 : 2;
 };
 
 // ------------------------------------------------------------------------------------------
@@ -406,18 +448,20 @@ __device__ __forceinline__ uint32_t load_shared_u32(const uint32_t* p) {
 }
 
 // Sums of a job's records for (slot s, row n) of matrices 0..NM-1: records first..last in order,
-// each record's two lane halves added first. The loads of four records are issued before any of
-// them is used, so a fixup waits about one memory latency per four records.
+// each record's two lane halves added first. The loads of eight records are issued before any of
+// them is used, so a fixup waits about one memory latency per eight records (a job rarely has
+// more contributors than that).
 template <int NT, int NM>
 __device__ __forceinline__ void sum_records(const float* rec, uint32_t rec_floats, uint32_t j,
                                             uint32_t first, uint32_t last, uint32_t s, uint32_t n,
                                             float (&out)[NM]) {
+    constexpr int B = 8;
 #pragma unroll
     for (int m = 0; m < NM; ++m) out[m] = 0.0f;
-    for (uint32_t k0 = first; k0 <= last; k0 += 4u) {
-        float v[4][NM][2];
+    for (uint32_t k0 = first; k0 <= last; k0 += B) {
+        float v[B][NM][2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < B; ++i) {
             const uint32_t k = k0 + i <= last ? k0 + i : last;  // clamped loads are not added
             const float* r = rec + (uint64_t)(k + j) * rec_floats + s * 64u + n;
 #pragma unroll
@@ -427,7 +471,7 @@ __device__ __forceinline__ void sum_records(const float* rec, uint32_t rec_float
             }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < B; ++i)
             if (k0 + i <= last)
 #pragma unroll
                 for (int m = 0; m < NM; ++m) out[m] += v[i][m][0] + v[i][m][1];
@@ -549,7 +593,9 @@ __device__ __forceinline__ void prep_x_block(const float* __restrict__ x, uint64
 //   void job_begin(uint32_t j)            prepares as, hscale for job j
 //   ASrc<LDS> as; float hscale;
 //   void scales(uint32_t j, uint32_t c, float (&fs)[NT])
-//   void flush(uint32_t j, const float (&m0)[NT], const float (&m1)[NT])
+//   uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&m1)[NT], uint32_t& kc)
+//       stores the wave's record of job j; returns the job's counter and its contributor count
+//   void fixup(uint32_t j)   the job's epilogue, by the last contributor
 // ------------------------------------------------------------------------------------------
 
 template <uint32_t FMT, int NT, bool LDS, typename Pol>
@@ -588,6 +634,11 @@ __device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1)
     }
     uint32_t pj = u0 / UJ, pm = (u0 - pj * UJ) / C, pc = u0 - pj * UJ - pm * C;
     pol.job_begin(pj);
+    auto flush = [&](uint32_t j, const float (&m0)[NT], const float (&m1)[NT]) {
+        uint32_t kc;
+        uint32_t* ctr = pol.store(j, m0, m1, kc);
+        if (arrive(ctr, kc)) pol.fixup(j);
+    };
     float acc[NT], keep[NT], fs[NT];
 #pragma unroll
     for (int s = 0; s < NT; ++s) acc[s] = keep[s] = 0.0f;
@@ -617,8 +668,8 @@ __device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1)
                     }
                 }
                 if (job_end || uu + 1 == u1) {
-                    if (NM == 2 && pm == 1) pol.flush(pj, keep, acc);
-                    else pol.flush(pj, acc, keep);  // keep is zero here
+                    if (NM == 2 && pm == 1) flush(pj, keep, acc);
+                    else flush(pj, acc, keep);  // keep is zero here
 #pragma unroll
                     for (int s = 0; s < NT; ++s) acc[s] = keep[s] = 0.0f;
                     if (job_end) {

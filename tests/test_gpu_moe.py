@@ -104,11 +104,11 @@ def _device_layer(ops, lib, wl, experts, shared, sem, routing, router=None, bias
 
 def _check_layer(ops, lib, oracle, wl, experts, shared, sem, routing_name, routing, x,
                  score_fn=SCORE_SIGMOID, bias=None, table=None, route_scale=1.0,
-                 routed_limit=0.0, shared_limit=0.0, sample=None):
+                 routed_limit=0.0, shared_limit=0.0, sample=None, router=None):
     """Routes of every token must equal the oracle's; outputs are checked for every token, or
     for the tokens in `sample` (each token's output depends on its own routes only)."""
     H, F = wl.width, wl.intermediate
-    router = wl.router()
+    router = wl.router() if router is None else router
     layer = _device_layer(ops, lib, wl, experts, shared, sem, routing, router, bias, score_fn,
                           route_scale, routed_limit, shared_limit)
     xt = torch.from_numpy(x).cuda()
@@ -156,6 +156,31 @@ def test_small_layers(ops, lib, oracle, routing_name, score):
                  table, route_scale=1.5 if sem == "deepseek" else 1.0,
                  routed_limit=0.3 if sem == "deepseek" else 0.0,
                  shared_limit=0.2 if sem == "deepseek" else 0.0)
+
+
+@pytest.mark.parametrize("experts_n,tokens,routing_name", [(256, 1, "learned"), (100, 3, "learned"),
+                                                         (64, 2, "softmax")])
+def test_tied_router_rows_route_to_lower_ids(ops, lib, oracle, experts_n, tokens, routing_name):
+    """Router rows repeated in runs of four give equal logits (and keys) within each run; the
+    selection must take the runs' lower expert ids first, as the reference's stable ranking does."""
+    print(f"[moe ties] E={experts_n} tokens={tokens} {routing_name}", flush=True)
+    rng = np.random.default_rng(7 + experts_n)
+    from vastloom_amd.workloads import MoeWorkload
+    sem = "qwen" if routing_name == "softmax" else "deepseek"
+    H, F, K = 256, 256, 6
+    wl = MoeWorkload("ties", 13, H, F, experts_n, K, tokens, IQ2_XXS, IQ2_XXS, 0.01, sem)
+    base = (rng.standard_normal(((experts_n + 3) // 4, H)) * 0.02).astype(np.float32)
+    router = np.ascontiguousarray(np.repeat(base, 4, axis=0)[:experts_n])
+    experts = [make_expert(rng, IQ2_XXS, IQ2_XXS, H, F) for _ in range(experts_n)]
+    shared = make_expert(rng, IQ2_XXS, IQ2_XXS, H, F)
+    x = rng.standard_normal((tokens, H)).astype(np.float32)
+    routing = lib.ROUTE_SOFTMAX if routing_name == "softmax" else lib.ROUTE_LEARNED
+    layer = _check_layer(ops, lib, oracle, wl, experts, shared, sem, routing_name, routing, x,
+                         router=router)
+    ids, _ = layer.routes(tokens)
+    for t in range(tokens):  # every run the selection enters is entered at its lowest id
+        for e in ids[t]:
+            assert e % 4 == 0 or (e - 1) in ids[t], (t, ids[t])
 
 
 def test_bad_table_route_is_refused(ops, lib, oracle):

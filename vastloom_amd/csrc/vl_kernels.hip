@@ -298,6 +298,8 @@ struct Matvec {
         for (int s = 0; s < NT; ++s) fs[s] = lds_load<float>(scale_off + 4u * (8u * eb + s));
     }
 
+    static constexpr bool kPrefetch = false;
+
     __device__ uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&)[NT], uint32_t& kc) const {
         const uint32_t lane = threadIdx.x & 63u;
         float* rec = reinterpret_cast<float*>(const_cast<uint8_t*>(ws) + m.off_rec);

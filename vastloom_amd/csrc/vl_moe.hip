@@ -302,6 +302,16 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xb1, 0xf, 0xf, false));
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4e, 0xf, 0xf, false));
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xf, 0xf, false));
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xf, 0xf, false));
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xa, 0xf, false));
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xc, 0xf, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // Per-token selection scratch in LDS.
 struct TopKLds {
     uint32_t id[kMoeMaxTopK];
@@ -310,15 +320,17 @@ struct TopKLds {
 };
 
 // Top-k of one token by one wave (all lanes active). Lane l holds experts l, l + 64, ... (PER of
-// them) with the selection keys of the router kernel. Round k takes the largest remaining key,
-// ties to the lowest id (a DPP wave maximum, then the first ballot lane), so the experts come
-// out in the reference's rank order; lanes k < K then form the weights with the reference's
-// float64 arithmetic, summing in rank order. Returns true when the token cannot be routed
-// (non-finite logits or a non-positive weight sum).
+// them) with the selection keys of the router kernel, and first sorts them by key, descending,
+// equal keys keeping ascending ids. Round k then takes the largest remaining key, ties to the
+// lowest id: a DPP wave maximum over the lanes' heads, the head's lane (a wave minimum of ids
+// only when several heads tie), and that lane drops its head. The experts thus come out in the
+// reference's rank order; lanes k < K then form the weights with the reference's float64
+// arithmetic, summing in rank order. Returns true when the token cannot be routed (non-finite
+// logits or a non-positive weight sum).
 template <int PER>
 __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* keys, uint32_t E,
                            uint32_t K, bool softmax, const MoeShape& s, TopKLds& tk,
-                           uint32_t* out_idx, float* out_w) {
+                           uint32_t* out_idx, float* out_w, bool coherent) {
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t key[PER];
     float lv[PER], sv[PER];
@@ -329,28 +341,42 @@ __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* ke
         key[i] = 0;
         lv[i] = sv[i] = 0.0f;
         if (e < E) {
-            key[i] = load_shared_u32(keys + e);
-            lv[i] = load_shared(lg + e);
-            sv[i] = load_shared(scr + e);
+            key[i] = coherent ? load_shared_u32(keys + e) : *gp(keys + e);
+            lv[i] = coherent ? load_shared(lg + e) : *gp(lg + e);
+            sv[i] = coherent ? load_shared(scr + e) : *gp(scr + e);
             bad |= !isfinite(lv[i]);
         }
     }
+    // key[] is sorted in place; hid[] follows it. Values are read from lv/sv by id.
+    uint32_t hid[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) hid[i] = lane + 64u * i;
+#pragma unroll
+    for (int i = 1; i < PER; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j)
+            if (key[j] > key[j - 1]) {
+                const uint32_t tk_ = key[j], ti = hid[j];
+                key[j] = key[j - 1];
+                hid[j] = hid[j - 1];
+                key[j - 1] = tk_;
+                hid[j - 1] = ti;
+            }
     for (uint32_t k = 0; k < K; ++k) {
-        uint32_t best = 0;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) best = max(best, key[i]);
-        const uint32_t m = wave_max_u32(best);
-        uint32_t id = 0xffffffffu;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const uint64_t hit = __ballot(key[i] == m && m != 0);
-            if (id == 0xffffffffu && hit) id = 64u * i + (uint32_t)__builtin_ctzll(hit);
-        }
-        if (id == 0xffffffffu) {
+        const uint32_t m = wave_max_u32(key[0]);
+        const bool top = key[0] == m && m != 0;
+        const uint64_t hit = __ballot(top);
+        uint32_t wl = 0;
+        if (hit == 0) {
             bad = true;
-            id = 0;
+        } else if ((hit & (hit - 1)) == 0) {
+            wl = (uint32_t)__builtin_ctzll(hit);
+        } else {
+            const uint32_t mid = wave_min_u32(top ? hid[0] : 0xffffffffu);
+            wl = (uint32_t)__builtin_ctzll(__ballot(top && hid[0] == mid));
         }
-        const uint32_t wl = id & 63u, wi = id >> 6;
+        const uint32_t id = hit ? (uint32_t)__builtin_amdgcn_readlane((int)hid[0], wl) : 0u;
+        const uint32_t wi = id >> 6;
         float l = lv[0], sc = sv[0];
 #pragma unroll
         for (int i = 1; i < PER; ++i)
@@ -358,13 +384,18 @@ __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* ke
                 l = lv[i];
                 sc = sv[i];
             }
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (wi == (uint32_t)i && lane == wl) key[i] = 0;
-        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax ? l : sc), wl));
+        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax ? l : sc), id & 63u));
         if (lane == 0) {
             tk.id[k] = id;
             tk.val[k] = v;
+        }
+        if (lane == wl) {
+#pragma unroll
+            for (int i = 0; i + 1 < PER; ++i) {
+                key[i] = key[i + 1];
+                hid[i] = hid[i + 1];
+            }
+            key[PER - 1] = 0;
         }
     }
     double sum_all = 0.0, mx = 0.0;
@@ -420,7 +451,7 @@ struct RouteLds {
 // order); returns true in every lane when the token is refused.
 __device__ __forceinline__ bool route_token(const MoeShape& s, const MoeInputs& in,
                                             const MoeWorkspace& w, uint32_t t, TopKLds& tk,
-                                            uint32_t* idx, float* wt) {
+                                            uint32_t* idx, float* wt, bool coherent = false) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t K = s.top_k, E = s.experts;
     const uint64_t base = (uint64_t)t * E;
@@ -449,8 +480,8 @@ __device__ __forceinline__ bool route_token(const MoeShape& s, const MoeInputs& 
             float sc[kMoeMaxTopK];
             for (uint32_t k = 0; k < K; ++k) {
                 const uint32_t e = idx[k];
-                bad |= !isfinite(load_shared(lg + e));
-                sc[k] = load_shared(scr + e);
+                bad |= !isfinite(coherent ? load_shared(lg + e) : *gp(lg + e));
+                sc[k] = coherent ? load_shared(scr + e) : *gp(scr + e);
                 sum += (double)sc[k];
             }
             if (!(sum > 0.0) || isinf(sum)) bad = true;
@@ -462,11 +493,11 @@ __device__ __forceinline__ bool route_token(const MoeShape& s, const MoeInputs& 
         const float* scr = ws_ptr<const float>(w, w.off_scores) + base;
         const uint32_t* keys = ws_ptr<const uint32_t>(w, w.off_keys) + base;
         const bool softmax = s.routing == kRouteSoftmax;
-        if (E <= 64) bad = route_topk<1>(lg, scr, keys, E, K, softmax, s, tk, idx, wt);
-        else if (E <= 128) bad = route_topk<2>(lg, scr, keys, E, K, softmax, s, tk, idx, wt);
-        else if (E <= 256) bad = route_topk<4>(lg, scr, keys, E, K, softmax, s, tk, idx, wt);
-        else if (E <= 512) bad = route_topk<8>(lg, scr, keys, E, K, softmax, s, tk, idx, wt);
-        else bad = route_topk<16>(lg, scr, keys, E, K, softmax, s, tk, idx, wt);
+        if (E <= 64) bad = route_topk<1>(lg, scr, keys, E, K, softmax, s, tk, idx, wt, coherent);
+        else if (E <= 128) bad = route_topk<2>(lg, scr, keys, E, K, softmax, s, tk, idx, wt, coherent);
+        else if (E <= 256) bad = route_topk<4>(lg, scr, keys, E, K, softmax, s, tk, idx, wt, coherent);
+        else if (E <= 512) bad = route_topk<8>(lg, scr, keys, E, K, softmax, s, tk, idx, wt, coherent);
+        else bad = route_topk<16>(lg, scr, keys, E, K, softmax, s, tk, idx, wt, coherent);
     }
     return __any(bad);
 }
@@ -474,9 +505,10 @@ __device__ __forceinline__ bool route_token(const MoeShape& s, const MoeInputs& 
 // Routing of token t by one wave of a gate/up block: ids and weights into rt.idx/wt, refusal into
 // rt.bad[t].
 __device__ __forceinline__ void route_token_wave(const MoeShape& s, const MoeInputs& in,
-                                                 const MoeWorkspace& w, uint32_t t, RouteLds& rt) {
+                                                 const MoeWorkspace& w, uint32_t t, RouteLds& rt,
+                                                 bool coherent = false) {
     const uint32_t K = s.top_k;
-    const bool bad = route_token(s, in, w, t, rt.topk[t], rt.idx + t * K, rt.wt + t * K);
+    const bool bad = route_token(s, in, w, t, rt.topk[t], rt.idx + t * K, rt.wt + t * K, coherent);
     if ((threadIdx.x & 63u) == 0) rt.bad[t] = bad ? 1u : 0u;
 }
 
@@ -789,6 +821,8 @@ struct GateUp {
             fs[s2] = (uint32_t)s2 < ntok ? lds_load<float>(scale_off + 4u * (8u * eb + tok[s2])) : 0.0f;
     }
 
+    static constexpr bool kPrefetch = false;
+
     __device__ uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&m1)[NT], uint32_t& kc) const {
         const uint32_t lane = threadIdx.x & 63u;
         constexpr uint32_t RF = 2u * NT * 64u;
@@ -1014,6 +1048,8 @@ struct Down {
 #pragma unroll
         for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? lds_load<float>(sc + 4u * s2) : 0.0f;
     }
+
+    static constexpr bool kPrefetch = false;
 
     __device__ uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&)[NT], uint32_t& kc) const {
         const uint32_t lane = threadIdx.x & 63u;
@@ -1242,7 +1278,7 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_fused(const MoeSha
     // agent-scope loads of phase A's values.
     int nonfinite = 0;
     if (wave < s.tokens) {
-        route_token_wave(s, in, w, wave, rt);
+        route_token_wave(s, in, w, wave, rt, true);
     } else {
         const uint32_t t0 = tid - 64u * s.tokens, nt0 = nth - 64u * s.tokens;
         const uint32_t* src = ws_ptr<const uint32_t>(w, w.off_xlimbs);
@@ -1575,6 +1611,40 @@ struct GateUpGrouped {
             fs[s2] = (uint32_t)s2 < ntok ? __builtin_amdgcn_ldexpf(1.0f, -*gp(xe + tok[s2])) : 0.0f;
     }
 
+    // Activations and exponents of up to 1024 tokens stay in global memory: a unit's eight A
+    // fragments and slot scales are fetched one unit ahead.
+    static constexpr bool kPrefetch = true;
+    __device__ void load_ops(uint32_t j, uint32_t c, Operands<NT>& o) const {
+        const uint32_t a = j / tiles;
+        const uint32_t lane = threadIdx.x & 63u, m = lane & 31u, kh = lane >> 5;
+        const uint32_t nt = lds_load<uint32_t>(ntok_off + 4u * a);
+        const uint32_t tb = tok_off + 2u * NT * a;
+        const uint32_t sl = a_slot(m), limb = a_limb(m);
+        const uint32_t tk = lds_load<uint16_t>(tb + 2u * (sl < nt ? sl : 0u));
+        const int8_t* p = ws_ptr<const int8_t>(w, w.off_xlimbs) + (uint64_t)tk * 128u + limb * 32u + 16u * kh;
+        constexpr uint32_t NF = FMT == VL_TYPE_Q8_0 ? 4u : 8u;
+#pragma unroll
+        for (uint32_t g = 0; g < NF; ++g) {
+            const uint32_t G = NF * c + g < ng ? NF * c + g : ng - 1u;  // past the row end: unused
+            o.a[g] = *gp(reinterpret_cast<const i32x4*>(p + (uint64_t)G * as.stride));
+        }
+        // Lane s (< NT) fetches slot s's exponent; unused slots read token 0's and are masked
+        // when the scales are formed.
+        const uint32_t eb = FMT == VL_TYPE_Q8_0 ? c / 2u : c;
+        const uint32_t ts = lds_load<uint16_t>(tb + 2u * (lane & (NT - 1u)));
+        o.ev = (uint32_t)*gp(ws_ptr<const int>(w, w.off_xexp) + (uint64_t)eb * w.estride + ts);
+    }
+
+    __device__ void ops_scales(const Operands<NT>& o, uint32_t j, uint32_t, float (&fs)[NT]) const {
+        const uint32_t nt = uni(lds_load<uint32_t>(ntok_off + 4u * (j / tiles)));
+#pragma unroll
+        for (int s2 = 0; s2 < NT; ++s2)
+            fs[s2] = (uint32_t)s2 < nt
+                         ? __builtin_amdgcn_ldexpf(1.0f, -(int)__builtin_amdgcn_readlane((int)o.ev, s2))
+                         : 0.0f;
+    }
+
+
     __device__ uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&m1)[NT], uint32_t& kc) const {
         const uint32_t lane = threadIdx.x & 63u;
         constexpr uint32_t RF = 2u * NT * 64u;
@@ -1668,6 +1738,10 @@ struct DownGrouped {
 #pragma unroll
         for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? lds_load<float>(sc + 4u * s2) : 0.0f;
     }
+
+    // The staged h limbs are L2-resident (written by this block's prologue) and jobs are eight
+    // units long: loading a unit's A fragments one unit ahead measured slower than in place.
+    static constexpr bool kPrefetch = false;
 
     __device__ uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&)[NT], uint32_t& kc) const {
         const uint32_t lane = threadIdx.x & 63u;

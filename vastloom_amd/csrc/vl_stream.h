@@ -354,11 +354,22 @@ struct ASrc {
 // Chunk processing: accf[s] += this lane's partial of (row, slot s) over the unit.
 // ------------------------------------------------------------------------------------------
 
+// A unit's activation fragments and slot scales, for policies that prefetch them with the
+// weights (their activations live in global memory, where a load per unit would wait a memory
+// latency each time).
+template <int NT>
+struct Operands {
+    i32x4 a[8];
+    uint32_t ev;  // lane s < NT: slot s's activation exponent (policy-defined encoding)
+};
+
 // df: weight factor of the lane's row for the unit (d times the format factor, times 65536 in
-// the high-limb half); fs[s]: 2^-e of slot s for the unit's exponent block.
-template <uint32_t FMT, int NT, typename AS>
+// the high-limb half); fs[s]: 2^-e of slot s for the unit's exponent block. With PRE the A
+// fragments come from pre[] instead of as.
+template <uint32_t FMT, int NT, typename AS, bool PRE = false>
 __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint32_t ng, const AS& as,
-                                              float hscale, const float (&fs)[NT], float (&accf)[NT]) {
+                                              float hscale, const float (&fs)[NT], float (&accf)[NT],
+                                              const i32x4* pre = nullptr) {
     const uint32_t lane = threadIdx.x & 63u;
     const int hh = (int)(lane >> 5);
     const uint32_t lane_off = (lane & 31u) * 8u;
@@ -368,7 +379,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint3
         for (int b = 0; b < 4; ++b) {
             const uint32_t G = 4u * c + b;
             if (G >= ng) break;
-            const i32x4 afr = as.load(G);
+            const i32x4 afr = PRE ? pre[b] : as.load(G);
             const uint4& q = b == 0 ? ch.q0 : b == 1 ? ch.q1 : b == 2 ? ch.q2 : ch.q3;
             i32x4 bfr;
             bfr[0] = (int)q.x; bfr[1] = (int)q.y; bfr[2] = (int)q.z; bfr[3] = (int)q.w;
@@ -383,7 +394,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint3
     }
     i32x4 afr[8];
 #pragma unroll
-    for (int g = 0; g < 8; ++g) afr[g] = as.load(8u * c + g);
+    for (int g = 0; g < 8; ++g) afr[g] = PRE ? pre[g] : as.load(8u * c + g);
     ChunkDecoder<FMT> dec;
     dec.init(ch);
     int acc[2 * NT];
@@ -596,6 +607,13 @@ __device__ __forceinline__ void prep_x_block(const float* __restrict__ x, uint64
 //   uint32_t* store(uint32_t j, const float (&m0)[NT], const float (&m1)[NT], uint32_t& kc)
 //       stores the wave's record of job j; returns the job's counter and its contributor count
 //   void fixup(uint32_t j)   the job's epilogue, by the last contributor
+//   static constexpr bool kPrefetch; with it set,
+//   void load_ops(uint32_t j, uint32_t c, Operands<NT>& o)
+//       issues unit (j, c)'s A fragment and exponent loads one unit ahead, waiting for nothing
+//       (issued before that iteration's weight prefetch, so waiting for them never waits for
+//       newer weights); as is not used
+//   void ops_scales(const Operands<NT>& o, uint32_t j, uint32_t c, float (&fs)[NT])
+//       the unit's slot scales, when it is processed
 // ------------------------------------------------------------------------------------------
 
 template <uint32_t FMT, int NT, bool LDS, typename Pol>
@@ -626,13 +644,19 @@ __device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1)
             htr = pol.tref(hj, hm);
         }
     };
+    constexpr bool PF = Pol::kPrefetch;
+    uint32_t pj = u0 / UJ, pm = (u0 - pj * UJ) / C, pc = u0 - pj * UJ - pm * C;
+    Operands<NT> ob;
+    if constexpr (PF) {
+        pol.load_ops(pj, pc, ob);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     Chunk buf[D];
 #pragma unroll
     for (int k = 0; k < D; ++k) {
         load_chunk<FMT>(htr, hc, pol.ng, buf[k]);
         head_next();
     }
-    uint32_t pj = u0 / UJ, pm = (u0 - pj * UJ) / C, pc = u0 - pj * UJ - pm * C;
     pol.job_begin(pj);
     auto flush = [&](uint32_t j, const float (&m0)[NT], const float (&m1)[NT]) {
         uint32_t kc;
@@ -647,11 +671,19 @@ __device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1)
         for (int k = 0; k < D; ++k) {
             const uint32_t uu = u + k;
             if (uu < u1) {
-                pol.scales(pj, pc, fs);
-                process_chunk<FMT, NT>(buf[k], pc, pol.ng, pol.as, pol.hscale, fs, acc);
+                if constexpr (PF) {
+                    pol.ops_scales(ob, pj, pc, fs);
+                    process_chunk<FMT, NT, decltype(pol.as), true>(buf[k], pc, pol.ng, pol.as, pol.hscale,
+                                                                   fs, acc, ob.a);
+                } else {
+                    pol.scales(pj, pc, fs);
+                    process_chunk<FMT, NT>(buf[k], pc, pol.ng, pol.as, pol.hscale, fs, acc);
+                }
             }
-            load_chunk<FMT>(htr, hc, pol.ng, buf[k]);
-            head_next();
+            if constexpr (!PF) {
+                load_chunk<FMT>(htr, hc, pol.ng, buf[k]);
+                head_next();
+            }
             if (uu < u1) {
                 bool job_end = false;
                 if (++pc == C) {
@@ -678,6 +710,12 @@ __device__ __forceinline__ void stream_range(Pol& pol, uint32_t u0, uint32_t u1)
                         if (uu + 1 < u1) pol.job_begin(pj);
                     }
                 }
+            }
+            if constexpr (PF) {
+                if (uu + 1 < u1) pol.load_ops(pj, pc, ob);  // (pj, pc) is now the next unit
+                __builtin_amdgcn_sched_barrier(0);  // the operand loads stay ahead of the weights'
+                load_chunk<FMT>(htr, hc, pol.ng, buf[k]);
+                head_next();
             }
         }
     }

@@ -189,7 +189,7 @@ __global__ void __launch_bounds__(256) k_dequant(vl_tiled_layout L, const uint8_
     dec.init(ch);  // all lanes: the IQ2_XXS halves exchange scale bytes
     if (row >= L.rows) return;
     const float df = half_bits_to_float(ch.d0) * unit_factor<FMT>();
-    const uint32_t lane_off = n * 8u;
+    const uint32_t lane_off = (n % kTabCopies) * 8u;
     for (int g = 0; g < 8; ++g) {
         int sc = 1;
         const i32x4 frag = dec.group(ch, g, lane_off, hh, sc);

@@ -1086,21 +1086,38 @@ __device__ __forceinline__ void convert_h(const MoeWorkspace& w, uint32_t inter,
         const uint32_t m = *gp(hmax + (uint64_t)a0 * w.hblocks * 8u + i);
         scale[i] = __builtin_amdgcn_ldexpf(1.0f, -limb_exponent(__uint_as_float(m)));
     }
-    const uint32_t quads = inter / 4u;
-    for (uint32_t i = threadIdx.x; i < na * NT * quads; i += blockDim.x) {
-        const uint32_t q = i % quads, sl = (i / quads) % NT, al = i / (quads * NT);
-        const uint32_t a = a0 + al, col = 4u * q;
-        if (sl >= ntok[a * ntok_stride]) continue;
-        const uint32_t m = *gp(hmax + ((uint64_t)a * w.hblocks + col / 256u) * 8u + sl);
-        const int e = limb_exponent(__uint_as_float(m));
-        const float4 f4 = ld_f4(h + ((uint64_t)a * NT + sl) * inter + col);
-        const float v[4] = {f4.x, f4.y, f4.z, f4.w};
-        uint32_t packed[4];
-        limbs4(v, e, packed);
-        int8_t* d = dst + (uint64_t)al * down_expert_bytes(inter, NT) +
-                    ((uint64_t)(col / 32u) * NT + sl) * 128u + (col % 32u);
+    // Eight quads per thread have their loads in flight before any is converted.
+    constexpr int B = 8;
+    const uint32_t quads = inter / 4u, total = na * NT * quads;
+    for (uint32_t i0 = threadIdx.x; i0 < total; i0 += B * blockDim.x) {
+        float4 f4[B];
+        uint32_t mx[B];
+        bool live[B];
 #pragma unroll
-        for (int l = 0; l < 4; ++l) *reinterpret_cast<uint32_t*>(d + 32u * l) = packed[l];
+        for (int j = 0; j < B; ++j) {
+            const uint32_t i = i0 + j * blockDim.x;
+            const uint32_t q = i % quads, sl = (i / quads) % NT, al = i / (quads * NT);
+            const uint32_t a = a0 + al, col = 4u * q;
+            live[j] = i < total && sl < ntok[a * ntok_stride];
+            if (live[j]) {
+                mx[j] = *gp(hmax + ((uint64_t)a * w.hblocks + col / 256u) * 8u + sl);
+                f4[j] = ld_f4(h + ((uint64_t)a * NT + sl) * inter + col);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+            if (!live[j]) continue;
+            const uint32_t i = i0 + j * blockDim.x;
+            const uint32_t q = i % quads, sl = (i / quads) % NT, al = i / (quads * NT);
+            const uint32_t col = 4u * q;
+            const float v[4] = {f4[j].x, f4[j].y, f4[j].z, f4[j].w};
+            uint32_t packed[4];
+            limbs4(v, limb_exponent(__uint_as_float(mx[j])), packed);
+            int8_t* d = dst + (uint64_t)al * down_expert_bytes(inter, NT) +
+                        ((uint64_t)(col / 32u) * NT + sl) * 128u + (col % 32u);
+#pragma unroll
+            for (int l = 0; l < 4; ++l) *reinterpret_cast<uint32_t*>(d + 32u * l) = packed[l];
+        }
     }
 }
 
@@ -1127,15 +1144,11 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_down(const MoeShap
                                                              const MoeWorkspace w) {
     extern __shared__ __align__(16) uint8_t lds[];
     const MoeHeader* hdr = ws_ptr<const MoeHeader>(w, w.off_header);
-    const uint32_t n_active = uni(*gp(&hdr->n_active));
+    // The active count is loaded now but first used after the copies below have issued their
+    // loads, so the kernel waits one memory latency for all of them.
+    const uint32_t n_active_raw = *gp(&hdr->n_active);
     const uint32_t tiles = w.tiles_dn, UJ = units_per_row(FMT, s.inter);
     constexpr uint32_t WV = stream_waves<NT>();
-    const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * WV, TU);
-    // Experts this block's units touch.
-    const uint32_t ub0 = range_begin(blockIdx.x * WV, NW, TU);
-    const uint32_t ub1 = range_begin((blockIdx.x + 1u) * WV, NW, TU);
-    const uint32_t a0 = ub0 < ub1 ? (ub0 / UJ) / tiles : 0u;
-    const uint32_t a1 = ub0 < ub1 ? ((ub1 - 1u) / UJ) / tiles : 0u;
     constexpr uint32_t TB = table_bytes<FMT>();
     const uint32_t eb = down_expert_bytes(s.inter, NT);
     const uint32_t stage_bytes = LDS ? w.stage * eb : 0u;
@@ -1144,7 +1157,7 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_down(const MoeShap
     const uint8_t** wptr = reinterpret_cast<const uint8_t**>(lds + lay.wptr);
     int8_t* slab = ws_ptr<int8_t>(w, w.off_hslab) + (uint64_t)blockIdx.x * w.stage * eb;
     {
-        const uint32_t words = n_active * (uint32_t)(sizeof(ActiveExpert) / 4u);
+        const uint32_t words = w.max_active * (uint32_t)(sizeof(ActiveExpert) / 4u);
         const uint32_t* src = ws_ptr<const uint32_t>(w, w.off_active);
         uint32_t* dst = reinterpret_cast<uint32_t*>(act);
         for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) dst[i] = *gp(src + i);
@@ -1154,6 +1167,13 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_down(const MoeShap
         for (uint32_t i = threadIdx.x; i < cwords; i += blockDim.x) cdst[i] = *gp(csrc + i);
     }
     fill_tables<FMT>(lds);
+    const uint32_t n_active = uni(n_active_raw);
+    const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * WV, TU);
+    // Experts this block's units touch.
+    const uint32_t ub0 = range_begin(blockIdx.x * WV, NW, TU);
+    const uint32_t ub1 = range_begin((blockIdx.x + 1u) * WV, NW, TU);
+    const uint32_t a0 = ub0 < ub1 ? (ub0 / UJ) / tiles : 0u;
+    const uint32_t a1 = ub0 < ub1 ? ((ub1 - 1u) / UJ) / tiles : 0u;
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < n_active; i += blockDim.x)
         wptr[i] = in.experts[act[i].expert].down;

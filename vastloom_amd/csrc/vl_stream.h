@@ -112,23 +112,25 @@ __device__ __forceinline__ void fill_tables(uint8_t* lds, uint32_t tid0 = thread
     // memory latency per eight stores rather than one per store.
     constexpr int B = 8;
     if (FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_IQ3_XXS) {
-        constexpr uint32_t nB = 128u * kTabCopies / 2u, nA = 256u * kTabCopies / 2u;  // uint4 stores
+        // Store i writes copies 2(i % 8) and 2(i % 8) + 1 of entry i / 8 (16 bytes) into the lower
+        // half of the entry's 256-byte row.
+        constexpr uint32_t per = kTabCopies / 2u;                   // 16-byte stores per entry
+        constexpr uint32_t nB = 128u * per, nA = 256u * per;
         for (uint32_t i0 = tid0; i0 < nB + nA; i0 += B * nthr) {
             uint64_t v[B];
 #pragma unroll
             for (int j = 0; j < B; ++j) {
                 const uint32_t i = i0 + j * nthr;
                 v[j] = 0;
-                if (i < nB) v[j] = FMT == VL_TYPE_IQ2_XXS ? g_tables.sign_sel[i / (kTabCopies / 2u)]
-                                                          : g_tables.iq3_sel[i / (kTabCopies / 2u)];
+                if (i < nB) v[j] = FMT == VL_TYPE_IQ2_XXS ? g_tables.sign_sel[i / per] : g_tables.iq3_sel[i / per];
                 else if (i < nB + nA)
-                    v[j] = FMT == VL_TYPE_IQ2_XXS ? g_tables.iq2_codes[(i - nB) / (kTabCopies / 2u)]
-                                                  : g_tables.iq3_pm[(i - nB) / (kTabCopies / 2u)];
+                    v[j] = FMT == VL_TYPE_IQ2_XXS ? g_tables.iq2_codes[(i - nB) / per] : g_tables.iq3_pm[(i - nB) / per];
             }
 #pragma unroll
             for (int j = 0; j < B; ++j) {
                 const uint32_t i = i0 + j * nthr;
-                const uint32_t off = i < nB ? kTabB + i * 16u : kTabA + (i - nB) * 16u;
+                const uint32_t k = i < nB ? i : i - nB;
+                const uint32_t off = (i < nB ? kTabB : kTabA) + (k / per) * 256u + (k % per) * 16u;
                 if (i < nB + nA)
                     *reinterpret_cast<uint4*>(lds + off) = make_uint4(lo32(v[j]), hi32(v[j]), lo32(v[j]), hi32(v[j]));
             }
@@ -372,7 +374,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint3
                                               const i32x4* pre = nullptr) {
     const uint32_t lane = threadIdx.x & 63u;
     const int hh = (int)(lane >> 5);
-    const uint32_t lane_off = (lane & 31u) * 8u;
+    const uint32_t lane_off = (lane % kTabCopies) * 8u;
     const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     if (FMT == VL_TYPE_Q8_0) {
 #pragma unroll

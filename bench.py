@@ -40,7 +40,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--workload", default="iq2_moe",
-                   choices=["q8_expert", "q8_moe", "iq2_moe", "grouped_moe"])
+                   choices=["q8_expert", "q8_moe", "iq2_moe", "mixed_moe", "grouped_moe"])
     p.add_argument("--layers", type=int, default=None,
                    help="layer instances rotated between steps (defeats caching of weights); "
                         "default 6, or 2 for the grouped workload")
@@ -112,7 +112,7 @@ def build_layers(wl, instances: int):
     return experts, shared, layers
 
 
-def cpu_baseline(wl, experts, shared, pool, seconds: float) -> dict:
+def cpu_baseline(wl, experts, shared, pool, seconds: float, measured: float | None = None) -> dict:
     """The reference's own CPU kernels (oracle/_ref, built from its sources) on a bounded
     sample of the same workload: router logits and routing, then per selected expert the
     reference matvecs (row-split over the runtime policy's threads), SwiGLU and combine."""
@@ -175,7 +175,7 @@ def cpu_baseline(wl, experts, shared, pool, seconds: float) -> dict:
             break
     elapsed = time.perf_counter() - t0
     per_layer = elapsed / done * wl.tokens
-    layer_bytes = layer_weight_bytes(wl)
+    layer_bytes = layer_weight_bytes(wl, measured)
     return {"value": round(layer_bytes / per_layer / 1e9, 4), "unit": "GB/s",
             "cores": threads, "kind": kind,
             "us_per_layer": round(per_layer * 1e6, 1),
@@ -183,19 +183,32 @@ def cpu_baseline(wl, experts, shared, pool, seconds: float) -> dict:
                       f"{elapsed:.1f} s on {threads} thread(s) of {os.cpu_count()} logical CPUs"}
 
 
-def routed_experts(wl) -> int:
-    """Distinct routed experts one layer call reads."""
+def routed_experts(wl, measured: float | None = None) -> float:
+    """Distinct routed experts one layer call reads (for learned multi-token routing, the mean
+    over the token pool of what the device routed, passed in as `measured`)."""
     if wl.routing == "single":
         return 1
     if wl.tokens == 1:
         return wl.top_k
     if wl.routing == "zipf_table":
         return int(np.unique(wl.zipf_table()).size)
-    raise ValueError("per-layer bytes depend on the activations for this multi-token workload")
+    if measured is None:
+        raise ValueError("per-layer bytes depend on the activations for this multi-token workload")
+    return measured
 
 
-def layer_weight_bytes(wl) -> int:
-    return (routed_experts(wl) + (1 if wl.has_shared else 0)) * wl.expert_bytes()
+def layer_weight_bytes(wl, measured: float | None = None) -> int:
+    return int(round((routed_experts(wl, measured) + (1 if wl.has_shared else 0)) * wl.expert_bytes()))
+
+
+def device_routed_experts(layer, pool, table) -> float:
+    """Mean number of distinct experts the device routes each pool entry's tokens to."""
+    counts = []
+    for b in range(len(pool)):
+        layer.forward(pool[b], check=False, table_ids=table)
+        ids, _ = layer.routes(pool.shape[1])
+        counts.append(np.unique(ids).size)
+    return float(np.mean(counts))
 
 
 def main() -> int:
@@ -212,10 +225,6 @@ def main() -> int:
     from vastloom_amd.workloads import workload
 
     wl = workload(args.workload)
-    if wl.tokens != 1 and wl.routing != "zipf_table":
-        print("bench.py times single-token layers and the table-routed grouped workload",
-              file=sys.stderr)
-        return 2
     if args.layers is None:
         args.layers = 6 if wl.tokens == 1 else 2
     if wl.tokens > 1:
@@ -262,10 +271,13 @@ def main() -> int:
     tl.close()
     stage_us = {k: round(1000.0 * float(np.mean([s[k] for s in stages])), 2) for k in stages[0]}
 
-    layer_bytes = layer_weight_bytes(wl)
+    measured = None
+    if wl.tokens > 1 and wl.routing not in ("zipf_table", "single"):
+        measured = device_routed_experts(layers[0], pool, table)
+    layer_bytes = layer_weight_bytes(wl, measured)
     gbs = layer_bytes / (ms_per_step * 1e-3) / 1e9
     # Dominant kernel: the gate/up pass, which reads two matrices of every selected expert.
-    n_exp = routed_experts(wl) + (1 if wl.has_shared else 0)
+    n_exp = routed_experts(wl, measured) + (1 if wl.has_shared else 0)
     H, F = wl.width, wl.intermediate
     from vastloom_amd.workloads import storage_bytes
     gateup_bytes = n_exp * 2 * storage_bytes(wl.gate_type, F, H)
@@ -286,9 +298,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "iq2_xxs weights, i8xi8->i32 MFMA, f32 accumulate",
-        "data": "synthetic (seeded PCG64; uniform random IQ2_XXS payload bytes, |N(0,1)|*0.01 "
-                "fp16 scales, N(0,0.02) router, N(0,1) tokens)",
+        "dtype": f"{TYPE(wl.gate_type).lower()}/{TYPE(wl.down_type).lower()} weights, "
+                 "i8xi8->i32 MFMA, f32 accumulate",
+        "data": f"synthetic (seeded PCG64; uniform random {TYPE(wl.gate_type)}/{TYPE(wl.down_type)} "
+                f"payload bytes, |N(0,1)|*{wl.scale_factor} fp16 scales, N(0,0.02) router, N(0,1) tokens)",
         "config": {"workload": f"{wl.name}: DeepSeek-class MoE layer, width {wl.width}, expert "
                                f"width {wl.intermediate}, {wl.experts} routed experts top-"
                                f"{wl.top_k} + {int(wl.has_shared)} shared, {wl.tokens} token(s), "
@@ -311,7 +324,8 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(wl, experts, shared, pool_host, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(wl, experts, shared, pool_host, args.cpu_seconds,
+                                              measured)
     print(json.dumps(result))
     return 0
 

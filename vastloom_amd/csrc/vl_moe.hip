@@ -1689,8 +1689,15 @@ struct GateUpGrouped {
     }
 };
 
+// Waves per block of the grouped gate/up kernel: 12 (three per SIMD, 170 registers each) where
+// the eight-slot loop fits that budget without spilling (IQ2_XXS, Q8_0), else 8.
 template <uint32_t FMT>
-__global__ void __launch_bounds__(stream_threads<kMoeMaxTokens>()) k_moe_gateup_grouped(const MoeShape s, const MoeInputs in,
+__host__ __device__ constexpr uint32_t gateup_grouped_waves() {
+    return FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_Q8_0 ? 12u : 8u;
+}
+
+template <uint32_t FMT>
+__global__ void __launch_bounds__(gateup_grouped_waves<FMT>() * 64u) k_moe_gateup_grouped(const MoeShape s, const MoeInputs in,
                                                                        const MoeWorkspace w) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int NT = kMoeMaxTokens;
@@ -1710,8 +1717,8 @@ __global__ void __launch_bounds__(stream_threads<kMoeMaxTokens>()) k_moe_gateup_
     pol.tiles = w.tiles_gu;
     pol.UJ = 2u * pol.chunks;
     pol.TU = n * w.tiles_gu * pol.UJ;
-    pol.NW = active_waves(gridDim.x * stream_waves<NT>(), pol.TU);
-    pol.wid = blockIdx.x * stream_waves<NT>() + uni(threadIdx.x >> 6);
+    pol.NW = active_waves(gridDim.x * gateup_grouped_waves<FMT>(), pol.TU);
+    pol.wid = blockIdx.x * gateup_grouped_waves<FMT>() + uni(threadIdx.x >> 6);
     pol.wptr_off = lay.wptr;
     pol.tok_off = lay.tok;
     pol.ntok_off = lay.ntok;
@@ -1928,7 +1935,7 @@ static hipError_t launch_gateup_grouped(const MoeShape& s, const MoeInputs& in, 
                                         hipStream_t st) {
     const GroupLds lay = group_lds(table_bytes<FMT>(), w.max_active, 2u, 0u);
     if (lay.bytes > kLdsBudget) return hipErrorInvalidValue;
-    return launch_stream(k_moe_gateup_grouped<FMT>, w.blocks, stream_threads<kMoeMaxTokens>(), lay.bytes, st, s, in, w);
+    return launch_stream(k_moe_gateup_grouped<FMT>, w.blocks, gateup_grouped_waves<FMT>() * 64u, lay.bytes, st, s, in, w);
 }
 
 template <uint32_t FMT>

@@ -199,19 +199,33 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 // Threads 0..255 of the block: partial sums of expert row b's logits for tokens [t0, t1) into
 // red[t - t0][wave] (four waves take interleaved quarters of the row with every lane's float4
 // loads in flight).
+// Threads 0..255: the first 8 float4 of their share of expert row b (issued early by the caller).
+struct RouterRow {
+    float4 wv[8];
+    int nv;
+};
+__device__ __forceinline__ void router_row_load(const MoeShape& s, const MoeInputs& in, uint32_t b,
+                                                RouterRow& rr) {
+    const uint32_t r = threadIdx.x;
+    const float4* row = reinterpret_cast<const float4*>(in.router + (uint64_t)b * s.width);
+    const uint32_t n4 = s.width / 4u;
+    rr.nv = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t i = r + 256u * j;
+        if (i < n4) { rr.wv[j] = row[i]; rr.nv = j + 1; }
+    }
+}
+
 __device__ __forceinline__ void router_row_partials(const MoeShape& s, const MoeInputs& in, uint32_t b,
-                                                    uint32_t t0, uint32_t t1, double (*red)[4]) {
+                                                    uint32_t t0, uint32_t t1, double (*red)[4],
+                                                    const RouterRow& rr) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t r = threadIdx.x;
     const float4* row = reinterpret_cast<const float4*>(in.router + (uint64_t)b * s.width);
     const uint32_t n4 = s.width / 4u;
-    float4 wv[8];
-    int nv = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t i = r + 256u * j;
-        if (i < n4) { wv[j] = row[i]; nv = j + 1; }
-    }
+    const float4 (&wv)[8] = rr.wv;
+    const int nv = rr.nv;
     for (uint32_t t = t0; t < t1; ++t) {
         const float4* xr = reinterpret_cast<const float4*>(in.x + (uint64_t)t * s.width);
         double acc = 0.0;
@@ -268,6 +282,11 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
     const uint32_t b = blockIdx.x;
     const uint32_t t0 = blockIdx.y * kMoeMaxTokens;
     const uint32_t t1 = t0 + kMoeMaxTokens < s.tokens ? t0 + kMoeMaxTokens : s.tokens;
+    // The row's weights are requested first; zeroing and the activation limbs overlap their
+    // latency.
+    RouterRow rr;
+    const bool routes = s.routing != kRouteGiven && b < s.experts;
+    if (routes) router_row_load(s, in, b, rr);
     if (b == 0 && blockIdx.y == 0 && threadIdx.x < 2) {
         MoeHeader* h = ws_ptr<MoeHeader>(w, w.off_header);
         (&h->status)[threadIdx.x] = 0;
@@ -281,8 +300,8 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
         prep_x_block(in.x, s.width, s.width, t0, t1, w.xslots, w.estride, b,
                      ws_ptr<int8_t>(w, w.off_xlimbs), ws_ptr<int>(w, w.off_xexp),
                      ws_ptr<uint32_t>(w, w.off_xflags));
-    if (s.routing == kRouteGiven || b >= s.experts) return;
-    router_row_partials(s, in, b, t0, t1, red);
+    if (!routes) return;
+    router_row_partials(s, in, b, t0, t1, red, rr);
     __syncthreads();
     if (threadIdx.x < t1 - t0) router_logit_finish(s, in, w, b, t0 + threadIdx.x, red[threadIdx.x]);
 }
@@ -1286,7 +1305,11 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_fused(const MoeSha
                          ws_ptr<uint32_t>(w, w.off_xflags));
     if (s.routing != kRouteGiven) {
         for (uint32_t r = blockIdx.x; r < s.experts; r += gridDim.x) {
-            if (wave < 4) router_row_partials(s, in, r, 0u, s.tokens, red);
+            if (wave < 4) {
+                RouterRow rr;
+                router_row_load(s, in, r, rr);
+                router_row_partials(s, in, r, 0u, s.tokens, red, rr);
+            }
             __syncthreads();
             if (tid < s.tokens) router_logit_finish(s, in, w, r, tid, red[tid]);
             __syncthreads();

@@ -200,20 +200,28 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 // red[t - t0][wave] (four waves take interleaved quarters of the row with every lane's float4
 // loads in flight).
 // Threads 0..255: the first 8 float4 of their share of expert row b (issued early by the caller).
+// The row's first 8192 weights and the same columns of token t0's activations, requested
+// together so that both arrive within one memory latency.
 struct RouterRow {
     float4 wv[8];
+    float4 xv[8];
     int nv;
 };
 __device__ __forceinline__ void router_row_load(const MoeShape& s, const MoeInputs& in, uint32_t b,
-                                                RouterRow& rr) {
+                                                uint32_t t0, RouterRow& rr) {
     const uint32_t r = threadIdx.x;
     const float4* row = reinterpret_cast<const float4*>(in.router + (uint64_t)b * s.width);
+    const float4* xr = reinterpret_cast<const float4*>(in.x + (uint64_t)t0 * s.width);
     const uint32_t n4 = s.width / 4u;
     rr.nv = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const uint32_t i = r + 256u * j;
-        if (i < n4) { rr.wv[j] = row[i]; rr.nv = j + 1; }
+        if (i < n4) {
+            rr.wv[j] = row[i];
+            rr.xv[j] = xr[i];
+            rr.nv = j + 1;
+        }
     }
 }
 
@@ -232,7 +240,7 @@ __device__ __forceinline__ void router_row_partials(const MoeShape& s, const Moe
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if (j < nv) {
-                const float4 a = wv[j], c = xr[r + 256u * j];
+                const float4 a = wv[j], c = t == t0 ? rr.xv[j] : xr[r + 256u * j];
                 acc += (double)a.x * (double)c.x;
                 acc += (double)a.y * (double)c.y;
                 acc += (double)a.z * (double)c.z;
@@ -286,7 +294,7 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
     // latency.
     RouterRow rr;
     const bool routes = s.routing != kRouteGiven && b < s.experts;
-    if (routes) router_row_load(s, in, b, rr);
+    if (routes) router_row_load(s, in, b, t0, rr);
     if (b == 0 && blockIdx.y == 0 && threadIdx.x < 2) {
         MoeHeader* h = ws_ptr<MoeHeader>(w, w.off_header);
         (&h->status)[threadIdx.x] = 0;
@@ -1307,7 +1315,7 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_fused(const MoeSha
         for (uint32_t r = blockIdx.x; r < s.experts; r += gridDim.x) {
             if (wave < 4) {
                 RouterRow rr;
-                router_row_load(s, in, r, rr);
+                router_row_load(s, in, r, 0u, rr);
                 router_row_partials(s, in, r, 0u, s.tokens, red, rr);
             }
             __syncthreads();

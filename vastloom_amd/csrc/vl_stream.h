@@ -439,9 +439,10 @@ __device__ __forceinline__ uint32_t active_waves(uint32_t nw, uint32_t total) {
 __device__ __forceinline__ uint32_t range_begin(uint32_t w, uint32_t nw, uint32_t total) {
     return w < nw ? (uint32_t)((uint64_t)w * total / nw) : total;
 }
-// The wave whose range holds unit u.
+// The wave whose range holds unit u (a 32-bit division whenever the product fits in 32 bits).
 __device__ __forceinline__ uint32_t wave_of_unit(uint32_t u, uint32_t nw, uint32_t total) {
-    return (uint32_t)((((uint64_t)u + 1u) * nw - 1u) / total);
+    const uint64_t q = ((uint64_t)u + 1u) * nw - 1u;
+    return (q >> 32) ? (uint32_t)(q / total) : (uint32_t)q / total;
 }
 
 __device__ __forceinline__ void store_shared(float* p, float v) {

@@ -881,8 +881,12 @@ struct GateUp {
 // Dynamic LDS of the gate/up kernel, from byte 0: decode tables, staged activation limbs (LDS
 // path), the 2^-e scales of the activation blocks, per-wave flags, the routing state and the
 // weight pointers.
+// Layers with at most kPtrTabExperts routed experts keep every expert's gate and up pointers in
+// LDS (loaded while the block routes), so the active experts' pointers cost no memory latency
+// after routing.
+constexpr uint32_t kPtrTabExperts = 256;
 struct GateUpLds {
-    uint32_t stage, scale, flags, route, wptr, bytes;
+    uint32_t stage, scale, flags, route, wptr, ptab, bytes;
 };
 __host__ __device__ inline GateUpLds gateup_lds(uint32_t table_bytes, uint32_t stage_bytes,
                                                 uint32_t xblocks) {
@@ -892,7 +896,8 @@ __host__ __device__ inline GateUpLds gateup_lds(uint32_t table_bytes, uint32_t s
     l.flags = l.scale + xblocks * 8u * 4u;
     l.route = (l.flags + kStreamWaves * 4u + 15u) & ~15u;
     l.wptr = (l.route + (uint32_t)sizeof(RouteLds) + 15u) & ~15u;
-    l.bytes = l.wptr + kMaxActive * 2u * 8u;
+    l.ptab = l.wptr + kMaxActive * 2u * 8u;
+    l.bytes = l.ptab + (kPtrTabExperts + 1u) * 2u * 8u;
     return l;
 }
 
@@ -916,6 +921,14 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_gateup(const MoeSh
         const uint32_t first = fillers ? s.tokens : 0u;
         const uint32_t tid = threadIdx.x - 64u * first, nthr = blockDim.x - 64u * first;
         fill_tables<FMT>(lds, tid, nthr);
+        if (s.experts <= kPtrTabExperts) {
+            uint64_t* pt = reinterpret_cast<uint64_t*>(lds + lay.ptab);
+            const uint32_t ne = s.experts + (s.has_shared ? 1u : 0u);
+            for (uint32_t i = tid; i < 2u * ne; i += nthr) {
+                const MoeExpert& ex = in.experts[i / 2u];
+                pt[i] = reinterpret_cast<uint64_t>((i % 2u) ? ex.up : ex.gate);
+            }
+        }
         if (LDS) {
             const uint4* src = ws_ptr<const uint4>(w, w.off_xlimbs);
             uint4* dst = reinterpret_cast<uint4*>(lds + lay.stage);
@@ -932,9 +945,15 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_gateup(const MoeSh
     }
     const bool any_nonfinite = block_any(nonfinite != 0, reinterpret_cast<uint32_t*>(lds + lay.flags));
     build_active(s, w, blockIdx.x == 0, any_nonfinite, rt);
+    const uint64_t* pt = reinterpret_cast<const uint64_t*>(lds + lay.ptab);
     for (uint32_t i = threadIdx.x; i < 2u * rt.n_active; i += blockDim.x) {
-        const MoeExpert& ex = in.experts[rt.act[i / 2u].expert];
-        wptr[i] = (i % 2u) ? ex.up : ex.gate;
+        const uint32_t e = rt.act[i / 2u].expert;
+        if (s.experts <= kPtrTabExperts) {
+            wptr[i] = reinterpret_cast<const uint8_t*>(pt[2u * e + i % 2u]);
+        } else {
+            const MoeExpert& ex = in.experts[e];
+            wptr[i] = (i % 2u) ? ex.up : ex.gate;
+        }
     }
     __syncthreads();
     GateUp<FMT, NT, LDS> pol;

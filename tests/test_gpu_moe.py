@@ -183,6 +183,24 @@ def test_tied_router_rows_route_to_lower_ids(ops, lib, oracle, experts_n, tokens
             assert e % 4 == 0 or (e - 1) in ids[t], (t, ids[t])
 
 
+@pytest.mark.parametrize("experts_n,tokens,routing_name", [(300, 1, "learned"), (600, 2, "softmax"),
+                                                         (1024, 1, "learned")])
+def test_wide_expert_pools(ops, lib, oracle, experts_n, tokens, routing_name):
+    """Pools above 256 experts: the gate/up blocks take the experts' pointers from global memory
+    instead of their LDS table, and the top-k keeps 8 or 16 keys per lane."""
+    print(f"[moe wide] E={experts_n} tokens={tokens} {routing_name}", flush=True)
+    rng = np.random.default_rng(11 + experts_n)
+    from vastloom_amd.workloads import MoeWorkload
+    sem = "qwen" if routing_name == "softmax" else "deepseek"
+    H, F, K = 256, 256, 8
+    wl = MoeWorkload("wide", 19, H, F, experts_n, K, tokens, IQ2_XXS, IQ2_XXS, 0.01, sem)
+    experts = [make_expert(rng, IQ2_XXS, IQ2_XXS, H, F) for _ in range(experts_n)]
+    shared = make_expert(rng, IQ2_XXS, IQ2_XXS, H, F) if sem == "deepseek" else None
+    x = rng.standard_normal((tokens, H)).astype(np.float32)
+    routing = lib.ROUTE_SOFTMAX if routing_name == "softmax" else lib.ROUTE_LEARNED
+    _check_layer(ops, lib, oracle, wl, experts, shared, sem, routing_name, routing, x)
+
+
 def test_bad_table_route_is_refused(ops, lib, oracle):
     rng = np.random.default_rng(1)
     from vastloom_amd.workloads import MoeWorkload

@@ -923,28 +923,71 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_gateup(const MoeSh
     if (!fillers || wave >= s.tokens) {
         const uint32_t first = fillers ? s.tokens : 0u;
         const uint32_t tid = threadIdx.x - 64u * first, nthr = blockDim.x - 64u * first;
-        fill_tables<FMT>(lds, tid, nthr);
-        if (s.experts <= kPtrTabExperts) {
-            uint64_t* pt = reinterpret_cast<uint64_t*>(lds + lay.ptab);
-            const uint32_t ne = s.experts + (s.has_shared ? 1u : 0u);
-            for (uint32_t i = tid; i < 2u * ne; i += nthr) {
-                const MoeExpert& ex = in.experts[i / 2u];
-                pt[i] = reinterpret_cast<uint64_t>((i % 2u) ? ex.up : ex.gate);
-            }
-        }
-        if (LDS) {
-            const uint4* src = ws_ptr<const uint4>(w, w.off_xlimbs);
-            uint4* dst = reinterpret_cast<uint4*>(lds + lay.stage);
-            copy_to_lds(dst, src, stage_bytes / 16u, tid, nthr);
-        }
+        // The first batch of every copy below is loaded before anything is stored, so the phase
+        // waits about one memory latency: decode tables, activation limbs, slot exponents and
+        // flags, and the experts' gate/up pointers. Larger copies finish in plain loops.
+        using TF = TableFill<FMT>;
+        constexpr uint32_t XB = 4, SB = 2, PB = 2;
+        TF tf;
+        const bool one = TF::single(nthr);
+        if (one) tf.load(tid, nthr);
+        const uint4* xsrc = ws_ptr<const uint4>(w, w.off_xlimbs);
+        uint4* xdst = reinterpret_cast<uint4*>(lds + lay.stage);
+        const uint32_t xn = LDS ? stage_bytes / 16u : 0u;
+        uint4 xv[XB];
+#pragma unroll
+        for (uint32_t j = 0; j < XB; ++j)
+            if (tid + j * nthr < xn) xv[j] = ld_u4(xsrc + tid + j * nthr);
         const int* xe = ws_ptr<const int>(w, w.off_xexp);
         const uint32_t* xf = ws_ptr<const uint32_t>(w, w.off_xflags);
         float* sc = reinterpret_cast<float*>(lds + lay.scale);
-        for (uint32_t i = tid; i < w.xblocks * 8u; i += nthr) {
+        const uint32_t sn = w.xblocks * 8u;
+        int ev[SB];
+        uint32_t fv[SB];
+#pragma unroll
+        for (uint32_t j = 0; j < SB; ++j) {
+            const uint32_t i = tid + j * nthr;
+            ev[j] = 0;
+            fv[j] = 0;
+            if (i < sn && (i & 7u) < s.tokens) {
+                ev[j] = *gp(xe + i);
+                fv[j] = *gp(xf + i);
+            }
+        }
+        uint64_t* pt = reinterpret_cast<uint64_t*>(lds + lay.ptab);
+        const uint32_t pn = s.experts <= kPtrTabExperts ? 2u * (s.experts + (s.has_shared ? 1u : 0u)) : 0u;
+        auto ptr_word = [&](uint32_t i) {
+            const MoeExpert& ex = in.experts[i / 2u];
+            return reinterpret_cast<uint64_t>((i % 2u) ? ex.up : ex.gate);
+        };
+        uint64_t pv[PB];
+#pragma unroll
+        for (uint32_t j = 0; j < PB; ++j)
+            if (tid + j * nthr < pn) pv[j] = ptr_word(tid + j * nthr);
+        if (one) tf.store(lds, tid, nthr);
+        else fill_tables<FMT>(lds, tid, nthr);
+#pragma unroll
+        for (uint32_t j = 0; j < XB; ++j)
+            if (tid + j * nthr < xn) xdst[tid + j * nthr] = xv[j];
+        for (uint32_t i = tid + XB * nthr; i < xn; i += nthr) xdst[i] = ld_u4(xsrc + i);
+#pragma unroll
+        for (uint32_t j = 0; j < SB; ++j) {
+            const uint32_t i = tid + j * nthr;
+            if (i < sn) {
+                const bool live = (i & 7u) < s.tokens;
+                sc[i] = live ? __builtin_amdgcn_ldexpf(1.0f, -ev[j]) : 0.0f;
+                if (live && fv[j]) nonfinite = 1;
+            }
+        }
+        for (uint32_t i = tid + SB * nthr; i < sn; i += nthr) {
             const bool live = (i & 7u) < s.tokens;
             sc[i] = live ? __builtin_amdgcn_ldexpf(1.0f, -*gp(xe + i)) : 0.0f;
             if (live && *gp(xf + i)) nonfinite = 1;
         }
+#pragma unroll
+        for (uint32_t j = 0; j < PB; ++j)
+            if (tid + j * nthr < pn) pt[tid + j * nthr] = pv[j];
+        for (uint32_t i = tid + PB * nthr; i < pn; i += nthr) pt[i] = ptr_word(i);
     }
     const bool any_nonfinite = block_any(nonfinite != 0, reinterpret_cast<uint32_t*>(lds + lay.flags));
     build_active(s, w, blockIdx.x == 0, any_nonfinite, rt);
@@ -1205,6 +1248,11 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_down(const MoeShap
     ActiveExpert* act = reinterpret_cast<ActiveExpert*>(lds + lay.act);
     const uint8_t** wptr = reinterpret_cast<const uint8_t**>(lds + lay.wptr);
     int8_t* slab = ws_ptr<int8_t>(w, w.off_hslab) + (uint64_t)blockIdx.x * w.stage * eb;
+    // The decode tables' source words are requested before the copies below, so the two wait
+    // for one memory latency together.
+    TableFill<FMT> tf;
+    const bool one = TableFill<FMT>::single(blockDim.x);
+    if (one) tf.load(threadIdx.x, blockDim.x);
     {
         const uint32_t words = w.max_active * (uint32_t)(sizeof(ActiveExpert) / 4u);
         const uint32_t* src = ws_ptr<const uint32_t>(w, w.off_active);
@@ -1215,7 +1263,8 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_down(const MoeShap
         uint32_t* cdst = reinterpret_cast<uint32_t*>(lds + lay.comb);
         for (uint32_t i = threadIdx.x; i < cwords; i += blockDim.x) cdst[i] = *gp(csrc + i);
     }
-    fill_tables<FMT>(lds);
+    if (one) tf.store(lds, threadIdx.x, blockDim.x);
+    else fill_tables<FMT>(lds);
     const uint32_t n_active = uni(n_active_raw);
     const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * WV, TU);
     // Experts this block's units touch.

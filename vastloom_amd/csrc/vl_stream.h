@@ -103,52 +103,64 @@ __host__ __device__ inline uint32_t units_per_row(uint32_t type, uint32_t cols) 
 // Exponent blocks (256 columns) of a row of activations.
 __host__ __device__ inline uint32_t exp_blocks(uint32_t cols) { return (cols + 255u) / 256u; }
 
-// Fills the block's decode tables in LDS, threads tid0, tid0 + nthr, ... of the block taking
-// part (the caller synchronizes).
+// Decode tables into LDS in two halves, so that a prologue can issue its other global loads
+// between them: load() fetches up to kB source words per thread (threads tid0, tid0 + nthr, ...,
+// word i0 + j * nthr), store() writes them. IQ2_XXS / IQ3_XXS: word i < nB is copies 2(i % 8) and
+// 2(i % 8) + 1 of selector entry i / 8 (16 bytes into the lower half of the entry's 256-byte
+// row), the nA words after it the same for the grid entries. IQ1_S: word i is grid entry i.
 template <uint32_t FMT>
-__device__ __forceinline__ void fill_tables(uint8_t* lds, uint32_t tid0 = threadIdx.x,
-                                            uint32_t nthr = blockDim.x) {
-    // Eight source loads per thread are issued before their stores, so a thread waits about one
-    // memory latency per eight stores rather than one per store.
-    constexpr int B = 8;
-    if (FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_IQ3_XXS) {
-        // Store i writes copies 2(i % 8) and 2(i % 8) + 1 of entry i / 8 (16 bytes) into the lower
-        // half of the entry's 256-byte row.
-        constexpr uint32_t per = kTabCopies / 2u;                   // 16-byte stores per entry
-        constexpr uint32_t nB = 128u * per, nA = 256u * per;
-        for (uint32_t i0 = tid0; i0 < nB + nA; i0 += B * nthr) {
-            uint64_t v[B];
+struct TableFill {
+    static constexpr int kB = 8;
+    static constexpr uint32_t per = kTabCopies / 2u;  // 16-byte stores per IQ2/IQ3 entry
+    static constexpr uint32_t nB = 128u * per, nA = 256u * per;
+    static constexpr uint32_t words = FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_IQ3_XXS ? nB + nA
+                                      : FMT == VL_TYPE_IQ1_S                             ? 2048u
+                                                                                         : 0u;
+    uint64_t v[kB];
+
+    __device__ void load(uint32_t i0, uint32_t nthr) {
 #pragma unroll
-            for (int j = 0; j < B; ++j) {
-                const uint32_t i = i0 + j * nthr;
-                v[j] = 0;
+        for (int j = 0; j < kB; ++j) {
+            const uint32_t i = i0 + j * nthr;
+            v[j] = 0;
+            if (FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_IQ3_XXS) {
                 if (i < nB) v[j] = FMT == VL_TYPE_IQ2_XXS ? g_tables.sign_sel[i / per] : g_tables.iq3_sel[i / per];
                 else if (i < nB + nA)
                     v[j] = FMT == VL_TYPE_IQ2_XXS ? g_tables.iq2_codes[(i - nB) / per] : g_tables.iq3_pm[(i - nB) / per];
+            } else if (FMT == VL_TYPE_IQ1_S) {
+                if (i < words) v[j] = g_tables.iq1_codes[i];
             }
+        }
+    }
+    __device__ void store(uint8_t* lds, uint32_t i0, uint32_t nthr) const {
 #pragma unroll
-            for (int j = 0; j < B; ++j) {
-                const uint32_t i = i0 + j * nthr;
+        for (int j = 0; j < kB; ++j) {
+            const uint32_t i = i0 + j * nthr;
+            if (i >= words) continue;
+            if (FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_IQ3_XXS) {
                 const uint32_t k = i < nB ? i : i - nB;
                 const uint32_t off = (i < nB ? kTabB : kTabA) + (k / per) * 256u + (k % per) * 16u;
-                if (i < nB + nA)
-                    *reinterpret_cast<uint4*>(lds + off) = make_uint4(lo32(v[j]), hi32(v[j]), lo32(v[j]), hi32(v[j]));
+                *reinterpret_cast<uint4*>(lds + off) = make_uint4(lo32(v[j]), hi32(v[j]), lo32(v[j]), hi32(v[j]));
+            } else {
+                reinterpret_cast<uint64_t*>(lds)[i] = v[j];
             }
         }
-    } else if (FMT == VL_TYPE_IQ1_S) {
-        for (uint32_t i0 = tid0; i0 < 2048u; i0 += B * nthr) {
-            uint64_t v[B];
-#pragma unroll
-            for (int j = 0; j < B; ++j) {
-                const uint32_t i = i0 + j * nthr;
-                v[j] = i < 2048u ? g_tables.iq1_codes[i] : 0u;
-            }
-#pragma unroll
-            for (int j = 0; j < B; ++j) {
-                const uint32_t i = i0 + j * nthr;
-                if (i < 2048u) reinterpret_cast<uint64_t*>(lds)[i] = v[j];
-            }
-        }
+    }
+    // Whether one load/store pair covers every word.
+    __device__ static bool single(uint32_t nthr) { return words <= kB * nthr; }
+};
+
+// The decode tables of FMT into LDS by threads tid0, tid0 + nthr, ... (the caller synchronizes);
+// eight source loads per thread are issued before their stores, so a thread waits about one
+// memory latency per eight stores rather than one per store.
+template <uint32_t FMT>
+__device__ __forceinline__ void fill_tables(uint8_t* lds, uint32_t tid0 = threadIdx.x,
+                                            uint32_t nthr = blockDim.x) {
+    using TF = TableFill<FMT>;
+    for (uint32_t i0 = tid0; i0 < TF::words; i0 += TF::kB * nthr) {
+        TF tf;
+        tf.load(i0, nthr);
+        tf.store(lds, i0, nthr);
     }
 }
 

@@ -344,19 +344,16 @@ struct TopKLds {
     uint32_t id[kMoeMaxTopK];
     float val[kMoeMaxTopK];
     double p[kMoeMaxTopK];
-    uint32_t skey[kMoeMaxTopK], sid[kMoeMaxTopK];  // the taken experts in ascending id
-    float sval[kMoeMaxTopK];
 };
 
 // Top-k of one token by one wave (all lanes active). Lane l holds experts l, l + 64, ... (PER of
-// them) with the selection keys of the router kernel (0: no expert). The reference ranks by key,
-// descending, equal keys in ascending id. Here the K-th largest key T is found bit by bit from
-// the top (the largest T with at least K keys >= T, counted with ballots); every key above T is
-// taken, then keys equal to T in ascending id until K are taken. The K taken experts are staged
-// in LDS and lane q < K places its expert at its rank among them. The experts thus come out in
-// the reference's rank order; lanes k < K then form the weights with the reference's float64
-// arithmetic, summing in rank order. Returns true when the token cannot be routed (fewer than K
-// experts, non-finite logits or a non-positive weight sum).
+// them) with the selection keys of the router kernel, and first sorts them by key, descending,
+// equal keys keeping ascending ids. Round k then takes the largest remaining key, ties to the
+// lowest id: a DPP wave maximum over the lanes' heads, the head's lane (a wave minimum of ids
+// only when several heads tie), and that lane drops its head. The experts thus come out in the
+// reference's rank order; lanes k < K then form the weights with the reference's float64
+// arithmetic, summing in rank order. Returns true when the token cannot be routed (non-finite
+// logits or a non-positive weight sum).
 template <int PER>
 __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* keys, uint32_t E,
                            uint32_t K, bool softmax, const MoeShape& s, TopKLds& tk,
@@ -377,57 +374,57 @@ __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* ke
             bad |= !isfinite(lv[i]);
         }
     }
-    auto count_ge = [&](uint32_t c) {
-        uint32_t n = 0;
+    // key[] is sorted in place; hid[] follows it. Values are read from lv/sv by id.
+    uint32_t hid[PER];
 #pragma unroll
-        for (int i = 0; i < PER; ++i) n += (uint32_t)__popcll(__ballot(key[i] >= c));
-        return n;
-    };
-    uint32_t T = 0;
-    for (int b = 31; b >= 0; --b) {
-        const uint32_t c = T | (1u << b);
-        if (count_ge(c) >= K) T = c;
-    }
-    // Finite keys stay below 0xff800000, so T + 1 does not wrap.
-    const uint32_t need = K - count_ge(T + 1u);
-    const uint64_t below = (1ull << lane) - 1ull;
-    uint32_t eq_before = 0, taken_before = 0;
+    for (int i = 0; i < PER; ++i) hid[i] = lane + 64u * i;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const uint64_t eq = __ballot(key[i] == T);
-        const bool take = key[i] > T || (key[i] == T && eq_before + (uint32_t)__popcll(eq & below) < need);
-        const uint64_t tb = __ballot(take);
-        if (take) {
-            const uint32_t q = taken_before + (uint32_t)__popcll(tb & below);
-            tk.skey[q] = key[i];
-            tk.sid[q] = lane + 64u * i;
-            tk.sval[q] = softmax ? lv[i] : sv[i];
-        }
-        eq_before += (uint32_t)__popcll(eq);
-        taken_before += (uint32_t)__popcll(tb);
-    }
-    __builtin_amdgcn_wave_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (lane < K) {
-        uint32_t id = 0, rank = 0;
-        float v = 0.0f;
-        if (T != 0) {
-            const uint32_t kq = tk.skey[lane];
-            id = tk.sid[lane];
-            v = tk.sval[lane];
-            for (uint32_t r = 0; r < K; ++r) {
-                const uint32_t kr = tk.skey[r];
-                rank += (kr > kq || (kr == kq && tk.sid[r] < id)) ? 1u : 0u;
+    for (int i = 1; i < PER; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j)
+            if (key[j] > key[j - 1]) {
+                const uint32_t tk_ = key[j], ti = hid[j];
+                key[j] = key[j - 1];
+                hid[j] = hid[j - 1];
+                key[j - 1] = tk_;
+                hid[j - 1] = ti;
             }
+    for (uint32_t k = 0; k < K; ++k) {
+        const uint32_t m = wave_max_u32(key[0]);
+        const bool top = key[0] == m && m != 0;
+        const uint64_t hit = __ballot(top);
+        uint32_t wl = 0;
+        if (hit == 0) {
+            bad = true;
+        } else if ((hit & (hit - 1)) == 0) {
+            wl = (uint32_t)__builtin_ctzll(hit);
         } else {
-            bad = true;  // fewer than K experts
-            rank = lane;
+            const uint32_t mid = wave_min_u32(top ? hid[0] : 0xffffffffu);
+            wl = (uint32_t)__builtin_ctzll(__ballot(top && hid[0] == mid));
         }
-        tk.id[rank] = id;
-        tk.val[rank] = v;
+        const uint32_t id = hit ? (uint32_t)__builtin_amdgcn_readlane((int)hid[0], wl) : 0u;
+        const uint32_t wi = id >> 6;
+        float l = lv[0], sc = sv[0];
+#pragma unroll
+        for (int i = 1; i < PER; ++i)
+            if (wi == (uint32_t)i) {
+                l = lv[i];
+                sc = sv[i];
+            }
+        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax ? l : sc), id & 63u));
+        if (lane == 0) {
+            tk.id[k] = id;
+            tk.val[k] = v;
+        }
+        if (lane == wl) {
+#pragma unroll
+            for (int i = 0; i + 1 < PER; ++i) {
+                key[i] = key[i + 1];
+                hid[i] = hid[i + 1];
+            }
+            key[PER - 1] = 0;
+        }
     }
-    __builtin_amdgcn_wave_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     double sum_all = 0.0, mx = 0.0;
     if (softmax) {
         // The largest key is the largest logit: the first selected expert's.

@@ -72,8 +72,9 @@ struct MoeWorkspace {
     uint64_t bytes;
     uint64_t off_header, off_logits, off_scores, off_keys, off_route_idx, off_route_w, off_active, off_combine,
         off_xexp, off_xflags, off_xlimbs, off_counters, off_rec_gu, off_rec_dn, off_h,
-        off_hslab, off_ypart, off_gweights, off_hlimbs, off_hscale, off_gbar;
+        off_hslab, off_ypart, off_gweights, off_hlimbs, off_hscale, off_gbar, off_lgpart;
     uint32_t grouped;                                 // more than kMoeMaxTokens tokens
+    uint32_t lg_slices;                               // column slices of the grouped router product
     uint32_t max_active, slots, waves, blocks;        // slots: MFMA token slots of a job
     uint32_t xslots, estride;                         // token strides of the limb and exponent arrays
     uint32_t tiles_gu, tiles_dn, hblocks, xblocks;  // gate/up and down tiles, h and x exponent blocks

@@ -82,6 +82,21 @@ __host__ __device__ inline uint32_t down_expert_bytes(uint32_t inter, uint32_t s
     return (inter / 32u) * slots * 128u;
 }
 
+// Router logits of grouped layers as a tiled product: kLgT tokens x kLgE experts per block,
+// kLgK columns staged per step.
+constexpr uint32_t kLgT = 64, kLgE = 64, kLgK = 32;
+
+// Column slices of the grouped router product: about two blocks per persistent block, at least
+// one k-step each, and at most 2^21 partial sums in all.
+static uint32_t router_slices(const MoeShape& s, uint32_t blocks) {
+    const uint64_t tiles = (uint64_t)((s.experts + kLgE - 1u) / kLgE) * ((s.tokens + kLgT - 1u) / kLgT);
+    uint64_t n = (2u * (uint64_t)blocks + tiles - 1u) / tiles;
+    const uint64_t steps = s.width / kLgK, cap = (1ull << 21) / ((uint64_t)s.tokens * s.experts);
+    if (n > steps) n = steps;
+    if (n > cap) n = cap;
+    return n ? (uint32_t)n : 1u;
+}
+
 MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base) {
     MoeWorkspace w{};
     w.base = static_cast<uint8_t*>(base);
@@ -128,6 +143,9 @@ MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base
     w.off_hscale = o; o = align256(o + (w.grouped ? 0u : A * w.hblocks * 8u * 4u));
     // Grid barrier words: generation, then one arrival word per block.
     w.off_gbar = o; o = align256(o + (w.grouped ? 0u : (1u + (uint64_t)blocks) * 4u));
+    // Grouped layers: f64 partial router logits of each column slice, [slice][token][expert].
+    w.lg_slices = w.grouped ? router_slices(s, blocks) : 0u;
+    w.off_lgpart = o; o = align256(o + (uint64_t)w.lg_slices * T * s.experts * 8u);
     w.bytes = o;
     return w;
 }
@@ -263,11 +281,11 @@ __device__ __forceinline__ void router_row_partials(const MoeShape& s, const Moe
 // Token t's logit of expert b from the four partial sums (added in wave order), its score and
 // its selection key: learned routing ranks score + bias (the reference's float keys), softmax
 // routing ranks probabilities, which order as the logits do.
-__device__ __forceinline__ void router_logit_finish(const MoeShape& s, const MoeInputs& in,
-                                                    const MoeWorkspace& w, uint32_t b, uint32_t t,
-                                                    const double (&red)[4]) {
+__device__ __forceinline__ void router_logit_store(const MoeShape& s, const MoeInputs& in,
+                                                   const MoeWorkspace& w, uint32_t b, uint32_t t,
+                                                   double sum) {
     const uint64_t i = (uint64_t)t * s.experts + b;
-    const float logit = (float)(((red[0] + red[1]) + red[2]) + red[3]);
+    const float logit = (float)sum;
     float score = 0.0f;
     uint32_t key;
     if (s.routing == kRouteSoftmax) {
@@ -279,6 +297,89 @@ __device__ __forceinline__ void router_logit_finish(const MoeShape& s, const Moe
     store_shared(ws_ptr<float>(w, w.off_logits) + i, logit);
     store_shared(ws_ptr<float>(w, w.off_scores) + i, score);
     store_shared_u32(ws_ptr<uint32_t>(w, w.off_keys) + i, key);
+}
+__device__ __forceinline__ void router_logit_finish(const MoeShape& s, const MoeInputs& in,
+                                                    const MoeWorkspace& w, uint32_t b, uint32_t t,
+                                                    const double (&red)[4]) {
+    router_logit_store(s, in, w, b, t, ((red[0] + red[1]) + red[2]) + red[3]);
+}
+
+// Grouped layers: the router logits as a tiled product. Block (i, j, z) sums columns of slice z
+// for tokens kLgT*j .. and experts kLgE*i ..; each thread holds 4 tokens x 4 experts of f64 sums,
+// adding the exact f64 products of the f32 inputs column by column in ascending order. The next
+// step's inputs are loaded while the current step is summed.
+__global__ void __launch_bounds__(256) k_moe_logits_part(const MoeShape s, const MoeInputs in,
+                                                         const MoeWorkspace w) {
+    __shared__ __align__(16) float xs[kLgK][kLgT + 4];
+    __shared__ __align__(16) float rs[kLgK][kLgE + 4];
+    const uint32_t T = s.tokens, E = s.experts, H = s.width;
+    const uint32_t e0 = blockIdx.x * kLgE, t0 = blockIdx.y * kLgT, z = blockIdx.z;
+    const uint32_t steps = H / kLgK, S = w.lg_slices;
+    const uint32_t k0 = (uint32_t)((uint64_t)z * steps / S), k1 = (uint32_t)((uint64_t)(z + 1u) * steps / S);
+    const uint32_t tid = threadIdx.x, tx = tid % 16u, ty = tid / 16u;
+    // Staging: 512 float4 per operand tile, two per thread: row q / 8, columns 4 (q % 8) ...
+    float4 xv[2], rv[2];
+    auto load = [&](uint32_t ks) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t q = tid + 256u * h, row = q / 8u, col = ks * kLgK + 4u * (q % 8u);
+            xv[h] = t0 + row < T ? *reinterpret_cast<const float4*>(in.x + (uint64_t)(t0 + row) * H + col)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+            rv[h] = e0 + row < E ? *reinterpret_cast<const float4*>(in.router + (uint64_t)(e0 + row) * H + col)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    double acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+    if (k0 < k1) load(k0);
+    for (uint32_t ks = k0; ks < k1; ++ks) {
+        __syncthreads();  // the previous step's reads are done
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t q = tid + 256u * h, row = q / 8u, c = 4u * (q % 8u);
+            xs[c][row] = xv[h].x; xs[c + 1][row] = xv[h].y; xs[c + 2][row] = xv[h].z; xs[c + 3][row] = xv[h].w;
+            rs[c][row] = rv[h].x; rs[c + 1][row] = rv[h].y; rs[c + 2][row] = rv[h].z; rs[c + 3][row] = rv[h].w;
+        }
+        __syncthreads();
+        if (ks + 1u < k1) load(ks + 1u);
+#pragma unroll 8
+        for (uint32_t k = 0; k < kLgK; ++k) {
+            const float4 a = *reinterpret_cast<const float4*>(&xs[k][4u * ty]);
+            const float4 b = *reinterpret_cast<const float4*>(&rs[k][4u * tx]);
+            const double av[4] = {(double)a.x, (double)a.y, (double)a.z, (double)a.w};
+            const double bv[4] = {(double)b.x, (double)b.y, (double)b.z, (double)b.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fma(av[i], bv[j], acc[i][j]);
+        }
+    }
+    double* part = ws_ptr<double>(w, w.off_lgpart);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t t = t0 + 4u * ty + i;
+        if (t >= T) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t e = e0 + 4u * tx + j;
+            if (e < E) part[((uint64_t)z * T + t) * E + e] = acc[i][j];
+        }
+    }
+}
+
+// Grouped layers: each (token, expert) logit is the sum of its slices' partial sums in slice
+// order, rounded to f32, with its score and selection key.
+__global__ void __launch_bounds__(256) k_moe_logits_finish(const MoeShape s, const MoeInputs in,
+                                                           const MoeWorkspace w) {
+    const uint64_t n = (uint64_t)s.tokens * s.experts, i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const double* part = ws_ptr<const double>(w, w.off_lgpart);
+    double sum = part[i];
+    for (uint32_t z = 1; z < w.lg_slices; ++z) sum += part[(uint64_t)z * n + i];
+    router_logit_store(s, in, w, (uint32_t)(i % s.experts), (uint32_t)(i / s.experts), sum);
 }
 
 // Block (b, g): expert row b's logits for the tokens of group g (tokens 8g .. 8g + 7), then the
@@ -2052,12 +2153,23 @@ static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, con
         if (ev) (void)hipEventRecord(ev[stage], st);
     };
     mark(kStageRouter);
-    const uint32_t router_blocks = s.routing == kRouteGiven ? 1u : s.experts;
+    // The router kernel zeroes the counters and forms the activation limbs; the logits come
+    // from the tiled product.
     const uint32_t groups = (s.tokens + kMoeMaxTokens - 1u) / kMoeMaxTokens;
-    hipLaunchKernelGGL(k_moe_router, dim3(router_blocks > w.xblocks ? router_blocks : w.xblocks, groups),
-                       dim3(256), 0, st, s, in, w);
+    MoeShape sx = s;
+    sx.routing = kRouteGiven;
+    hipLaunchKernelGGL(k_moe_router, dim3(w.xblocks, groups), dim3(256), 0, st, sx, in, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (s.routing != kRouteGiven) {
+        hipLaunchKernelGGL(k_moe_logits_part,
+                           dim3((s.experts + kLgE - 1u) / kLgE, (s.tokens + kLgT - 1u) / kLgT, w.lg_slices),
+                           dim3(256), 0, st, s, in, w);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        const uint64_t n = (uint64_t)s.tokens * s.experts;
+        hipLaunchKernelGGL(k_moe_logits_finish, dim3((uint32_t)((n + 255u) / 256u)), dim3(256), 0, st, s, in, w);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(k_moe_route_many, dim3((s.tokens + kStreamWaves - 1u) / kStreamWaves),
                        dim3(kStreamThreads), 0, st, s, in, w);
     if ((e = hipGetLastError()) != hipSuccess) return e;

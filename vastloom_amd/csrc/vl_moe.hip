@@ -1265,41 +1265,62 @@ struct Down {
 
 // h of experts a0..a1 -> limbs (dst, [expert - a0][inter/32][NT][4][32]) with one exponent per
 // 256-row block and slot from the gate/up kernel's maxima; scale[(a - a0)][block][8] = 2^-e.
+// load() requests one batch of kB quads per thread (quads i0 + j * blockDim.x) and, with the
+// first batch, this thread's scale maximum; store() converts and writes them, so a thread waits
+// one memory latency per batch. ntok[a * stride] is expert a's token count.
 template <int NT>
-__device__ __forceinline__ void convert_h(const MoeWorkspace& w, uint32_t inter, uint32_t a0,
-                                          uint32_t a1, const uint32_t* ntok, uint32_t ntok_stride,
-                                          int8_t* dst, float* scale) {
-    const uint32_t* hmax = counters_of(w).hmax;
-    const float* h = ws_ptr<const float>(w, w.off_h);
-    const uint32_t na = a1 - a0 + 1u;
-    for (uint32_t i = threadIdx.x; i < na * w.hblocks * 8u; i += blockDim.x) {
-        const uint32_t m = *gp(hmax + (uint64_t)a0 * w.hblocks * 8u + i);
-        scale[i] = __builtin_amdgcn_ldexpf(1.0f, -limb_exponent(__uint_as_float(m)));
+struct HConvert {
+    static constexpr int kB = 8;
+    const MoeWorkspace* w;
+    const uint32_t* ntok;
+    uint32_t inter, a0, stride, quads, total, nsc;
+    float4 f4[kB];
+    uint32_t mx[kB], sm;
+
+    __device__ void init(const MoeWorkspace& ws, uint32_t inter_, uint32_t a0_, uint32_t a1,
+                         const uint32_t* ntok_, uint32_t stride_) {
+        w = &ws;
+        ntok = ntok_;
+        stride = stride_;
+        inter = inter_;
+        a0 = a0_;
+        quads = inter / 4u;
+        total = (a1 - a0 + 1u) * NT * quads;
+        nsc = (a1 - a0 + 1u) * ws.hblocks * 8u;
     }
-    // Eight quads per thread have their loads in flight before any is converted.
-    constexpr int B = 8;
-    const uint32_t quads = inter / 4u, total = na * NT * quads;
-    for (uint32_t i0 = threadIdx.x; i0 < total; i0 += B * blockDim.x) {
-        float4 f4[B];
-        uint32_t mx[B];
-        bool live[B];
+    __device__ uint32_t tokens(uint32_t a) const { return ntok[a * stride]; }
+    __device__ bool live(uint32_t i) const {
+        return i < total && (i / quads) % NT < tokens(a0 + i / (quads * NT));
+    }
+    __device__ void load(uint32_t i0) {
+        const uint32_t* hmax = counters_of(*w).hmax;
+        const float* h = ws_ptr<const float>(*w, w->off_h);
+        if (i0 == threadIdx.x && threadIdx.x < nsc)
+            sm = *gp(hmax + (uint64_t)a0 * w->hblocks * 8u + threadIdx.x);
 #pragma unroll
-        for (int j = 0; j < B; ++j) {
+        for (int j = 0; j < kB; ++j) {
             const uint32_t i = i0 + j * blockDim.x;
-            const uint32_t q = i % quads, sl = (i / quads) % NT, al = i / (quads * NT);
-            const uint32_t a = a0 + al, col = 4u * q;
-            live[j] = i < total && sl < ntok[a * ntok_stride];
-            if (live[j]) {
-                mx[j] = *gp(hmax + ((uint64_t)a * w.hblocks + col / 256u) * 8u + sl);
+            const uint32_t q = i % quads, sl = (i / quads) % NT, a = a0 + i / (quads * NT), col = 4u * q;
+            if (live(i)) {
+                mx[j] = *gp(hmax + ((uint64_t)a * w->hblocks + col / 256u) * 8u + sl);
                 f4[j] = ld_f4(h + ((uint64_t)a * NT + sl) * inter + col);
             }
         }
+    }
+    __device__ void store(uint32_t i0, int8_t* dst, float* scale) const {
+        if (i0 == threadIdx.x) {
+            const uint32_t* hmax = counters_of(*w).hmax;
+            if (threadIdx.x < nsc) scale[threadIdx.x] = __builtin_amdgcn_ldexpf(1.0f, -limb_exponent(__uint_as_float(sm)));
+            for (uint32_t i = threadIdx.x + blockDim.x; i < nsc; i += blockDim.x) {
+                const uint32_t m = *gp(hmax + (uint64_t)a0 * w->hblocks * 8u + i);
+                scale[i] = __builtin_amdgcn_ldexpf(1.0f, -limb_exponent(__uint_as_float(m)));
+            }
+        }
 #pragma unroll
-        for (int j = 0; j < B; ++j) {
-            if (!live[j]) continue;
+        for (int j = 0; j < kB; ++j) {
             const uint32_t i = i0 + j * blockDim.x;
-            const uint32_t q = i % quads, sl = (i / quads) % NT, al = i / (quads * NT);
-            const uint32_t col = 4u * q;
+            if (!live(i)) continue;
+            const uint32_t q = i % quads, sl = (i / quads) % NT, al = i / (quads * NT), col = 4u * q;
             const float v[4] = {f4[j].x, f4[j].y, f4[j].z, f4[j].w};
             uint32_t packed[4];
             limbs4(v, limb_exponent(__uint_as_float(mx[j])), packed);
@@ -1309,13 +1330,26 @@ __device__ __forceinline__ void convert_h(const MoeWorkspace& w, uint32_t inter,
             for (int l = 0; l < 4; ++l) *reinterpret_cast<uint32_t*>(d + 32u * l) = packed[l];
         }
     }
+};
+
+// HConvert's halves over every batch; a thread with no quads still writes its scales.
+template <int NT>
+__device__ __forceinline__ void convert_h(const MoeWorkspace& w, uint32_t inter, uint32_t a0,
+                                          uint32_t a1, const uint32_t* ntok, uint32_t ntok_stride,
+                                          int8_t* dst, float* scale) {
+    HConvert<NT> c;
+    c.init(w, inter, a0, a1, ntok, ntok_stride);
+    for (uint32_t i0 = threadIdx.x; i0 < c.total || i0 == threadIdx.x; i0 += HConvert<NT>::kB * blockDim.x) {
+        c.load(i0);
+        c.store(i0, dst, scale);
+    }
 }
 
 // Dynamic LDS of the down kernel, from byte 0: decode tables, staged h limbs (LDS path), the 2^-e
 // scales of the staged experts' h blocks, the active list, the down weight pointers and the
 // combine table.
 struct DownLds {
-    uint32_t stage, scale, act, wptr, comb, bytes;
+    uint32_t stage, scale, act, wptr, comb, dtab, bytes;
 };
 __host__ __device__ inline DownLds down_lds(uint32_t table_bytes, uint32_t stage_bytes,
                                             uint32_t stage, uint32_t hblocks) {
@@ -1325,7 +1359,8 @@ __host__ __device__ inline DownLds down_lds(uint32_t table_bytes, uint32_t stage
     l.act = (l.scale + stage * hblocks * 8u * 4u + 15u) & ~15u;
     l.wptr = l.act + kMaxActive * (uint32_t)sizeof(ActiveExpert);
     l.comb = l.wptr + kMaxActive * 8u;
-    l.bytes = l.comb + kMoeMaxTokens * (kMoeMaxTopK + 1u) * (uint32_t)sizeof(CombineEntry);
+    l.dtab = (l.comb + kMoeMaxTokens * (kMoeMaxTopK + 1u) * (uint32_t)sizeof(CombineEntry) + 7u) & ~7u;
+    l.bytes = l.dtab + (kPtrTabExperts + 1u) * 8u;
     return l;
 }
 
@@ -1346,11 +1381,18 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_down(const MoeShap
     ActiveExpert* act = reinterpret_cast<ActiveExpert*>(lds + lay.act);
     const uint8_t** wptr = reinterpret_cast<const uint8_t**>(lds + lay.wptr);
     int8_t* slab = ws_ptr<int8_t>(w, w.off_hslab) + (uint64_t)blockIdx.x * w.stage * eb;
-    // The decode tables' source words are requested before the copies below, so the two wait
-    // for one memory latency together.
+    // The decode tables' source words and every expert's down pointer (pools of up to
+    // kPtrTabExperts) are requested before the active list and combine table are copied, so
+    // the block waits one memory latency for all of them, and none for the weight pointers
+    // after the barrier.
     TableFill<FMT> tf;
     const bool one = TableFill<FMT>::single(blockDim.x);
     if (one) tf.load(threadIdx.x, blockDim.x);
+    static_assert(stream_threads<NT>() > kPtrTabExperts, "one down pointer per thread");
+    uint64_t* dtab = reinterpret_cast<uint64_t*>(lds + lay.dtab);
+    const uint32_t dn = s.experts <= kPtrTabExperts ? s.experts + (s.has_shared ? 1u : 0u) : 0u;
+    uint64_t dv = 0;
+    if (threadIdx.x < dn) dv = reinterpret_cast<uint64_t>(in.experts[threadIdx.x].down);
     {
         const uint32_t words = w.max_active * (uint32_t)(sizeof(ActiveExpert) / 4u);
         const uint32_t* src = ws_ptr<const uint32_t>(w, w.off_active);
@@ -1363,6 +1405,7 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_down(const MoeShap
     }
     if (one) tf.store(lds, threadIdx.x, blockDim.x);
     else fill_tables<FMT>(lds);
+    if (threadIdx.x < dn) dtab[threadIdx.x] = dv;
     const uint32_t n_active = uni(n_active_raw);
     const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * WV, TU);
     // Experts this block's units touch.
@@ -1372,7 +1415,7 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_down(const MoeShap
     const uint32_t a1 = ub0 < ub1 ? ((ub1 - 1u) / UJ) / tiles : 0u;
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < n_active; i += blockDim.x)
-        wptr[i] = in.experts[act[i].expert].down;
+        wptr[i] = dn ? reinterpret_cast<const uint8_t*>(dtab[act[i].expert]) : in.experts[act[i].expert].down;
     if (ub0 < ub1)
         convert_h<NT>(w, s.inter, a0, a1, &act[0].ntok, (uint32_t)(sizeof(ActiveExpert) / 4u),
                       LDS ? reinterpret_cast<int8_t*>(lds + lay.stage) : slab,

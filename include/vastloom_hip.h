@@ -59,6 +59,29 @@ const char* vl_last_error(void);
  * (src/cuda/cuda_driver.cpp:1573-1576). */
 int vl_device_count(int* count);
 
+/* One visible GPU, as the reference's GpuInfo (include/vastloom/hardware/hardware_probe.hpp:27-35),
+ * read from the HIP runtime where the reference runs nvidia-smi (src/hardware/hardware_probe.cpp:
+ * 304-311). Temperature and power limit are not reported by the runtime: has_temperature and
+ * has_power_limit are 0, as the reference's empty optionals. */
+typedef struct vl_gpu_info {
+    char backend[16];        /* "hip" */
+    char name[128];          /* marketing name */
+    char arch[64];           /* e.g. "gfx950:sramecc+:xnack-" */
+    char driver_version[32]; /* hipDriverGetVersion, decimal */
+    uint64_t total_vram_bytes;
+    uint64_t free_vram_bytes; /* hipMemGetInfo on the device, at the call */
+    uint32_t compute_units;
+    uint32_t has_temperature;
+    uint32_t has_power_limit;
+    uint32_t reserved;
+} vl_gpu_info;
+int vl_gpu_probe(int device, vl_gpu_info* out);
+
+/* The runtime policy's VRAM hard limit from a probed GPU (src/safety/runtime_policy.cpp:137-141):
+ * min(80 % of total, free - 1 GiB) when more than 1 GiB is free, else 0 (no VRAM budget). The 80 %
+ * is the reference's percentage() (src/core/bytes.cpp:99-107): a long double product, truncated. */
+int vl_vram_hard_limit(uint64_t total_vram_bytes, uint64_t free_vram_bytes, uint64_t* limit);
+
 /* Bytes of a GGUF matrix and of its resident (tiled) device form. The tiled form holds the same
  * block bytes rearranged for aligned loads, plus zero rows up to a multiple of 32 rows.
  * Mirrors ggml_storage_bytes (include/vastloom/inference/ggml_quantization.hpp:93-97). */

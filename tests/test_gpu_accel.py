@@ -122,3 +122,19 @@ def test_governed_buffers(gov):
     assert e.value.name == "resource_exhausted"
     assert gov.snapshot()["reserved"] == before
     del t
+
+
+def test_gpu_probe_reports_the_device_and_a_policy_limit():
+    """The GPU probe (GpuInfo from the HIP runtime) and the runtime policy's VRAM limit from it."""
+    from vastloom_amd.accel import gpu_probe, vram_hard_limit
+    info = gpu_probe(0)
+    print(f"[gpu probe] {info}", flush=True)
+    assert info.backend == "hip" and info.name and info.arch.startswith("gfx")
+    assert int(info.driver_version) > 0
+    assert info.compute_units > 0
+    assert 0 < info.free_vram_bytes <= info.total_vram_bytes
+    assert info.temperature_celsius is None and info.power_limit_watts is None
+    limit = vram_hard_limit(info.total_vram_bytes, info.free_vram_bytes)
+    assert 0 < limit <= min(info.total_vram_bytes * 4 // 5, info.free_vram_bytes - GiB)
+    with pytest.raises(VlError):
+        gpu_probe(1 << 20)

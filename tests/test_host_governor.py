@@ -106,3 +106,27 @@ def test_buffer_refusals_before_any_device_call():
     with pytest.raises(VlError):
         Buffer(g, KIND_VRAM, 1024, tag="")
     assert g.snapshot()["reserved"] == [0, 0, 0, 0]
+
+
+def test_vram_hard_limit_follows_the_runtime_policy():
+    """min(80 % of total, free - 1 GiB) above 1 GiB free, else 0
+    (src/safety/runtime_policy.cpp:137-141; percentage() at src/core/bytes.cpp:99-107). The
+    expected values use exact rationals (the double 0.80 as a fraction); each case's product lies
+    far from an integer, so the reference's long double rounding cannot change its truncation."""
+    from fractions import Fraction
+
+    from vastloom_amd.accel import vram_hard_limit
+
+    def expected(total, free):
+        if free <= GiB:
+            return 0
+        return min(int(Fraction(total) * Fraction(0.80)), free - GiB)
+
+    cases = [(288 * GiB, 287 * GiB), (288 * GiB, 10 * GiB), (288 * GiB, GiB + 1), (288 * GiB, GiB),
+             (288 * GiB, 0), (80_000_000_000, 79_000_000_000), (24 * GiB, 23 * GiB + 7),
+             (17, 2 * GiB), ((1 << 64) - 1, (1 << 64) - 1)]
+    for total, free in cases:
+        assert vram_hard_limit(total, free) == expected(total, free), (total, free)
+    assert vram_hard_limit(288 * GiB, 287 * GiB) == 247_390_116_249  # floor(0.8 * 288 GiB)
+    assert vram_hard_limit(288 * GiB, 10 * GiB) == 9 * GiB
+    assert vram_hard_limit(288 * GiB, GiB) == 0

@@ -31,9 +31,20 @@ class VlError(RuntimeError):
 _U32, _U64, _I32, _P = C.c_uint32, C.c_uint64, C.c_int, C.c_void_p
 
 # name -> argument types (all return int status unless listed in _RESTYPES)
+class GpuInfo(C.Structure):
+    """vl_gpu_info (GpuInfo, include/vastloom/hardware/hardware_probe.hpp:27-35)."""
+    _fields_ = [("backend", C.c_char * 16), ("name", C.c_char * 128), ("arch", C.c_char * 64),
+                ("driver_version", C.c_char * 32), ("total_vram_bytes", C.c_uint64),
+                ("free_vram_bytes", C.c_uint64), ("compute_units", C.c_uint32),
+                ("has_temperature", C.c_uint32), ("has_power_limit", C.c_uint32),
+                ("reserved", C.c_uint32)]
+
+
 _SIGNATURES = {
     "vl_last_error": [],
     "vl_device_count": [C.POINTER(C.c_int)],
+    "vl_gpu_probe": [C.c_int, C.POINTER(GpuInfo)],
+    "vl_vram_hard_limit": [C.c_uint64, C.c_uint64, C.POINTER(C.c_uint64)],
     "vl_matrix_layout": [_U32, _U64, _U64, C.POINTER(_U64), C.POINTER(_U64)],
     "vl_pack_matrix": [_U32, _U64, _U64, _P, _P, _P],
     "vl_dequantize": [_U32, _U64, _U64, _P, _P, _P],

@@ -23,6 +23,40 @@ KIND_RAM, KIND_VRAM, KIND_STAGING, KIND_SCRATCH = (_lib.KIND_RAM, _lib.KIND_VRAM
 STATE_NAMES = {0: "normal", 1: "pressure", 2: "critical", 3: "emergency"}
 
 
+@dataclass(frozen=True)
+class GpuInfo:
+    """One visible GPU (``hardware::GpuInfo``, include/vastloom/hardware/hardware_probe.hpp:27-35),
+    from the HIP runtime; temperature and power limit are not reported (None)."""
+    backend: str
+    name: str
+    arch: str
+    driver_version: str
+    total_vram_bytes: int
+    free_vram_bytes: int
+    compute_units: int
+    temperature_celsius: float | None = None
+    power_limit_watts: float | None = None
+
+
+def gpu_probe(device: int = 0) -> GpuInfo:
+    """The GPU probe the runtime policy reads (src/hardware/hardware_probe.cpp:304-311 runs
+    nvidia-smi there)."""
+    info = _lib.GpuInfo()
+    check(lib().vl_gpu_probe(device, C.byref(info)), "vl_gpu_probe")
+    return GpuInfo(info.backend.decode(), info.name.decode(), info.arch.decode(),
+                   info.driver_version.decode(), info.total_vram_bytes, info.free_vram_bytes,
+                   info.compute_units)
+
+
+def vram_hard_limit(total_vram_bytes: int, free_vram_bytes: int) -> int:
+    """The runtime policy's VRAM hard limit of a probed GPU (src/safety/runtime_policy.cpp:137-141):
+    min(80 % of total, free - 1 GiB) above 1 GiB free, else 0."""
+    out = C.c_uint64()
+    check(lib().vl_vram_hard_limit(total_vram_bytes, free_vram_bytes, C.byref(out)),
+          "vl_vram_hard_limit")
+    return out.value
+
+
 def default_limits(**overrides) -> _lib.ResourceLimits:
     """ResourceLimits with the reference's defaults and every hard budget 0, then overrides."""
     limits = _lib.ResourceLimits()

@@ -67,6 +67,36 @@ int vl_device_count(int* count) {
     return VL_OK;
 }
 
+int vl_gpu_probe(int device, vl_gpu_info* out) {
+    if (!out) return fail(VL_INVALID_ARGUMENT, "out is null");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess && e != hipErrorNoDevice) return hip_fail(e, "hipGetDeviceCount");
+    if (e == hipErrorNoDevice || device < 0 || device >= n)
+        return fail(VL_INVALID_ARGUMENT, "no HIP device %d", device);
+    hipDeviceProp_t prop{};
+    if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    int cur = 0;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    size_t free_b = 0, total_b = 0;
+    e = hipMemGetInfo(&free_b, &total_b);
+    (void)hipSetDevice(cur);
+    if (e != hipSuccess) return hip_fail(e, "hipMemGetInfo");
+    int drv = 0;
+    if ((e = hipDriverGetVersion(&drv)) != hipSuccess) return hip_fail(e, "hipDriverGetVersion");
+    vl_gpu_info g{};
+    std::snprintf(g.backend, sizeof g.backend, "%s", "hip");
+    std::snprintf(g.name, sizeof g.name, "%s", prop.name);
+    std::snprintf(g.arch, sizeof g.arch, "%s", prop.gcnArchName);
+    std::snprintf(g.driver_version, sizeof g.driver_version, "%d", drv);
+    g.total_vram_bytes = total_b;
+    g.free_vram_bytes = free_b;
+    g.compute_units = (uint32_t)prop.multiProcessorCount;
+    *out = g;
+    return VL_OK;
+}
+
 int vl_matrix_layout(uint32_t type, uint64_t rows, uint64_t cols, uint64_t* gguf_bytes,
                      uint64_t* device_bytes) {
     vl_tiled_layout L;

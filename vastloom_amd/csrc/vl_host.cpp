@@ -100,6 +100,18 @@ void vl_resource_limits_default(vl_resource_limits* l) {
     l->recovery_samples = 3;
 }
 
+int vl_vram_hard_limit(uint64_t total_vram_bytes, uint64_t free_vram_bytes, uint64_t* limit) {
+    if (!limit) return fail(VL_INVALID_ARGUMENT, "limit is null");
+    constexpr uint64_t kGiB = 1ull << 30;
+    uint64_t v = 0;
+    if (free_vram_bytes > kGiB) {
+        const uint64_t pct = (uint64_t)((long double)total_vram_bytes * (long double)0.80);
+        v = pct < free_vram_bytes - kGiB ? pct : free_vram_bytes - kGiB;
+    }
+    *limit = v;
+    return VL_OK;
+}
+
 int vl_governor_create(const vl_resource_limits* limits, vl_governor** out) {
     if (!limits || !out) return fail(VL_INVALID_ARGUMENT, "null argument");
     vl_governor* g = new (std::nothrow) vl_governor;

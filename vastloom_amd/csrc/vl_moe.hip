@@ -2087,27 +2087,45 @@ __global__ void __launch_bounds__(stream_threads<kMoeMaxTokens>()) k_moe_down_gr
 // out[t][r]: token t's expert rows added in its combine order (zero when the layer was refused).
 __global__ void __launch_bounds__(256) k_moe_combine(const MoeShape s, const MoeInputs in,
                                                      const MoeWorkspace w) {
-    constexpr uint32_t NT = kMoeMaxTokens;
+    constexpr uint32_t NT = kMoeMaxTokens, kMaxEnt = kMoeMaxTopK + 1u;
     const uint32_t H = s.width, K = s.top_k, nent = K + (s.has_shared ? 1u : 0u);
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    // Four consecutive columns per thread (the width is a multiple of 32). Every entry's source
+    // and row values are requested before the first is added; the sum keeps the combine order.
+    const uint64_t i = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4u;
     const MoeHeader* hdr = ws_ptr<const MoeHeader>(w, w.off_header);
     const uint32_t n_active = *gp(&hdr->n_active);
     bool bad = false;
     if (i < (uint64_t)s.tokens * H) {
         const uint32_t t = (uint32_t)(i / H), r = (uint32_t)(i - (uint64_t)t * H);
-        float acc = 0.0f;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (n_active) {
             const CombineEntry* ce = ws_ptr<const CombineEntry>(w, w.off_combine) + (uint64_t)t * (K + 1u);
             const float* yp = ws_ptr<const float>(w, w.off_ypart);
-            for (uint32_t k = 0; k < nent; ++k) {
-                const uint32_t src = *gp(&ce[k].src);
-                const float y = *gp(yp + ((uint64_t)(src >> 3) * NT + (src & 7u)) * H + r);
-                acc = (s.semantics == kSemQwen && k < K) ? __fadd_rn(acc, __fmul_rn(y, *gp(&ce[k].w)))
-                                                         : __fadd_rn(acc, y);
+            uint32_t src[kMaxEnt];
+            float wt[kMaxEnt];
+#pragma unroll
+            for (uint32_t k = 0; k < kMaxEnt; ++k) {
+                src[k] = k < nent ? *gp(&ce[k].src) : 0u;
+                wt[k] = k < nent ? *gp(&ce[k].w) : 0.0f;
+            }
+            float4 y[kMaxEnt];
+#pragma unroll
+            for (uint32_t k = 0; k < kMaxEnt; ++k)
+                if (k < nent) y[k] = ld_f4(yp + ((uint64_t)(src[k] >> 3) * NT + (src[k] & 7u)) * H + r);
+#pragma unroll
+            for (uint32_t k = 0; k < kMaxEnt; ++k) {
+                if (k >= nent) continue;
+                const float v[4] = {y[k].x, y[k].y, y[k].z, y[k].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    acc[c] = (s.semantics == kSemQwen && k < K) ? __fadd_rn(acc[c], __fmul_rn(v[c], wt[k]))
+                                                                : __fadd_rn(acc[c], v[c]);
             }
         }
-        bad = !isfinite(acc);
-        *gp(in.out + i) = acc;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bad |= !isfinite(acc[c]);
+        const f32x4 o = {acc[0], acc[1], acc[2], acc[3]};
+        *gp(reinterpret_cast<f32x4*>(in.out + i)) = o;
     }
     if (__any(bad) && (threadIdx.x & 63u) == 0)
         or_bits(&ws_ptr<MoeHeader>(w, w.off_header)->status, kStatusNonFiniteOutput);
@@ -2239,7 +2257,7 @@ static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, con
     }
     if (e != hipSuccess) return e;
     const uint64_t outs = (uint64_t)s.tokens * s.width;
-    hipLaunchKernelGGL(k_moe_combine, dim3((uint32_t)((outs + 255u) / 256u)), dim3(256), 0, st, s, in, w);
+    hipLaunchKernelGGL(k_moe_combine, dim3((uint32_t)((outs / 4u + 255u) / 256u)), dim3(256), 0, st, s, in, w);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     mark(kStageCount);
     return hipSuccess;

@@ -649,81 +649,135 @@ __device__ __forceinline__ void build_active(const MoeShape& s, const MoeWorkspa
                                             CombineEntry* comb_lds = nullptr) {
     const uint32_t K = s.top_k, E = s.experts, P = s.tokens * K;
     const uint32_t p = threadIdx.x;
-    // The loops below read LDS words whose loads are independent; unrolling lets several be in
-    // flight at once instead of one latency per word.
-    if (p < P) {
-        uint32_t first = 1;
-        const uint32_t ep = rt.idx[p];
-#pragma unroll 8
-        for (uint32_t q = 0; q < p; ++q) first &= rt.idx[q] != ep ? 1u : 0u;
-        rt.first[p] = first;
-    }
-    __syncthreads();
-    bool bad = false;
-#pragma unroll 8
-    for (uint32_t t = 0; t < s.tokens; ++t) bad |= rt.bad[t] != 0;
     CombineEntry* comb = ws_ptr<CombineEntry>(w, w.off_combine);
-    if (p < P) {
-        const uint32_t e = rt.idx[p], t = p / K, k = p % K;
-        const float wt = rt.wt[p];
-        if (publish) {
-            *gp(ws_ptr<uint32_t>(w, w.off_route_idx) + p) = e;
-            *gp(ws_ptr<float>(w, w.off_route_w) + p) = wt;
-        }
-        uint32_t a = 0, slot = 0, ntok = 0, pos = 0;
+    if (s.tokens == 1 && rt.bad[0] == 0) {
+        // One routed token: its K experts are distinct, so expert p's active index and combine
+        // position are its rank by id, with one token in slot 0 (what the general pass below
+        // computes for this case, without its first-occurrence pass and barrier).
+        if (p < K) {
+            const uint32_t e = rt.idx[p];
+            const float wt = rt.wt[p];
+            if (publish) {
+                *gp(ws_ptr<uint32_t>(w, w.off_route_idx) + p) = e;
+                *gp(ws_ptr<float>(w, w.off_route_w) + p) = wt;
+            }
+            uint32_t a = 0;
 #pragma unroll 8
-        for (uint32_t q = 0; q < P; ++q) {
-            const uint32_t eq = rt.idx[q];
-            a += (rt.first[q] && eq < e) ? 1u : 0u;
-            ntok += eq == e ? 1u : 0u;
-            slot += (eq == e && q < p) ? 1u : 0u;
-        }
-#pragma unroll 8
-        for (uint32_t j = 0; j < K; ++j) pos += rt.idx[t * K + j] < e ? 1u : 0u;
-        rt.act[a].tok[slot] = t;
-        rt.act[a].route_w[slot] = wt;
-        if (slot == 0) {
+            for (uint32_t q = 0; q < K; ++q) a += rt.idx[q] < e ? 1u : 0u;
+            rt.act[a].tok[0] = 0;
+            rt.act[a].route_w[0] = wt;
             rt.act[a].expert = e;
-            rt.act[a].ntok = ntok;
+            rt.act[a].ntok = 1;
             rt.act[a].apply_w = s.semantics == kSemDeepseek ? 1u : 0u;
             rt.act[a].limit = s.routed_limit;
+            const uint32_t at = s.semantics == kSemDeepseek ? a : p;
+            const CombineEntry entry{a << 3, s.semantics == kSemQwen ? wt : 1.0f};
+            if (publish) {
+                uint32_t* ce = reinterpret_cast<uint32_t*>(comb + at);
+                *gp(ce) = entry.src;
+                *gp(ce + 1) = __float_as_uint(entry.w);
+            }
+            if (comb_lds) comb_lds[at] = entry;
         }
-        const uint32_t at = s.semantics == kSemDeepseek ? pos : k;
-        const CombineEntry entry{(a << 3) | slot, s.semantics == kSemQwen ? wt : 1.0f};
-        if (publish) {
-            uint32_t* ce = reinterpret_cast<uint32_t*>(comb + t * (K + 1) + at);
-            *gp(ce) = entry.src;
-            *gp(ce + 1) = __float_as_uint(entry.w);
-        }
-        if (comb_lds) comb_lds[t * (K + 1) + at] = entry;
-    }
-    if (threadIdx.x == 0) {
-        uint32_t n_routed = 0;
-#pragma unroll 8
-        for (uint32_t q = 0; q < P; ++q) n_routed += rt.first[q];
-        if (s.has_shared) {
-            ActiveExpert& sh = rt.act[n_routed];
-            sh.expert = E;
-            sh.ntok = s.tokens;
-            sh.apply_w = 0;
-            sh.limit = s.shared_limit;
-            for (uint32_t t = 0; t < s.tokens; ++t) {
-                sh.tok[t] = t;
-                sh.route_w[t] = 1.0f;
+        if (threadIdx.x == 0) {
+            if (s.has_shared) {
+                ActiveExpert& sh = rt.act[K];
+                sh.expert = E;
+                sh.ntok = 1;
+                sh.apply_w = 0;
+                sh.limit = s.shared_limit;
+                sh.tok[0] = 0;
+                sh.route_w[0] = 1.0f;
                 if (publish) {
-                    uint32_t* ce = reinterpret_cast<uint32_t*>(comb + t * (K + 1) + K);
-                    *gp(ce) = (n_routed << 3) | t;
+                    uint32_t* ce = reinterpret_cast<uint32_t*>(comb + K);
+                    *gp(ce) = K << 3;
                     *gp(ce + 1) = __float_as_uint(1.0f);
                 }
-                if (comb_lds) comb_lds[t * (K + 1) + K] = CombineEntry{(n_routed << 3) | t, 1.0f};
+                if (comb_lds) comb_lds[K] = CombineEntry{K << 3, 1.0f};
+            }
+            rt.n_active = K + (s.has_shared ? 1u : 0u);
+            if (publish) {
+                MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
+                *gp(&hdr->n_active) = rt.n_active;
+                if (x_nonfinite) or_bits(&hdr->status, kStatusNonFiniteInput);
             }
         }
-        rt.n_active = bad ? 0u : n_routed + (s.has_shared ? 1u : 0u);
-        if (publish) {
-            MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
-            *gp(&hdr->n_active) = rt.n_active;
-            const uint32_t bits = (bad ? kStatusBadRoute : 0u) | (x_nonfinite ? kStatusNonFiniteInput : 0u);
-            if (bits) or_bits(&hdr->status, bits);
+    } else {
+        // The loops below read LDS words whose loads are independent; unrolling lets several be in
+        // flight at once instead of one latency per word.
+        if (p < P) {
+            uint32_t first = 1;
+            const uint32_t ep = rt.idx[p];
+#pragma unroll 8
+            for (uint32_t q = 0; q < p; ++q) first &= rt.idx[q] != ep ? 1u : 0u;
+            rt.first[p] = first;
+        }
+        __syncthreads();
+        bool bad = false;
+#pragma unroll 8
+        for (uint32_t t = 0; t < s.tokens; ++t) bad |= rt.bad[t] != 0;
+        if (p < P) {
+            const uint32_t e = rt.idx[p], t = p / K, k = p % K;
+            const float wt = rt.wt[p];
+            if (publish) {
+                *gp(ws_ptr<uint32_t>(w, w.off_route_idx) + p) = e;
+                *gp(ws_ptr<float>(w, w.off_route_w) + p) = wt;
+            }
+            uint32_t a = 0, slot = 0, ntok = 0, pos = 0;
+#pragma unroll 8
+            for (uint32_t q = 0; q < P; ++q) {
+                const uint32_t eq = rt.idx[q];
+                a += (rt.first[q] && eq < e) ? 1u : 0u;
+                ntok += eq == e ? 1u : 0u;
+                slot += (eq == e && q < p) ? 1u : 0u;
+            }
+#pragma unroll 8
+            for (uint32_t j = 0; j < K; ++j) pos += rt.idx[t * K + j] < e ? 1u : 0u;
+            rt.act[a].tok[slot] = t;
+            rt.act[a].route_w[slot] = wt;
+            if (slot == 0) {
+                rt.act[a].expert = e;
+                rt.act[a].ntok = ntok;
+                rt.act[a].apply_w = s.semantics == kSemDeepseek ? 1u : 0u;
+                rt.act[a].limit = s.routed_limit;
+            }
+            const uint32_t at = s.semantics == kSemDeepseek ? pos : k;
+            const CombineEntry entry{(a << 3) | slot, s.semantics == kSemQwen ? wt : 1.0f};
+            if (publish) {
+                uint32_t* ce = reinterpret_cast<uint32_t*>(comb + t * (K + 1) + at);
+                *gp(ce) = entry.src;
+                *gp(ce + 1) = __float_as_uint(entry.w);
+            }
+            if (comb_lds) comb_lds[t * (K + 1) + at] = entry;
+        }
+        if (threadIdx.x == 0) {
+            uint32_t n_routed = 0;
+#pragma unroll 8
+            for (uint32_t q = 0; q < P; ++q) n_routed += rt.first[q];
+            if (s.has_shared) {
+                ActiveExpert& sh = rt.act[n_routed];
+                sh.expert = E;
+                sh.ntok = s.tokens;
+                sh.apply_w = 0;
+                sh.limit = s.shared_limit;
+                for (uint32_t t = 0; t < s.tokens; ++t) {
+                    sh.tok[t] = t;
+                    sh.route_w[t] = 1.0f;
+                    if (publish) {
+                        uint32_t* ce = reinterpret_cast<uint32_t*>(comb + t * (K + 1) + K);
+                        *gp(ce) = (n_routed << 3) | t;
+                        *gp(ce + 1) = __float_as_uint(1.0f);
+                    }
+                    if (comb_lds) comb_lds[t * (K + 1) + K] = CombineEntry{(n_routed << 3) | t, 1.0f};
+                }
+            }
+            rt.n_active = bad ? 0u : n_routed + (s.has_shared ? 1u : 0u);
+            if (publish) {
+                MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
+                *gp(&hdr->n_active) = rt.n_active;
+                const uint32_t bits = (bad ? kStatusBadRoute : 0u) | (x_nonfinite ? kStatusNonFiniteInput : 0u);
+                if (bits) or_bits(&hdr->status, bits);
+            }
         }
     }
     __syncthreads();

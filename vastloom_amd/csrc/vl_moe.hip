@@ -382,9 +382,10 @@ __global__ void __launch_bounds__(256) k_moe_logits_finish(const MoeShape s, con
     router_logit_store(s, in, w, (uint32_t)(i % s.experts), (uint32_t)(i / s.experts), sum);
 }
 
-// Block (b, g): expert row b's logits for the tokens of group g (tokens 8g .. 8g + 7), then the
-// limbs of column block b of the group's tokens. Block (0, 0) zeroes the status word; all blocks
-// together zero the handoff counters.
+// Blocks b < R (R = experts, or 0 for caller-given routes): expert row b's logits for the tokens
+// of group g (tokens 8g .. 8g + 7). Blocks R + c: the limbs of column block c of the group's
+// tokens, in blocks of their own so that no routing block waits for them. Block (0, 0) zeroes the
+// status word; all blocks together zero the handoff counters.
 __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeInputs in,
                                                     const MoeWorkspace w) {
     __shared__ double red[kMoeMaxTokens][4];
@@ -394,7 +395,8 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
     // The row's weights are requested first; zeroing and the activation limbs overlap their
     // latency.
     RouterRow rr;
-    const bool routes = s.routing != kRouteGiven && b < s.experts;
+    const uint32_t R = s.routing != kRouteGiven ? s.experts : 0u;
+    const bool routes = b < R;
     if (routes) router_row_load(s, in, b, t0, rr);
     if (b == 0 && blockIdx.y == 0 && threadIdx.x < 2) {
         MoeHeader* h = ws_ptr<MoeHeader>(w, w.off_header);
@@ -405,11 +407,13 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
         const uint32_t nb = gridDim.x * gridDim.y, lb = blockIdx.y * gridDim.x + b;
         for (uint32_t i = lb * blockDim.x + threadIdx.x; i < w.counters; i += nb * blockDim.x) cnt[i] = 0;
     }
-    if (b < w.xblocks)
-        prep_x_block(in.x, s.width, s.width, t0, t1, w.xslots, w.estride, b,
-                     ws_ptr<int8_t>(w, w.off_xlimbs), ws_ptr<int>(w, w.off_xexp),
-                     ws_ptr<uint32_t>(w, w.off_xflags));
-    if (!routes) return;
+    if (!routes) {
+        if (b - R < w.xblocks)
+            prep_x_block(in.x, s.width, s.width, t0, t1, w.xslots, w.estride, b - R,
+                         ws_ptr<int8_t>(w, w.off_xlimbs), ws_ptr<int>(w, w.off_xexp),
+                         ws_ptr<uint32_t>(w, w.off_xflags));
+        return;
+    }
     router_row_partials(s, in, b, t0, t1, red, rr);
     __syncthreads();
     if (threadIdx.x < t1 - t0) router_logit_finish(s, in, w, b, t0 + threadIdx.x, red[threadIdx.x]);
@@ -2390,9 +2394,8 @@ hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace
     auto mark = [&](uint32_t stage) {
         if (ev) (void)hipEventRecord(ev[stage], st);
     };
-    const uint32_t router_blocks = s.routing == kRouteGiven ? 1u : s.experts;
-    hipLaunchKernelGGL(k_moe_router, dim3(router_blocks > w.xblocks ? router_blocks : w.xblocks),
-                       dim3(256), 0, st, s, in, w);
+    const uint32_t router_blocks = (s.routing == kRouteGiven ? 0u : s.experts) + w.xblocks;
+    hipLaunchKernelGGL(k_moe_router, dim3(router_blocks), dim3(256), 0, st, s, in, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     mark(kStageGateUp);

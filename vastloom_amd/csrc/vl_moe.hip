@@ -498,6 +498,7 @@ __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* ke
                 key[j - 1] = tk_;
                 hid[j - 1] = ti;
             }
+    double sel = 0.0;  // the taken values, added in rank order
     for (uint32_t k = 0; k < K; ++k) {
         const uint32_t m = wave_max_u32(key[0]);
         const bool top = key[0] == m && m != 0;
@@ -521,6 +522,7 @@ __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* ke
                 sc = sv[i];
             }
         const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(softmax ? l : sc), id & 63u));
+        sel += (double)v;
         if (lane == 0) {
             tk.id[k] = id;
             tk.val[k] = v;
@@ -534,8 +536,19 @@ __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* ke
             key[PER - 1] = 0;
         }
     }
+    if (!softmax) {
+        // Weights are the taken scores over their sum (sel, added in rank order as taken).
+        __builtin_amdgcn_wave_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (lane < K) {
+            bad |= !(sel > 0.0) || isinf(sel);
+            out_idx[lane] = tk.id[lane];
+            out_w[lane] = (float)((double)tk.val[lane] / sel * (double)s.route_scale);
+        }
+        return __any(bad);
+    }
     double sum_all = 0.0, mx = 0.0;
-    if (softmax) {
+    {
         // The largest key is the largest logit: the first selected expert's.
         mx = (double)__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(tk.val[0])));
 #pragma unroll
@@ -549,7 +562,7 @@ __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* ke
     float vk = 0.0f;
     if (lane < K) {
         vk = tk.val[lane];
-        pk = softmax ? exp((double)vk - mx) * (sum_all > 0.0 ? 1.0 / sum_all : 0.0) : (double)vk;
+        pk = exp((double)vk - mx) * (sum_all > 0.0 ? 1.0 / sum_all : 0.0);
         tk.p[lane] = pk;
     }
     __builtin_amdgcn_wave_barrier();
@@ -558,14 +571,8 @@ __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* ke
         double sel_sum = 0.0;
 #pragma unroll 8
         for (uint32_t q = 0; q < K; ++q) sel_sum += tk.p[q];
-        float wk;
-        if (!softmax) {
-            bad |= !(sel_sum > 0.0) || isinf(sel_sum);
-            wk = (float)((double)vk / sel_sum * (double)s.route_scale);
-        } else {
-            wk = (float)pk;
-            if (s.renormalize && sel_sum > 0.0) wk = (float)((double)wk * (1.0 / sel_sum));
-        }
+        float wk = (float)pk;
+        if (s.renormalize && sel_sum > 0.0) wk = (float)((double)wk * (1.0 / sel_sum));
         out_idx[lane] = tk.id[lane];
         out_w[lane] = wk;
     }

@@ -253,7 +253,8 @@ def test_workload_deepseek_layers(ops, lib, oracle, name):
 
 @pytest.mark.parametrize("routing_name,tokens,gt,dt", [
     ("learned", 9, IQ2_XXS, IQ2_XXS), ("table", 37, IQ2_XXS, IQ2_XXS),
-    ("softmax", 100, Q8_0, Q8_0), ("learned", 64, IQ1_S, IQ3_XXS)])
+    ("softmax", 100, Q8_0, Q8_0), ("learned", 64, IQ1_S, IQ3_XXS),
+    ("learned", 1024, IQ2_XXS, IQ2_XXS)])
 def test_grouped_layers(ops, lib, oracle, routing_name, tokens, gt, dt):
     print(f"[moe grouped] {routing_name} tokens={tokens} types={gt},{dt}", flush=True)
     rng = np.random.default_rng(tokens)

@@ -1794,13 +1794,28 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_plan(const MoeShape s, c
         cnt[e] = run;
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t acc = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            base[e] = acc;
-            acc += (cnt[e] + kMoeMaxTokens - 1u) / kMoeMaxTokens;
+    static_assert(kStreamThreads >= 1024u, "one expert per thread: layers have at most 1024");
+    // Each expert's first group: an exclusive block scan of the group counts (one expert per
+    // thread; the layer has at most as many experts as the block has threads), in the waves by
+    // shuffles, then over the waves' totals.
+    {
+        const uint32_t g = tid < E ? (cnt[tid] + kMoeMaxTokens - 1u) / kMoeMaxTokens : 0u;
+        uint32_t inc = g;
+#pragma unroll
+        for (uint32_t d = 1; d < 64u; d <<= 1) {
+            const uint32_t v = (uint32_t)__shfl_up((int)inc, d);
+            if (lane >= d) inc += v;
         }
-        base[E] = acc;
+        if (lane == 63u) flags[wave] = inc;
+        __syncthreads();
+        uint32_t before = 0, all = 0;
+        for (uint32_t v = 0; v < nw; ++v) {
+            const uint32_t f = flags[v];
+            before += v < wave ? f : 0u;
+            all += f;
+        }
+        if (tid < E) base[tid] = before + inc - g;
+        if (tid == 0) base[E] = all;
     }
     __syncthreads();
     ActiveExpert* ent = ws_ptr<ActiveExpert>(w, w.off_active);

@@ -1779,9 +1779,13 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_plan(const MoeShape s, c
     const bool any_nonfinite = block_any(nonfinite, flags);
     // 1. Per-wave counts of each expert over the wave's tokens (a token's experts are distinct;
     //    the duplicates of a refused token can only lose increments, which keeps ranks in range).
+    //    Each assignment keeps its rank within the wave in the upper half of its id word.
     uint32_t* mine = hist + wave * E;
     for (uint32_t t = tw0; t < tw1; ++t)
-        for (uint32_t k = lane; k < K; k += 64u) ++mine[ids[t * K + k]];
+        for (uint32_t k = lane; k < K; k += 64u) {
+            const uint32_t e = ids[t * K + k];
+            ids[t * K + k] = e | (mine[e]++ << 16);
+        }
     __syncthreads();
     // 2. Per expert: the waves' counts become exclusive offsets; the total is the expert's count.
     for (uint32_t e = tid; e < E; e += nth) {
@@ -1822,33 +1826,34 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_plan(const MoeShape s, c
     MoeExpert* gw = ws_ptr<MoeExpert>(w, w.off_gweights);
     CombineEntry* comb = ws_ptr<CombineEntry>(w, w.off_combine);
     const bool deepseek = s.semantics == kSemDeepseek, qwen = s.semantics == kSemQwen;
-    // 3. Each wave walks its tokens in order again: an expert's ranks ascend with the tokens.
-    for (uint32_t t = tw0; t < tw1; ++t) {
-        for (uint32_t k = lane; k < K; k += 64u) {
-            const uint32_t p = t * K + k, e = ids[p];
-            const uint32_t r = mine[e]++;
-            const uint32_t a = base[e] + r / kMoeMaxTokens, sl = r % kMoeMaxTokens;
-            ActiveExpert* A = ent + a;
-            const float wt = *gp(rwt + p);
-            *gp(&A->tok[sl]) = t;
-            *gp(&A->route_w[sl]) = wt;
-            if (sl == 0) {
-                const uint32_t n = cnt[e];
-                *gp(&A->expert) = e;
-                *gp(&A->ntok) = n - r < kMoeMaxTokens ? n - r : kMoeMaxTokens;
-                *gp(&A->apply_w) = deepseek ? 1u : 0u;
-                *gp(&A->limit) = s.routed_limit;
-                gw[a] = in.experts[e];
-            }
-            uint32_t at = k;
-            if (deepseek) {
-                at = 0;
-                for (uint32_t k2 = 0; k2 < K; ++k2) at += ids[t * K + k2] < e ? 1u : 0u;
-            }
-            uint32_t* ce = reinterpret_cast<uint32_t*>(comb + (uint64_t)t * (K + 1u) + at);
-            *gp(ce) = (a << 3) | sl;
-            *gp(ce + 1) = __float_as_uint(qwen ? wt : 1.0f);
+    // 3. Every assignment in parallel: its rank among the expert's assignments is its wave's
+    //    offset plus its rank within the wave, so an expert's ranks ascend with the tokens.
+    for (uint32_t p = tid; p < P; p += nth) {
+        const uint32_t t = p / K, k = p - t * K;
+        const uint32_t e = ids[p] & 0xffffu;
+        const uint32_t v = (uint32_t)((((uint64_t)t + 1u) * nw - 1u) / T);  // the wave holding t
+        const uint32_t r = hist[v * E + e] + (ids[p] >> 16);
+        const uint32_t a = base[e] + r / kMoeMaxTokens, sl = r % kMoeMaxTokens;
+        ActiveExpert* A = ent + a;
+        const float wt = *gp(rwt + p);
+        *gp(&A->tok[sl]) = t;
+        *gp(&A->route_w[sl]) = wt;
+        if (sl == 0) {
+            const uint32_t n = cnt[e];
+            *gp(&A->expert) = e;
+            *gp(&A->ntok) = n - r < kMoeMaxTokens ? n - r : kMoeMaxTokens;
+            *gp(&A->apply_w) = deepseek ? 1u : 0u;
+            *gp(&A->limit) = s.routed_limit;
+            gw[a] = in.experts[e];
         }
+        uint32_t at = k;
+        if (deepseek) {
+            at = 0;
+            for (uint32_t k2 = 0; k2 < K; ++k2) at += (ids[t * K + k2] & 0xffffu) < e ? 1u : 0u;
+        }
+        uint32_t* ce = reinterpret_cast<uint32_t*>(comb + (uint64_t)t * (K + 1u) + at);
+        *gp(ce) = (a << 3) | sl;
+        *gp(ce + 1) = __float_as_uint(qwen ? wt : 1.0f);
     }
     const uint32_t routed_groups = base[E];
     if (s.has_shared) {

@@ -262,14 +262,22 @@ def main() -> int:
             if bits:
                 raise RuntimeError(f"layer reported status bits {bits:#x}")
 
-    # Per-stage durations from HIP events on the same stream, in a separate profiled pass.
+    # Per-stage durations from HIP events on the same stream, in a separate profiled pass; then
+    # each stage's kernel alone, from events the launch records around its execution, in another.
     tl = ops.Timeline(args.profile_steps)
     for i in range(args.profile_steps):
         step(i, timeline=tl, call_slot=i)
     torch.cuda.synchronize()
     stages = [tl.stage_ms(i) for i in range(args.profile_steps)]
     tl.close()
+    tk = ops.Timeline(args.profile_steps, kernel_brackets=True)
+    for i in range(args.profile_steps):
+        step(i, timeline=tk, call_slot=i)
+    torch.cuda.synchronize()
+    kernels = [tk.kernel_ms(i) for i in range(args.profile_steps)]
+    tk.close()
     stage_us = {k: round(1000.0 * float(np.mean([s[k] for s in stages])), 2) for k in stages[0]}
+    kernel_us = {k: round(1000.0 * float(np.mean([s[k] for s in kernels])), 2) for k in kernels[0]}
 
     measured = None
     if wl.tokens > 1 and wl.routing not in ("zipf_table", "single"):
@@ -281,8 +289,9 @@ def main() -> int:
     H, F = wl.width, wl.intermediate
     from vastloom_amd.workloads import storage_bytes
     gateup_bytes = n_exp * 2 * storage_bytes(wl.gate_type, F, H)
-    gateup_gbs = gateup_bytes / (stage_us["gate_up"] * 1e-6) / 1e9
-    down_gbs = n_exp * storage_bytes(wl.down_type, H, F) / (stage_us["down"] * 1e-6) / 1e9
+    # The kernels' own durations (events around their execution), as a kernel trace reports them.
+    gateup_gbs = gateup_bytes / (kernel_us["gate_up"] * 1e-6) / 1e9
+    down_gbs = n_exp * storage_bytes(wl.down_type, H, F) / (kernel_us["down"] * 1e-6) / 1e9
     traffic, traffic_src = measured_traffic() if wl.name == "iq2_moe" else (None, None)
 
     result = {
@@ -313,13 +322,14 @@ def main() -> int:
                    "router_bytes_per_layer": wl.router_bytes(),
                    "layer_instances": args.layers, "token_pool": args.token_pool},
         "stages_us": stage_us,
+        "kernels_us": kernel_us,
         "roofline": {"bound": "hbm", "kernel": "k_moe_gateup" if wl.tokens <= 8 else "k_moe_gateup_grouped",
                      "achieved": round(gateup_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gateup_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
                      "bytes_per_launch": gateup_bytes,
-                     "kernel_avg_us": stage_us["gate_up"],
+                     "kernel_avg_us": kernel_us["gate_up"],
                      "down_kernel_achieved": round(down_gbs, 1)},
         "cpu_baseline": None,
     }

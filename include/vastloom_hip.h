@@ -241,6 +241,17 @@ int vl_moe_layer_profiled(const vl_moe_config* config, const vl_moe_inputs* inpu
 /* Milliseconds of each stage of a recorded call (the events must have completed). */
 int vl_timeline_stage_ms(vl_timeline* timeline, uint32_t call, float* ms /* [VL_STAGE_COUNT] */);
 
+/* With enabled, later profiled calls record, instead of stage marks, events that the launch
+ * places around each stage's kernel execution (such launches lengthen the gaps between kernels,
+ * so the two are recorded in separate calls). */
+int vl_timeline_set_kernel_brackets(vl_timeline* timeline, int enabled);
+
+/* Milliseconds of each stage's kernel of a call recorded with kernel brackets: the kernel's own
+ * execution, without the gaps between launches. Stages of several kernels (layers of more than 8
+ * tokens) and single-launch layers report their stage time. Like the stage times, this replaces
+ * the steady-clock kernel_ms of cuda_matvec_accelerator.cpp:258-311. */
+int vl_timeline_kernel_ms(vl_timeline* timeline, uint32_t call, float* ms /* [VL_STAGE_COUNT] */);
+
 /* ---- Safety Governor ------------------------------------------------------------------------
  * A native counterpart of safety::ResourceGovernor (src/safety/resource_governor.cpp:19-214,
  * include/vastloom/safety/resource_governor.hpp:15-117): per-kind hard budgets, an optional

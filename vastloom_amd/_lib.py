@@ -59,6 +59,8 @@ _SIGNATURES = {
     "vl_timeline_destroy": [_P],
     "vl_moe_layer_profiled": [_P, _P, _P, _U64, _P, _P, _U32],
     "vl_timeline_stage_ms": [_P, _U32, C.POINTER(C.c_float)],
+    "vl_timeline_kernel_ms": [_P, _U32, C.POINTER(C.c_float)],
+    "vl_timeline_set_kernel_brackets": [_P, C.c_int],
     "vl_resource_limits_default": [_P],
     "vl_governor_create": [_P, C.POINTER(C.c_void_p)],
     "vl_governor_destroy": [_P],

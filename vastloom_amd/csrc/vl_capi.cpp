@@ -212,7 +212,10 @@ int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void*
 
 struct vl_timeline {
     uint32_t calls = 0;
-    std::vector<hipEvent_t> events;  // calls x (stages + 1)
+    bool brackets = false;                // record kernel brackets instead of stage marks
+    std::vector<hipEvent_t> events;       // calls x (stages + 1): marks between the stages
+    std::vector<hipEvent_t> kernels;      // calls x 2 stages: start and stop of each stage's kernel
+    std::vector<uint8_t> bracketed;       // per call: kernels recorded
 };
 
 extern "C" {
@@ -223,22 +226,32 @@ int vl_timeline_create(uint32_t calls, vl_timeline** out) {
     if (!t) return fail(VL_RESOURCE_EXHAUSTED, "timeline allocation failed");
     t->calls = calls;
     t->events.assign((size_t)calls * (vl::kStageCount + 1), nullptr);
-    for (auto& e : t->events) {
-        const hipError_t r = hipEventCreate(&e);
-        if (r != hipSuccess) {
-            vl_timeline_destroy(t);
-            return hip_fail(r, "hipEventCreate");
+    t->kernels.assign((size_t)calls * 2u * vl::kStageCount, nullptr);
+    t->bracketed.assign(calls, 0);
+    for (auto* v : {&t->events, &t->kernels})
+        for (auto& e : *v) {
+            const hipError_t r = hipEventCreate(&e);
+            if (r != hipSuccess) {
+                vl_timeline_destroy(t);
+                return hip_fail(r, "hipEventCreate");
+            }
         }
-    }
     *out = t;
     return VL_OK;
 }
 
 void vl_timeline_destroy(vl_timeline* t) {
     if (!t) return;
-    for (auto e : t->events)
-        if (e) (void)hipEventDestroy(e);
+    for (auto* v : {&t->events, &t->kernels})
+        for (auto e : *v)
+            if (e) (void)hipEventDestroy(e);
     delete t;
+}
+
+int vl_timeline_set_kernel_brackets(vl_timeline* t, int enabled) {
+    if (!t) return fail(VL_INVALID_ARGUMENT, "timeline is null");
+    t->brackets = enabled != 0;
+    return VL_OK;
 }
 
 int vl_moe_layer_profiled(const vl_moe_config* config, const vl_moe_inputs* inputs,
@@ -257,15 +270,31 @@ int vl_moe_layer_profiled(const vl_moe_config* config, const vl_moe_inputs* inpu
                            inputs->router, inputs->bias, inputs->table_ids, inputs->given_ids,
                            inputs->given_weights, inputs->x, inputs->out};
     hipEvent_t* ev = timeline->events.data() + (size_t)call * (vl::kStageCount + 1);
-    const hipError_t e = vl::launch_moe(s, in, ws, static_cast<hipStream_t>(stream), ev);
+    hipEvent_t* kev = timeline->kernels.data() + (size_t)call * 2u * vl::kStageCount;
+    timeline->bracketed[call] = timeline->brackets ? 1 : 0;
+    const hipError_t e = vl::launch_moe(s, in, ws, static_cast<hipStream_t>(stream),
+                                        timeline->brackets ? nullptr : ev,
+                                        timeline->brackets ? kev : nullptr);
     return e == hipSuccess ? VL_OK : hip_fail(e, "MoE launch");
 }
 
 int vl_timeline_stage_ms(vl_timeline* t, uint32_t call, float* ms) {
     if (!t || call >= t->calls || !ms) return fail(VL_INVALID_ARGUMENT, "bad timeline read");
+    if (t->bracketed[call]) return fail(VL_INVALID_ARGUMENT, "call %u recorded kernel brackets", call);
     hipEvent_t* ev = t->events.data() + (size_t)call * (vl::kStageCount + 1);
     for (uint32_t i = 0; i < vl::kStageCount; ++i) {
         const hipError_t r = hipEventElapsedTime(&ms[i], ev[i], ev[i + 1]);
+        if (r != hipSuccess) return hip_fail(r, "hipEventElapsedTime");
+    }
+    return VL_OK;
+}
+
+int vl_timeline_kernel_ms(vl_timeline* t, uint32_t call, float* ms) {
+    if (!t || call >= t->calls || !ms) return fail(VL_INVALID_ARGUMENT, "bad timeline read");
+    if (!t->bracketed[call]) return fail(VL_INVALID_ARGUMENT, "call %u recorded stage marks", call);
+    hipEvent_t* ev = t->kernels.data() + (size_t)call * 2u * vl::kStageCount;
+    for (uint32_t i = 0; i < vl::kStageCount; ++i) {
+        const hipError_t r = hipEventElapsedTime(&ms[i], ev[2 * i], ev[2 * i + 1]);
         if (r != hipSuccess) return hip_fail(r, "hipEventElapsedTime");
     }
     return VL_OK;

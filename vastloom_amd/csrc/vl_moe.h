@@ -94,10 +94,14 @@ enum MoeStage : uint32_t { kStageRouter = 0, kStageGateUp, kStageDown, kStageCou
 // Whether single-launch layers may be used where they apply (process-wide; default on).
 void set_moe_fused(bool enabled);
 
-// Issues the whole layer on the stream. When events is non-null it holds kStageCount + 1
-// events recorded around the stages.
+// Issues the whole layer on the stream. When events is non-null it holds kStageCount + 1 events
+// recorded between the stages; when kernel_events is non-null, a start and a stop event per stage
+// that bracket the stage's kernel itself (recorded by the launch; stages of several kernels and
+// single-launch layers record them at the stage boundaries). Bracketed launches lengthen the gaps
+// between kernels, so the two are meant for separate calls.
 hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& ws,
-                      hipStream_t stream, hipEvent_t* events = nullptr);
+                      hipStream_t stream, hipEvent_t* events = nullptr,
+                      hipEvent_t* kernel_events = nullptr);
 
 }  // namespace vl
 

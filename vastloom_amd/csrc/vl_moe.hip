@@ -16,6 +16,7 @@
 //
 // The routing, clamp, route-weight placement and combine order follow the reference code named
 // in vl_moe.h. Every reduction has a fixed order, so results are deterministic.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -2227,56 +2228,74 @@ __global__ void __launch_bounds__(256) k_moe_combine(const MoeShape s, const Moe
 // LDS of one workgroup on gfx950; the stream kernels keep all their LDS in the dynamic part.
 constexpr uint32_t kLdsBudget = 160u * 1024u;
 
+// Events that the launch records around one kernel's execution (profiled layers), or none.
+struct KernelEvents {
+    hipEvent_t start, stop;
+};
+
+template <typename K, typename... Args>
+static hipError_t launch_timed(const KernelEvents* ke, K kernel, dim3 grid, dim3 block, uint32_t shm,
+                               hipStream_t st, Args... args) {
+    if (ke) hipExtLaunchKernelGGL(kernel, grid, block, shm, st, ke->start, ke->stop, 0u, args...);
+    else hipLaunchKernelGGL(kernel, grid, block, shm, st, args...);
+    return hipGetLastError();
+}
+
+template <typename K, typename... Args>
+static hipError_t launch_stream_ev(const KernelEvents* ke, K kernel, uint32_t blocks, uint32_t threads,
+                                   uint32_t shm, hipStream_t st, Args... args) {
+    const hipError_t e = ensure_dynamic_lds((const void*)kernel, shm);
+    if (e != hipSuccess) return e;
+    return launch_timed(ke, kernel, dim3(blocks), dim3(threads), shm, st, args...);
+}
+
 template <typename K, typename... Args>
 static hipError_t launch_stream(K kernel, uint32_t blocks, uint32_t threads, uint32_t shm,
                                 hipStream_t st, Args... args) {
-    const hipError_t e = ensure_dynamic_lds((const void*)kernel, shm);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(threads), shm, st, args...);
-    return hipGetLastError();
+    return launch_stream_ev(static_cast<const KernelEvents*>(nullptr), kernel, blocks, threads, shm, st, args...);
 }
 
 template <uint32_t FMT, int NT>
 static hipError_t launch_gateup_nt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
-                                   hipStream_t st) {
+                                   hipStream_t st, const KernelEvents* ke) {
     const uint32_t stage = (s.width / 32u) * NT * 128u;
     const GateUpLds staged = gateup_lds(table_bytes<FMT>(), stage, w.xblocks);
     if (staged.bytes <= kLdsBudget)
-        return launch_stream(k_moe_gateup<FMT, NT, true>, w.blocks, stream_threads<NT>(), staged.bytes, st, s, in, w);
+        return launch_stream_ev(ke, k_moe_gateup<FMT, NT, true>, w.blocks, stream_threads<NT>(), staged.bytes, st, s, in, w);
     const GateUpLds plain = gateup_lds(table_bytes<FMT>(), 0u, w.xblocks);
-    return launch_stream(k_moe_gateup<FMT, NT, false>, w.blocks, stream_threads<NT>(), plain.bytes, st, s, in, w);
+    return launch_stream_ev(ke, k_moe_gateup<FMT, NT, false>, w.blocks, stream_threads<NT>(), plain.bytes, st, s, in, w);
 }
 
 template <uint32_t FMT>
 static hipError_t launch_gateup_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
-                                    hipStream_t st) {
+                                    hipStream_t st, const KernelEvents* ke = nullptr) {
     switch (w.slots) {
-        case 1: return launch_gateup_nt<FMT, 1>(s, in, w, st);
-        case 2: return launch_gateup_nt<FMT, 2>(s, in, w, st);
-        case 4: return launch_gateup_nt<FMT, 4>(s, in, w, st);
-        default: return launch_gateup_nt<FMT, 8>(s, in, w, st);
+        case 1: return launch_gateup_nt<FMT, 1>(s, in, w, st, ke);
+        case 2: return launch_gateup_nt<FMT, 2>(s, in, w, st, ke);
+        case 4: return launch_gateup_nt<FMT, 4>(s, in, w, st, ke);
+        default: return launch_gateup_nt<FMT, 8>(s, in, w, st, ke);
     }
 }
 
 template <uint32_t FMT, int NT>
 static hipError_t launch_down_nt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
-                                 hipStream_t st) {
+                                 hipStream_t st, const KernelEvents* ke) {
     const DownLds staged = down_lds(table_bytes<FMT>(), w.stage * down_expert_bytes(s.inter, NT),
                                     w.stage, w.hblocks);
     if (staged.bytes <= kLdsBudget)
-        return launch_stream(k_moe_down<FMT, NT, true>, w.blocks, stream_threads<NT>(), staged.bytes, st, s, in, w);
+        return launch_stream_ev(ke, k_moe_down<FMT, NT, true>, w.blocks, stream_threads<NT>(), staged.bytes, st, s, in, w);
     const DownLds plain = down_lds(table_bytes<FMT>(), 0u, w.stage, w.hblocks);
-    return launch_stream(k_moe_down<FMT, NT, false>, w.blocks, stream_threads<NT>(), plain.bytes, st, s, in, w);
+    return launch_stream_ev(ke, k_moe_down<FMT, NT, false>, w.blocks, stream_threads<NT>(), plain.bytes, st, s, in, w);
 }
 
 template <uint32_t FMT>
 static hipError_t launch_down_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
-                                  hipStream_t st) {
+                                  hipStream_t st, const KernelEvents* ke = nullptr) {
     switch (w.slots) {
-        case 1: return launch_down_nt<FMT, 1>(s, in, w, st);
-        case 2: return launch_down_nt<FMT, 2>(s, in, w, st);
-        case 4: return launch_down_nt<FMT, 4>(s, in, w, st);
-        default: return launch_down_nt<FMT, 8>(s, in, w, st);
+        case 1: return launch_down_nt<FMT, 1>(s, in, w, st, ke);
+        case 2: return launch_down_nt<FMT, 2>(s, in, w, st, ke);
+        case 4: return launch_down_nt<FMT, 4>(s, in, w, st, ke);
+        default: return launch_down_nt<FMT, 8>(s, in, w, st, ke);
     }
 }
 
@@ -2298,9 +2317,12 @@ static hipError_t launch_down_grouped(const MoeShape& s, const MoeInputs& in, co
 
 // Routing, planning, gate/up, down and combine of the grouped path.
 static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
-                                     hipStream_t st, hipEvent_t* ev) {
+                                     hipStream_t st, hipEvent_t* ev, hipEvent_t* kev) {
+    // Stages of several kernels: each stage's kernel bracket is recorded at its boundaries.
     auto mark = [&](uint32_t stage) {
+        if (kev && stage > 0) (void)hipEventRecord(kev[2u * stage - 1u], st);  // previous stop
         if (ev) (void)hipEventRecord(ev[stage], st);
+        if (kev && stage < kStageCount) (void)hipEventRecord(kev[2u * stage], st);  // start
     };
     mark(kStageRouter);
     // The router kernel zeroes the counters and forms the activation limbs; the logits come
@@ -2392,9 +2414,13 @@ static hipError_t launch_fused_fmt(const MoeShape& s, const MoeInputs& in, const
     }
 }
 
+static bool fused_applies(const MoeShape& s, const MoeWorkspace& w) {
+    return g_fused_enabled && !w.grouped && s.gate_type == s.down_type;
+}
+
 static hipError_t launch_fused(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
                                hipStream_t st) {
-    if (!g_fused_enabled || w.grouped || s.gate_type != s.down_type) return hipErrorNotSupported;
+    if (!fused_applies(s, w)) return hipErrorNotSupported;
     switch (s.gate_type) {
         case VL_TYPE_IQ2_XXS: return launch_fused_fmt<VL_TYPE_IQ2_XXS>(s, in, w, st);
         case VL_TYPE_IQ3_XXS: return launch_fused_fmt<VL_TYPE_IQ3_XXS>(s, in, w, st);
@@ -2405,45 +2431,60 @@ static hipError_t launch_fused(const MoeShape& s, const MoeInputs& in, const Moe
 }
 
 hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
-                      hipStream_t st, hipEvent_t* ev) {
+                      hipStream_t st, hipEvent_t* ev, hipEvent_t* kev) {
     if (!moe_shape_ok(s) || w.blocks == 0) return hipErrorInvalidValue;
-    if (w.grouped) return launch_moe_grouped(s, in, w, st, ev);
-    if (ev) {
-        (void)hipEventRecord(ev[kStageRouter], st);
-        (void)hipEventRecord(ev[kStageGateUp], st);
-    }
-    const hipError_t fe = launch_fused(s, in, w, st);
-    if (fe == hipSuccess) {
-        // One launch: its time is reported as the gate/up stage, the others as empty.
-        if (ev) {
-            (void)hipEventRecord(ev[kStageDown], st);
-            (void)hipEventRecord(ev[kStageCount], st);
-        }
-        return hipSuccess;
-    }
-    if (fe != hipErrorNotSupported) return fe;
+    if (w.grouped) return launch_moe_grouped(s, in, w, st, ev, kev);
+    // Stage kernel brackets: start and stop of each stage's kernel.
+    KernelEvents ke[kStageCount];
+    for (uint32_t i = 0; kev && i < kStageCount; ++i) ke[i] = KernelEvents{kev[2u * i], kev[2u * i + 1u]};
+    auto rec = [&](hipEvent_t e) { (void)hipEventRecord(e, st); };
     auto mark = [&](uint32_t stage) {
-        if (ev) (void)hipEventRecord(ev[stage], st);
+        if (ev) rec(ev[stage]);
     };
+    mark(kStageRouter);
+    if (fused_applies(s, w)) {
+        // One cooperative launch: its time is reported as the gate/up stage (and kernel), the
+        // others as empty.
+        if (kev) {
+            rec(ke[kStageRouter].start);
+            rec(ke[kStageRouter].stop);
+            rec(ke[kStageGateUp].start);
+        }
+        mark(kStageGateUp);
+        const hipError_t fe = launch_fused(s, in, w, st);
+        if (fe != hipSuccess && fe != hipErrorNotSupported) return fe;
+        if (fe == hipSuccess) {
+            if (kev) {
+                rec(ke[kStageGateUp].stop);
+                rec(ke[kStageDown].start);
+                rec(ke[kStageDown].stop);
+            }
+            mark(kStageDown);
+            mark(kStageCount);
+            return hipSuccess;
+        }
+    }
     const uint32_t router_blocks = (s.routing == kRouteGiven ? 0u : s.experts) + w.xblocks;
-    hipLaunchKernelGGL(k_moe_router, dim3(router_blocks), dim3(256), 0, st, s, in, w);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_timed(kev ? &ke[kStageRouter] : nullptr, k_moe_router, dim3(router_blocks),
+                                dim3(256), 0u, st, s, in, w);
     if (e != hipSuccess) return e;
     mark(kStageGateUp);
+    const KernelEvents* kg = kev ? &ke[kStageGateUp] : nullptr;
     switch (s.gate_type) {
-        case VL_TYPE_IQ2_XXS: e = launch_gateup_fmt<VL_TYPE_IQ2_XXS>(s, in, w, st); break;
-        case VL_TYPE_IQ3_XXS: e = launch_gateup_fmt<VL_TYPE_IQ3_XXS>(s, in, w, st); break;
-        case VL_TYPE_IQ1_S: e = launch_gateup_fmt<VL_TYPE_IQ1_S>(s, in, w, st); break;
-        case VL_TYPE_Q8_0: e = launch_gateup_fmt<VL_TYPE_Q8_0>(s, in, w, st); break;
+        case VL_TYPE_IQ2_XXS: e = launch_gateup_fmt<VL_TYPE_IQ2_XXS>(s, in, w, st, kg); break;
+        case VL_TYPE_IQ3_XXS: e = launch_gateup_fmt<VL_TYPE_IQ3_XXS>(s, in, w, st, kg); break;
+        case VL_TYPE_IQ1_S: e = launch_gateup_fmt<VL_TYPE_IQ1_S>(s, in, w, st, kg); break;
+        case VL_TYPE_Q8_0: e = launch_gateup_fmt<VL_TYPE_Q8_0>(s, in, w, st, kg); break;
         default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess) return e;
     mark(kStageDown);
+    const KernelEvents* kd = kev ? &ke[kStageDown] : nullptr;
     switch (s.down_type) {
-        case VL_TYPE_IQ2_XXS: e = launch_down_fmt<VL_TYPE_IQ2_XXS>(s, in, w, st); break;
-        case VL_TYPE_IQ3_XXS: e = launch_down_fmt<VL_TYPE_IQ3_XXS>(s, in, w, st); break;
-        case VL_TYPE_IQ1_S: e = launch_down_fmt<VL_TYPE_IQ1_S>(s, in, w, st); break;
-        case VL_TYPE_Q8_0: e = launch_down_fmt<VL_TYPE_Q8_0>(s, in, w, st); break;
+        case VL_TYPE_IQ2_XXS: e = launch_down_fmt<VL_TYPE_IQ2_XXS>(s, in, w, st, kd); break;
+        case VL_TYPE_IQ3_XXS: e = launch_down_fmt<VL_TYPE_IQ3_XXS>(s, in, w, st, kd); break;
+        case VL_TYPE_IQ1_S: e = launch_down_fmt<VL_TYPE_IQ1_S>(s, in, w, st, kd); break;
+        case VL_TYPE_Q8_0: e = launch_down_fmt<VL_TYPE_Q8_0>(s, in, w, st, kd); break;
         default: return hipErrorInvalidValue;
     }
     mark(kStageCount);

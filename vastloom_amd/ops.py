@@ -195,14 +195,24 @@ class MoeLayer:
 class Timeline:
     """HIP events around the stages of profiled layer calls (vl_timeline_*)."""
 
-    def __init__(self, calls: int):
+    def __init__(self, calls: int, kernel_brackets: bool = False):
+        """kernel_brackets: record each stage's kernel execution (kernel_ms) instead of the
+        marks between stages (stage_ms)."""
         h = C.c_void_p()
         call("vl_timeline_create", calls, C.byref(h))
         self.handle, self.calls = h, calls
+        if kernel_brackets:
+            call("vl_timeline_set_kernel_brackets", self.handle, 1)
 
     def stage_ms(self, slot: int) -> dict[str, float]:
         ms = (C.c_float * len(_lib.STAGES))()
         call("vl_timeline_stage_ms", self.handle, slot, ms)
+        return dict(zip(_lib.STAGES, list(ms)))
+
+    def kernel_ms(self, slot: int) -> dict[str, float]:
+        """Each stage's kernel alone: events recorded by the launch around its execution."""
+        ms = (C.c_float * len(_lib.STAGES))()
+        call("vl_timeline_kernel_ms", self.handle, slot, ms)
         return dict(zip(_lib.STAGES, list(ms)))
 
     def close(self) -> None:

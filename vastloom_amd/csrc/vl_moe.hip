@@ -215,12 +215,9 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
-// Threads 0..255 of the block: partial sums of expert row b's logits for tokens [t0, t1) into
-// red[t - t0][wave] (four waves take interleaved quarters of the row with every lane's float4
-// loads in flight).
-// Threads 0..255: the first 8 float4 of their share of expert row b (issued early by the caller).
-// The row's first 8192 weights and the same columns of token t0's activations, requested
-// together so that both arrive within one memory latency.
+// Threads 0..255: the first 8 float4 of their share of expert row b (its first 8192 weights)
+// and the same columns of token t0's activations, requested together and early by the caller,
+// so that both arrive within one memory latency.
 struct RouterRow {
     float4 wv[8];
     float4 xv[8];
@@ -244,6 +241,9 @@ __device__ __forceinline__ void router_row_load(const MoeShape& s, const MoeInpu
     }
 }
 
+// Threads 0..255 of the block: partial sums of expert row b's logits for tokens [t0, t1) into
+// red[t - t0][wave] (four waves take interleaved quarters of the row with every lane's float4
+// loads in flight).
 __device__ __forceinline__ void router_row_partials(const MoeShape& s, const MoeInputs& in, uint32_t b,
                                                     uint32_t t0, uint32_t t1, double (*red)[4],
                                                     const RouterRow& rr) {

@@ -74,6 +74,30 @@ __device__ __forceinline__ uint32_t byte_entry(uint32_t v, int k, uint32_t lane_
 
 // IQ2_XXS group g of a superblock half (vl_layout.h): grid bytes in w[0..3], sign fields in
 // w[4..7]. Codes select from the palette {8, 25, 43, -8, -25, -43}.
+// IQ2_XXS group g in two halves: the table reads (fetch) and the B fragment from them (finish),
+// so that a caller can have the next group's reads in flight while it finishes this one.
+struct Iq2Fetch {
+    uint64_t a0, b0, a1, b1;
+};
+__device__ __forceinline__ Iq2Fetch fetch_iq2_xxs(const uint32_t (&w)[8], int g, uint32_t lane_off) {
+    const int q = g >> 1, odd = g & 1;
+    const uint32_t gw = w[q], sw = w[4 + q];
+    const uint32_t a0 = byte_entry(gw, 2 * odd, lane_off);
+    const uint32_t a1 = byte_entry(gw, 2 * odd + 1, lane_off);
+    const uint32_t b0 = ((odd ? sw >> 6 : sw << 8) & 0x7f00u) | lane_off;
+    const uint32_t b1 = ((odd ? sw >> 13 : sw << 1) & 0x7f00u) | lane_off;
+    return Iq2Fetch{lds_u64(kTabA + a0), lds_u64(kTabB + b0), lds_u64(kTabA + a1), lds_u64(kTabB + b1)};
+}
+__device__ __forceinline__ i32x4 finish_iq2_xxs(const Iq2Fetch& t) {
+    const uint64_t s0 = t.a0 | t.b0, s1 = t.a1 | t.b1;
+    i32x4 f;
+    f[0] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, lo32(s0));
+    f[1] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, hi32(s0));
+    f[2] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, lo32(s1));
+    f[3] = (int)perm(kIq2PaletteNeg, kIq2PalettePos, hi32(s1));
+    return f;
+}
+
 __device__ __forceinline__ i32x4 decode_iq2_xxs(const uint32_t (&w)[8], int g, uint32_t lane_off) {
     const int q = g >> 1, odd = g & 1;
     const uint32_t gw = w[q], sw = w[4 + q];

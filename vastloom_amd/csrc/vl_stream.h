@@ -414,10 +414,22 @@ __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint3
     int acc[2 * NT];
 #pragma unroll
     for (int i = 0; i < 2 * NT; ++i) acc[i] = 0;
+    // IQ2_XXS: the next group's table reads are issued before this group's fragment is formed
+    // (not with prefetched operands, whose registers leave no room for them).
+    constexpr bool kPipe = FMT == VL_TYPE_IQ2_XXS && !PRE;
+    Iq2Fetch tf[2];
+    if (kPipe) tf[0] = fetch_iq2_xxs(dec.w, 0, lane_off);
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
         int sc;
-        const i32x4 bfr = dec.group(ch, g, lane_off, hh, sc);
+        i32x4 bfr;
+        if (kPipe) {
+            if (g + 1 < 8) tf[(g + 1) & 1] = fetch_iq2_xxs(dec.w, g + 1, lane_off);
+            sc = (int)bfe(g < 4 ? dec.sc_lo : dec.sc_hi, 8u * (uint32_t)(g & 3), 8);
+            bfr = finish_iq2_xxs(tf[g & 1]);
+        } else {
+            bfr = dec.group(ch, g, lane_off, hh, sc);
+        }
         const i32x16 r = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[g], bfr, zero16, 0, 0, 0);
         // |r| < 2^18 and sc <= 31: the 24-bit multiply is exact; the superblock sum stays
         // below 2^27.

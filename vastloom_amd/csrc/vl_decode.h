@@ -164,6 +164,26 @@ __device__ __forceinline__ i32x4 decode_iq1_s(uint32_t qs4, uint32_t qh, int hh)
     return f;
 }
 
+// IQ1_S group in two halves (grid reads with the delta applied, then the fragment).
+struct Iq1Fetch {
+    uint64_t c0, c1;
+};
+__device__ __forceinline__ Iq1Fetch fetch_iq1_s(uint32_t qs4, uint32_t qh, int hh) {
+    const int s0 = 2 * hh;
+    const uint32_t i0 = ((qs4 >> (8 * s0)) & 0xffu) | (((qh >> (3 * s0)) & 7u) << 8);
+    const uint32_t i1 = ((qs4 >> (8 * s0 + 8)) & 0xffu) | (((qh >> (3 * s0 + 3)) & 7u) << 8);
+    const uint64_t dm = (qh & 0x8000u) ? 0x0404040404040404ull : 0ull;
+    return Iq1Fetch{lds_u64(i0 * 8u) | dm, lds_u64(i1 * 8u) | dm};
+}
+__device__ __forceinline__ i32x4 finish_iq1_s(const Iq1Fetch& t) {
+    i32x4 f;
+    f[0] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, lo32(t.c0));
+    f[1] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, hi32(t.c0));
+    f[2] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, lo32(t.c1));
+    f[3] = (int)perm(kIq1PaletteNeg, kIq1PalettePos, hi32(t.c1));
+    return f;
+}
+
 // Exact binary16 -> binary32 (v_cvt_f32_f16; fp16 denormals are preserved on gfx9).
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
     const uint16_t b = (uint16_t)bits;

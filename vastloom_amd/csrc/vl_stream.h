@@ -414,19 +414,29 @@ __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint3
     int acc[2 * NT];
 #pragma unroll
     for (int i = 0; i < 2 * NT; ++i) acc[i] = 0;
-    // IQ2_XXS: the next group's table reads are issued before this group's fragment is formed
-    // (not with prefetched operands, whose registers leave no room for them).
-    constexpr bool kPipe = FMT == VL_TYPE_IQ2_XXS && !PRE;
-    Iq2Fetch tf[2];
-    if (kPipe) tf[0] = fetch_iq2_xxs(dec.w, 0, lane_off);
+    // The next group's table reads are issued before this group's fragment is formed, where the
+    // registers allow: IQ2_XXS without prefetched operands, IQ1_S in the 4- and 8-slot kernels
+    // (256 registers). IQ3_XXS (six reads a group) spills with it and decodes in place.
+    constexpr bool kPipe2 = FMT == VL_TYPE_IQ2_XXS && !PRE;
+    constexpr bool kPipe1 = FMT == VL_TYPE_IQ1_S && !PRE && NT >= 4;
+    Iq2Fetch t2[2];
+    Iq1Fetch t1[2];
+    auto iq1_qs = [&](int g) { return word(g < 4 ? ch.q0 : ch.q1, g & 3); };
+    auto iq1_qh = [&](int g) { return (word(ch.q2, g >> 1) >> (16 * (g & 1))) & 0xffffu; };
+    if (kPipe2) t2[0] = fetch_iq2_xxs(dec.w, 0, lane_off);
+    if (kPipe1) t1[0] = fetch_iq1_s(iq1_qs(0), iq1_qh(0), hh);
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
         int sc;
         i32x4 bfr;
-        if (kPipe) {
-            if (g + 1 < 8) tf[(g + 1) & 1] = fetch_iq2_xxs(dec.w, g + 1, lane_off);
+        if (kPipe2) {
+            if (g + 1 < 8) t2[(g + 1) & 1] = fetch_iq2_xxs(dec.w, g + 1, lane_off);
             sc = (int)bfe(g < 4 ? dec.sc_lo : dec.sc_hi, 8u * (uint32_t)(g & 3), 8);
-            bfr = finish_iq2_xxs(tf[g & 1]);
+            bfr = finish_iq2_xxs(t2[g & 1]);
+        } else if (kPipe1) {
+            if (g + 1 < 8) t1[(g + 1) & 1] = fetch_iq1_s(iq1_qs(g + 1), iq1_qh(g + 1), hh);
+            sc = 2 * (int)((iq1_qh(g) >> 12) & 7u) + 1;
+            bfr = finish_iq1_s(t1[g & 1]);
         } else {
             bfr = dec.group(ch, g, lane_off, hh, sc);
         }

@@ -389,11 +389,15 @@ __device__ __forceinline__ void process_chunk(const Chunk& ch, uint32_t c, uint3
     const uint32_t lane_off = (lane % kTabCopies) * 8u;
     const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     if (FMT == VL_TYPE_Q8_0) {
+        // Block b + 1's A fragment is requested before block b's MFMA (the compiler still waits
+        // for each fragment just before its MFMA; measured −0.1 µs per q8_moe layer).
+        i32x4 anext = PRE ? pre[0] : as.load(4u * c);
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const uint32_t G = 4u * c + b;
             if (G >= ng) break;
-            const i32x4 afr = PRE ? pre[b] : as.load(G);
+            const i32x4 afr = anext;
+            if (b + 1 < 4 && G + 1 < ng) anext = PRE ? pre[b + 1] : as.load(G + 1);
             const uint4& q = b == 0 ? ch.q0 : b == 1 ? ch.q1 : b == 2 ? ch.q2 : ch.q3;
             i32x4 bfr;
             bfr[0] = (int)q.x; bfr[1] = (int)q.y; bfr[2] = (int)q.z; bfr[3] = (int)q.w;

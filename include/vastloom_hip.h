@@ -417,11 +417,15 @@ int vl_accel_destroy(vl_accel* accel);
  * both host memory. VL_OK: output written; VL_DECLINED: output untouched; else an error. */
 int vl_accel_matvec(vl_accel* accel, const vl_packed_matrix* matrix, const float* input,
                     uint64_t input_len, float* output, uint64_t output_len);
-/* Makes the matrix resident without multiplying (upload on first sight). VL_OK or VL_DECLINED. */
+/* Makes the matrix resident without multiplying (upload on first sight). VL_OK or VL_DECLINED.
+ * On VL_OK the resident form is complete: the upload has finished on the device. */
 int vl_accel_prefetch(vl_accel* accel, const vl_packed_matrix* matrix);
 /* 1 when these weights are resident now, else 0 (CudaMatvecAccelerator::holds). */
 int vl_accel_holds(const vl_accel* accel, uint64_t cache_identity);
-/* Device address of a resident matrix's tiled form (for vl_expert_weights), or VL_NOT_FOUND. */
+/* Device address of a resident matrix's tiled form (for vl_expert_weights), or VL_NOT_FOUND. The
+ * address stays valid until the accelerator drops the matrix: a later vl_accel_matvec or
+ * vl_accel_prefetch that needs room may evict it, and vl_accel_destroy releases it. Work that
+ * reads it must have completed before such a call. */
 int vl_accel_resident_matrix(const vl_accel* accel, uint64_t cache_identity, const void** tiled);
 int vl_accel_stats_get(const vl_accel* accel, vl_accel_stats* out);
 

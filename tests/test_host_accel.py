@@ -176,6 +176,19 @@ def test_eviction_prefers_non_recurring_then_least_recent(fake):
     assert acc.holds(1) and acc.holds(5) and acc.stats()["evicted"] == 2
 
 
+def test_eviction_among_recurring_takes_least_recent(fake):
+    acc = make(governor(), fake, maximum_resident_bytes=2 * Q8_1x32_TILED)
+    x, y = np.zeros(32, np.float32), np.zeros(1, np.float32)
+    assert acc.matvec(q8(1, recurring=True), x, y)
+    assert acc.matvec(q8(2, recurring=True), x, y)
+    assert acc.matvec(q8(1, recurring=True), x, y)    # 1 is now more recent than 2
+    assert acc.matvec(q8(3, recurring=True), x, y)    # only recurring matrices: evicts 2
+    assert [acc.holds(i) for i in (1, 2, 3)] == [True, False, True]
+    assert acc.matvec(q8(4), x, y)                    # a non-recurring newcomer evicts 1
+    assert [acc.holds(i) for i in (1, 3, 4)] == [False, True, True]
+    assert acc.stats()["evicted"] == 2 and acc.stats()["resident_matrices"] == 2
+
+
 def test_matrix_count_ceiling(fake):
     acc = make(governor(), fake, maximum_matrices=2)
     x, y = np.zeros(32, np.float32), np.zeros(1, np.float32)

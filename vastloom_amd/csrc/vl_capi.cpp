@@ -184,26 +184,36 @@ int vl_moe_set_fused(int enabled) {
     return VL_OK;
 }
 
-int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
-                 uint64_t workspace_bytes, void* stream) {
-    vl::MoeShape s;
-    if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
+// Everything a layer call checks before it launches: the configuration, the pointers its routing
+// and semantics read, and the workspace size. Fills the launch arguments on success.
+static int prepare_moe(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
+                       uint64_t workspace_bytes, vl::MoeShape* s, vl::MoeInputs* in,
+                       vl::MoeWorkspace* ws) {
+    if (!to_shape(config, s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
     if (!inputs || !inputs->experts || !inputs->x || !inputs->out || !workspace)
         return fail(VL_INVALID_ARGUMENT, "null input pointer");
-    if ((s.routing == vl::kRouteLearned || s.routing == vl::kRouteSoftmax ||
-         s.routing == vl::kRouteTable) && !inputs->router)
+    if (s->routing != vl::kRouteGiven && !inputs->router)
         return fail(VL_INVALID_ARGUMENT, "routing needs the router weights");
-    if (s.routing == vl::kRouteTable && !inputs->table_ids)
+    if (s->routing == vl::kRouteTable && !inputs->table_ids)
         return fail(VL_INVALID_ARGUMENT, "table routing needs table ids");
     const uint32_t blocks = blocks_or_fail();
     if (!blocks) return VL_UNSUPPORTED;
-    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, blocks, workspace);
-    if (workspace_bytes < ws.bytes)
+    *ws = vl::moe_workspace_layout(*s, blocks, workspace);
+    if (workspace_bytes < ws->bytes)
         return fail(VL_INVALID_ARGUMENT, "workspace of %llu bytes is below the %llu needed",
-                    (unsigned long long)workspace_bytes, (unsigned long long)ws.bytes);
-    const vl::MoeInputs in{reinterpret_cast<const vl::MoeExpert*>(inputs->experts),
-                           inputs->router, inputs->bias, inputs->table_ids, inputs->given_ids,
-                           inputs->given_weights, inputs->x, inputs->out};
+                    (unsigned long long)workspace_bytes, (unsigned long long)ws->bytes);
+    *in = vl::MoeInputs{reinterpret_cast<const vl::MoeExpert*>(inputs->experts), inputs->router,
+                        inputs->bias, inputs->table_ids, inputs->given_ids, inputs->given_weights,
+                        inputs->x, inputs->out};
+    return VL_OK;
+}
+
+int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
+                 uint64_t workspace_bytes, void* stream) {
+    vl::MoeShape s;
+    vl::MoeInputs in;
+    vl::MoeWorkspace ws;
+    if (const int rc = prepare_moe(config, inputs, workspace, workspace_bytes, &s, &in, &ws)) return rc;
     const hipError_t e = vl::launch_moe(s, in, ws, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? VL_OK : hip_fail(e, "MoE launch");
 }
@@ -257,18 +267,11 @@ int vl_timeline_set_kernel_brackets(vl_timeline* t, int enabled) {
 int vl_moe_layer_profiled(const vl_moe_config* config, const vl_moe_inputs* inputs,
                           void* workspace, uint64_t workspace_bytes, void* stream,
                           vl_timeline* timeline, uint32_t call) {
-    if (!timeline || call >= timeline->calls) return fail(VL_INVALID_ARGUMENT, "bad timeline slot");
     vl::MoeShape s;
-    if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
-    if (!inputs || !inputs->experts || !inputs->x || !inputs->out || !workspace)
-        return fail(VL_INVALID_ARGUMENT, "null input pointer");
-    const uint32_t blocks = blocks_or_fail();
-    if (!blocks) return VL_UNSUPPORTED;
-    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, blocks, workspace);
-    if (workspace_bytes < ws.bytes) return fail(VL_INVALID_ARGUMENT, "workspace too small");
-    const vl::MoeInputs in{reinterpret_cast<const vl::MoeExpert*>(inputs->experts),
-                           inputs->router, inputs->bias, inputs->table_ids, inputs->given_ids,
-                           inputs->given_weights, inputs->x, inputs->out};
+    vl::MoeInputs in;
+    vl::MoeWorkspace ws;
+    if (const int rc = prepare_moe(config, inputs, workspace, workspace_bytes, &s, &in, &ws)) return rc;
+    if (!timeline || call >= timeline->calls) return fail(VL_INVALID_ARGUMENT, "bad timeline slot");
     hipEvent_t* ev = timeline->events.data() + (size_t)call * (vl::kStageCount + 1);
     hipEvent_t* kev = timeline->kernels.data() + (size_t)call * 2u * vl::kStageCount;
     timeline->bracketed[call] = timeline->brackets ? 1 : 0;

@@ -7,6 +7,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <list>
 #include <mutex>
 #include <new>
 #include <string>
@@ -21,58 +22,124 @@
 using vl::fail;
 
 // ------------------------------------------------------------------------------------------
-// Governor (src/safety/resource_governor.cpp).
+// Governor: the behaviour of safety::ResourceGovernor (src/safety/resource_governor.cpp:19-214),
+// written as data. A reservation passes through an ordered table of admission rules; the first
+// rule that objects decides the status. The safety state is the largest level any pressure
+// signal raises (a budget's fill ratio, an availability floor), stepped through a hysteresis
+// function that climbs at once and descends one level per run of calm samples.
 // ------------------------------------------------------------------------------------------
 
+namespace {
+
+constexpr uint32_t kKinds = 4;
+constexpr uint32_t kHostKinds[] = {VL_KIND_RAM, VL_KIND_STAGING, VL_KIND_SCRATCH};
+
+uint64_t sat_add(uint64_t a, uint64_t b) { return a > UINT64_MAX - b ? UINT64_MAX : a + b; }
+uint64_t sat_mul(uint64_t a, uint64_t b) { return b && a > UINT64_MAX / b ? UINT64_MAX : a * b; }
+
+}  // namespace
+
 struct vl_governor {
-    struct Held {
+    vl_resource_limits limits{};
+    mutable std::mutex mutex;
+    uint64_t used[kKinds]{};  // bytes held per kind
+    uint32_t level = VL_STATE_NORMAL;
+    uint32_t calm_samples = 0;  // consecutive samples below the current level
+    uint64_t next_id = 1;
+    struct Grant {
         uint32_t kind;
         uint64_t bytes;
     };
-    vl_resource_limits limits{};
-    mutable std::mutex mutex;
-    uint64_t reserved[4]{};
-    uint32_t state = VL_STATE_NORMAL;
-    uint32_t recovery_counter = 0;
-    uint64_t next_id = 1;
-    std::unordered_map<uint64_t, Held> held;
+    std::unordered_map<uint64_t, Grant> grants;
 
-    uint64_t limit_for(uint32_t kind) const {
-        switch (kind) {
-            case VL_KIND_RAM: return limits.ram_hard_limit;
-            case VL_KIND_VRAM: return limits.vram_hard_limit;
-            case VL_KIND_STAGING: return limits.staging_hard_limit;
-            case VL_KIND_SCRATCH: return limits.scratch_hard_limit;
-            default: return 0;
-        }
+    uint64_t budget(uint32_t kind) const {
+        const uint64_t b[kKinds] = {limits.ram_hard_limit, limits.vram_hard_limit,
+                                    limits.staging_hard_limit, limits.scratch_hard_limit};
+        return kind < kKinds ? b[kind] : 0;
+    }
+    // Host-side bytes held (RAM, staging, scratch), saturating.
+    uint64_t host_used() const {
+        uint64_t t = 0;
+        for (uint32_t k : kHostKinds) t = sat_add(t, used[k]);
+        return t;
     }
 };
 
 namespace {
 
-const char* kind_name(uint32_t kind) {
-    switch (kind) {
-        case VL_KIND_RAM: return "ram";
-        case VL_KIND_VRAM: return "vram";
-        case VL_KIND_STAGING: return "staging";
-        case VL_KIND_SCRATCH: return "scratch";
-        default: return "unknown";
-    }
-}
+const char* const kKindNames[kKinds] = {"ram", "vram", "staging", "scratch"};
+const char* const kLevelNames[4] = {"normal", "pressure", "critical", "emergency"};
 
-const char* state_name(uint32_t state) {
-    switch (state) {
-        case VL_STATE_NORMAL: return "normal";
-        case VL_STATE_PRESSURE: return "pressure";
-        case VL_STATE_CRITICAL: return "critical";
-        default: return "emergency";
-    }
-}
+struct Request {
+    uint32_t kind;
+    uint64_t bytes;
+    const char* tag;
+};
 
-uint32_t ratio_state(double ratio, const vl_resource_limits& l) {
+// Admission rules, in the order they are consulted. Each returns VL_OK to let the request pass.
+int admit_nonzero(const vl_governor&, const Request& r) {
+    return r.bytes ? VL_OK : fail(VL_INVALID_ARGUMENT, "governor: empty request (%s)", r.tag);
+}
+int admit_open(const vl_governor& g, const Request& r) {
+    return g.level < VL_STATE_CRITICAL
+               ? VL_OK
+               : fail(VL_RESOURCE_EXHAUSTED, "governor: closed to new work while %s (%s)",
+                      kLevelNames[g.level], r.tag);
+}
+int admit_kind_budget(const vl_governor& g, const Request& r) {
+    const uint64_t cap = g.budget(r.kind);
+    const bool fits = cap != 0 && r.bytes <= cap && g.used[r.kind] <= cap - r.bytes;
+    return fits ? VL_OK
+                : fail(VL_RESOURCE_EXHAUSTED, "governor: %s budget cannot take %llu more bytes (%s)",
+                       kKindNames[r.kind], (unsigned long long)r.bytes, r.tag);
+}
+int admit_host_total(const vl_governor& g, const Request& r) {
+    const uint64_t cap = g.limits.host_memory_hard_limit;
+    if (r.kind == VL_KIND_VRAM || cap == 0) return VL_OK;
+    const uint64_t held = g.host_used();
+    if (held > cap)
+        return fail(VL_INTEGRITY_ERROR, "governor: host bytes held already exceed the host budget (%s)", r.tag);
+    return r.bytes <= cap - held
+               ? VL_OK
+               : fail(VL_RESOURCE_EXHAUSTED, "governor: host budget cannot take %llu more bytes (%s)",
+                      (unsigned long long)r.bytes, r.tag);
+}
+using AdmissionRule = int (*)(const vl_governor&, const Request&);
+constexpr AdmissionRule kAdmission[] = {admit_nonzero, admit_open, admit_kind_budget, admit_host_total};
+
+// Level signalled by a budget holding `held` of `cap` bytes (no signal without a budget).
+uint32_t fill_level(uint64_t held, uint64_t cap, const vl_resource_limits& l) {
+    if (cap == 0) return VL_STATE_NORMAL;
+    const double ratio = (double)held / (double)cap;
     return ratio >= l.critical_ratio ? VL_STATE_CRITICAL
          : ratio >= l.pressure_ratio ? VL_STATE_PRESSURE
                                      : VL_STATE_NORMAL;
+}
+
+// Level signalled by `avail` bytes against a configured floor: a quarter of the floor or less is
+// an emergency, the floor or less critical, twice the floor or less pressure.
+uint32_t floor_level(uint64_t avail, uint64_t floor) {
+    static constexpr struct {
+        uint64_t num, den;
+        uint32_t level;
+    } kSteps[] = {{1, 4, VL_STATE_EMERGENCY}, {1, 1, VL_STATE_CRITICAL}, {2, 1, VL_STATE_PRESSURE}};
+    for (const auto& st : kSteps)
+        if (avail <= sat_mul(floor, st.num) / st.den) return st.level;
+    return VL_STATE_NORMAL;
+}
+
+// One sample of the hysteresis: a higher level is taken at once; a lower one only after
+// recovery_samples consecutive lower samples, and then one level at a time.
+void settle(vl_governor& g, uint32_t signalled) {
+    if (signalled > g.level) {
+        g.level = signalled;
+        g.calm_samples = 0;
+    } else if (signalled == g.level) {
+        g.calm_samples = 0;
+    } else if (++g.calm_samples >= g.limits.recovery_samples) {
+        --g.level;
+        g.calm_samples = 0;
+    }
 }
 
 // Native Governor behind vl_governor_ops.
@@ -117,10 +184,12 @@ int vl_governor_create(const vl_resource_limits* limits, vl_governor** out) {
     vl_governor* g = new (std::nothrow) vl_governor;
     if (!g) return fail(VL_RESOURCE_EXHAUSTED, "unable to allocate the governor");
     g->limits = *limits;
-    // ResourceGovernor::ResourceGovernor (resource_governor.cpp:58-62).
-    g->limits.pressure_ratio = std::clamp(g->limits.pressure_ratio, 0.10, 0.99);
-    g->limits.critical_ratio = std::clamp(g->limits.critical_ratio, g->limits.pressure_ratio + 0.01, 1.0);
-    g->limits.recovery_samples = std::max(1u, g->limits.recovery_samples);
+    // The ratios are kept in [0.10, 0.99] and above the pressure ratio, and at least one calm
+    // sample is needed to recover (ResourceGovernor::ResourceGovernor, resource_governor.cpp:58-62).
+    vl_resource_limits& l = g->limits;
+    l.pressure_ratio = std::clamp(l.pressure_ratio, 0.10, 0.99);
+    l.critical_ratio = std::clamp(l.critical_ratio, l.pressure_ratio + 0.01, 1.0);
+    l.recovery_samples = std::max(1u, l.recovery_samples);
     *out = g;
     return VL_OK;
 }
@@ -130,57 +199,39 @@ void vl_governor_destroy(vl_governor* g) { delete g; }
 int vl_governor_try_reserve(vl_governor* g, uint32_t kind, uint64_t bytes, const char* tag,
                             uint64_t* id) {
     if (!g || !id) return fail(VL_INVALID_ARGUMENT, "null argument");
-    const char* t = tag ? tag : "";
-    if (kind > VL_KIND_SCRATCH) return fail(VL_INVALID_ARGUMENT, "unknown resource kind %u (%s)", kind, t);
-    if (bytes == 0) return fail(VL_INVALID_ARGUMENT, "A zero-byte reservation is not allowed (%s)", t);
+    if (kind >= kKinds) return fail(VL_INVALID_ARGUMENT, "governor: unknown resource kind %u", kind);
+    const Request req{kind, bytes, tag ? tag : ""};
+    if (!bytes) return admit_nonzero(*g, req);
     std::lock_guard<std::mutex> lock(g->mutex);
-    if (g->state == VL_STATE_CRITICAL || g->state == VL_STATE_EMERGENCY)
-        return fail(VL_RESOURCE_EXHAUSTED, "Safety governor rejected new work in %s state (%s)",
-                    state_name(g->state), t);
-    const uint64_t limit = g->limit_for(kind);
-    if (limit == 0 || bytes > limit || g->reserved[kind] > limit - bytes)
-        return fail(VL_RESOURCE_EXHAUSTED, "Reservation would exceed the hard %s budget (%s)",
-                    kind_name(kind), t);
-    if (kind != VL_KIND_VRAM && g->limits.host_memory_hard_limit != 0) {
-        uint64_t remaining = g->limits.host_memory_hard_limit;
-        for (uint32_t hk : {VL_KIND_RAM, VL_KIND_STAGING, VL_KIND_SCRATCH}) {
-            if (g->reserved[hk] > remaining)
-                return fail(VL_INTEGRITY_ERROR,
-                            "Host-memory reservations exceed their aggregate hard limit (%s)", t);
-            remaining -= g->reserved[hk];
-        }
-        if (bytes > remaining)
-            return fail(VL_RESOURCE_EXHAUSTED,
-                        "Reservation would exceed the aggregate host-memory budget (%s)", t);
-    }
+    for (AdmissionRule rule : kAdmission)
+        if (const int rc = rule(*g, req)) return rc;
     try {
-        const uint64_t rid = g->next_id++;
-        g->held.emplace(rid, vl_governor::Held{kind, bytes});
-        g->reserved[kind] += bytes;
-        *id = rid;
+        g->grants.emplace(g->next_id, vl_governor::Grant{kind, bytes});
     } catch (const std::bad_alloc&) {
-        return fail(VL_RESOURCE_EXHAUSTED, "unable to record a reservation (%s)", t);
+        return fail(VL_RESOURCE_EXHAUSTED, "governor: no memory to record the grant (%s)", req.tag);
     }
+    g->used[kind] += bytes;
+    *id = g->next_id++;
     return VL_OK;
 }
 
 int vl_governor_release(vl_governor* g, uint64_t id) {
     if (!g) return fail(VL_INVALID_ARGUMENT, "null governor");
     std::lock_guard<std::mutex> lock(g->mutex);
-    auto it = g->held.find(id);
-    if (it == g->held.end()) return fail(VL_NOT_FOUND, "no reservation %llu", (unsigned long long)id);
-    uint64_t& r = g->reserved[it->second.kind];
-    r = it->second.bytes >= r ? 0 : r - it->second.bytes;
-    g->held.erase(it);
+    const auto it = g->grants.find(id);
+    if (it == g->grants.end()) return fail(VL_NOT_FOUND, "governor: no grant %llu", (unsigned long long)id);
+    uint64_t& u = g->used[it->second.kind];
+    u -= std::min(u, it->second.bytes);
+    g->grants.erase(it);
     return VL_OK;
 }
 
 int vl_governor_abandon(vl_governor* g, uint64_t id) {
     if (!g) return fail(VL_INVALID_ARGUMENT, "null governor");
     std::lock_guard<std::mutex> lock(g->mutex);
-    auto it = g->held.find(id);
-    if (it == g->held.end()) return fail(VL_NOT_FOUND, "no reservation %llu", (unsigned long long)id);
-    g->held.erase(it);  // the bytes stay in reserved[]
+    // The grant is forgotten but its bytes stay in used[]: memory that could not be freed must not
+    // be handed out again.
+    if (!g->grants.erase(id)) return fail(VL_NOT_FOUND, "governor: no grant %llu", (unsigned long long)id);
     return VL_OK;
 }
 
@@ -188,46 +239,23 @@ int vl_governor_update_pressure(vl_governor* g, const vl_runtime_pressure* p, ui
     if (!g || !p) return fail(VL_INVALID_ARGUMENT, "null argument");
     std::lock_guard<std::mutex> lock(g->mutex);
     const vl_resource_limits& l = g->limits;
-    uint32_t raw = VL_STATE_NORMAL;
-    const uint64_t hard[4] = {l.ram_hard_limit, l.vram_hard_limit, l.staging_hard_limit, l.scratch_hard_limit};
-    for (uint32_t k = 0; k < 4; ++k)
-        if (hard[k] != 0) raw = std::max(raw, ratio_state((double)g->reserved[k] / (double)hard[k], l));
-    if (l.host_memory_hard_limit != 0) {
-        uint64_t host = 0;
-        for (uint32_t hk : {VL_KIND_RAM, VL_KIND_STAGING, VL_KIND_SCRATCH}) {
-            const uint64_t r = g->reserved[hk];
-            host = r > l.host_memory_hard_limit - host ? l.host_memory_hard_limit : host + r;
-        }
-        raw = std::max(raw, ratio_state((double)host / (double)l.host_memory_hard_limit, l));
-    }
-    const auto reserve_state = [&raw](uint64_t avail, uint64_t minimum) {
-        if (avail <= minimum / 4u) raw = VL_STATE_EMERGENCY;
-        else if (avail <= minimum) raw = std::max(raw, (uint32_t)VL_STATE_CRITICAL);
-        else if (avail <= minimum * 2u) raw = std::max(raw, (uint32_t)VL_STATE_PRESSURE);
-    };
-    reserve_state(p->system_ram_available, l.minimum_system_ram_available);
-    reserve_state(p->storage_available, l.minimum_storage_available);
-    if (raw > g->state) {
-        g->state = raw;
-        g->recovery_counter = 0;
-    } else if (raw < g->state) {
-        if (++g->recovery_counter >= l.recovery_samples) {
-            g->state -= 1;
-            g->recovery_counter = 0;
-        }
-    } else {
-        g->recovery_counter = 0;
-    }
-    if (state) *state = g->state;
+    uint32_t signals[kKinds + 3];
+    uint32_t n = 0;
+    for (uint32_t k = 0; k < kKinds; ++k) signals[n++] = fill_level(g->used[k], g->budget(k), l);
+    signals[n++] = fill_level(std::min(g->host_used(), l.host_memory_hard_limit), l.host_memory_hard_limit, l);
+    signals[n++] = floor_level(p->system_ram_available, l.minimum_system_ram_available);
+    signals[n++] = floor_level(p->storage_available, l.minimum_storage_available);
+    settle(*g, *std::max_element(signals, signals + n));
+    if (state) *state = g->level;
     return VL_OK;
 }
 
 int vl_governor_snapshot_get(const vl_governor* g, vl_governor_snapshot* out) {
     if (!g || !out) return fail(VL_INVALID_ARGUMENT, "null argument");
     std::lock_guard<std::mutex> lock(g->mutex);
-    out->state = g->state;
-    out->recovery_counter = g->recovery_counter;
-    for (int k = 0; k < 4; ++k) out->reserved[k] = g->reserved[k];
+    out->state = g->level;
+    out->recovery_counter = g->calm_samples;
+    std::copy(g->used, g->used + kKinds, out->reserved);
     return VL_OK;
 }
 
@@ -456,6 +484,10 @@ int hb_upload(void* ctx, uint32_t type, uint64_t rows, uint64_t cols, const void
         if (rc == VL_OK) rc = hip_check(hipEventRecord(hb->pack_done[s], hb->compute), "hipEventRecord");
         hb->used[s] = true;
     }
+    // The matrix is complete when the upload returns (as the reference's synchronous
+    // copy_from_host leaves it): its pointer may be handed to kernels on any stream, and the
+    // upload time covers the whole transfer.
+    if (rc == VL_OK) rc = hip_check(hipStreamSynchronize(hb->compute), "hipStreamSynchronize");
     return rc;
 }
 
@@ -579,31 +611,35 @@ void hb_synchronize(HipBackend* hb) {
 }  // namespace
 
 // ------------------------------------------------------------------------------------------
-// Accelerator (src/cuda/cuda_matvec_accelerator.cpp:102-314).
+// Accelerator: the residency policy of CudaMatvecAccelerator
+// (src/cuda/cuda_matvec_accelerator.cpp:102-314). A matrix offered for the first time is
+// classified (taken, or declined for one of the policy's reasons); a taken matrix that is not
+// resident is uploaded after room is made. Resident matrices sit in two recency queues: the
+// matrices whose descriptors say they will not be asked for again this pass, and the recurring
+// ones. Room is made from the front (least recently used end) of the first queue, and only when
+// it is empty from the second, so a pass's stream of routed experts cannot push out the weights
+// every token needs. A hit moves a matrix to the back of its queue.
 // ------------------------------------------------------------------------------------------
 
 struct vl_accel {
-    struct Resident {
-        void* tiled = nullptr;
-        uint64_t reservation = 0;
-        uint64_t total_bytes = 0;
-        uint64_t matrix_bytes = 0;
-        uint64_t last_used = 0;
-        uint64_t rows = 0, cols = 0;
-        uint32_t type = 0;
-        bool recurring = false;
-    };
     struct Held {  // a Governor-reserved device or pinned allocation
         void* ptr = nullptr;
         uint64_t reservation = 0;
         uint64_t bytes = 0;
+    };
+    struct Resident {
+        Held mem;                  // tiled matrix (device)
+        uint64_t rows = 0, cols = 0;
+        uint32_t type = 0;
+        bool recurring = false;
+        std::list<uint64_t>::iterator queue_pos;  // in queue[recurring]
     };
     vl_accel_options opt{};
     vl_governor_ops gov{};
     vl_accel_backend be{};
     HipBackend* hip = nullptr;  // owned when be is the HIP backend
     std::unordered_map<uint64_t, Resident> resident;
-    uint64_t clock = 0;
+    std::list<uint64_t> queue[2];  // [0] not recurring, [1] recurring; front = least recently used
     vl_accel_stats stats{};
     Held staging, scratch, io;
 };
@@ -615,19 +651,16 @@ bool has_kernel(uint32_t type) {
            type == VL_GGML_IQ1_S;
 }
 
+// Counts a declined storage type in the first free or matching slot; types beyond the slots go
+// uncounted (a statistic, never a failure).
 void count_declined_type(vl_accel_stats& st, uint32_t type) {
     for (uint32_t i = 0; i < VL_ACCEL_TYPE_SLOTS; ++i) {
-        if (st.declined_by_type[i] != 0 && st.declined_type[i] == type) {
+        if (st.declined_by_type[i] == 0) st.declined_type[i] = type;
+        if (st.declined_type[i] == type) {
             ++st.declined_by_type[i];
             return;
         }
-        if (st.declined_by_type[i] == 0) {
-            st.declined_type[i] = type;
-            st.declined_by_type[i] = 1;
-            return;
-        }
     }
-    // More distinct types than slots: losing a statistic is not a reason to fail.
 }
 
 // Reserve, check the free-memory floor (device memory), allocate. A refusal returns
@@ -664,97 +697,100 @@ int give_back(vl_accel* a, uint32_t kind, vl_accel::Held* h) {
     const int rc = a->be.release(a->be.ctx, kind, h->ptr);
     if (rc != VL_OK) a->gov.abandon(a->gov.ctx, h->reservation);
     else a->gov.release(a->gov.ctx, h->reservation);
-    h->ptr = nullptr;
-    h->reservation = 0;
-    h->bytes = 0;
+    *h = vl_accel::Held{};
     return rc;
 }
 
-int release_resident(vl_accel* a, vl_accel::Resident& r) {
-    vl_accel::Held h{r.tiled, r.reservation, r.total_bytes};
-    r.tiled = nullptr;
-    return give_back(a, VL_KIND_VRAM, &h);
+// Why an offered matrix is or is not taken.
+enum class Offer { kTake, kRecurringRefused, kNoKernel, kBadShape, kNoIdentity };
+
+Offer classify(const vl_accel& a, const vl_packed_matrix& m) {
+    if (a.opt.experts_only && m.recurring) return Offer::kRecurringRefused;
+    if (!has_kernel(m.ggml_type)) return Offer::kNoKernel;
+    uint32_t elems = 0, bytes = 0;
+    vl_block_shape(m.ggml_type, &elems, &bytes);
+    if (!m.rows || !m.storage_columns || m.storage_columns % elems) return Offer::kBadShape;
+    return m.cache_identity ? Offer::kTake : Offer::kNoIdentity;
 }
 
-// The resident entry for this matrix, uploading it on first sight; *out = nullptr means the
-// accelerator declines it (CudaMatvecAccelerator::ensure_resident).
+// Drops one resident matrix: the front of the not-recurring queue, else of the recurring one.
+int evict_one(vl_accel* a) {
+    std::list<uint64_t>& q = a->queue[0].empty() ? a->queue[1] : a->queue[0];
+    const auto it = a->resident.find(q.front());
+    q.pop_front();
+    const uint64_t freed = it->second.mem.bytes;
+    const int rc = give_back(a, VL_KIND_VRAM, &it->second.mem);
+    a->resident.erase(it);
+    a->stats.resident_bytes -= std::min(freed, a->stats.resident_bytes);
+    a->stats.resident_matrices = a->resident.size();
+    ++a->stats.evicted;
+    return rc;
+}
+
+// The resident entry for this matrix, uploading it on first sight; *out stays null when the
+// accelerator declines it (a decline is not an error: the caller runs its CPU path).
 int ensure_resident(vl_accel* a, const vl_packed_matrix& m, vl_accel::Resident** out) {
     *out = nullptr;
-    if (a->opt.experts_only && m.recurring) {
-        ++a->stats.declined_recurring;
-        return VL_OK;
+    switch (classify(*a, m)) {
+        case Offer::kRecurringRefused: ++a->stats.declined_recurring; return VL_OK;
+        case Offer::kNoKernel: count_declined_type(a->stats, m.ggml_type); return VL_OK;
+        case Offer::kBadShape:
+        case Offer::kNoIdentity: return VL_OK;
+        case Offer::kTake: break;
     }
-    if (!has_kernel(m.ggml_type)) {
-        count_declined_type(a->stats, m.ggml_type);
-        return VL_OK;
-    }
-    uint32_t be = 0, bb = 0;
-    vl_block_shape(m.ggml_type, &be, &bb);
-    if (m.rows == 0 || m.storage_columns == 0 || m.storage_columns % be != 0) return VL_OK;
-    if (m.cache_identity == 0) return VL_OK;
-    auto it = a->resident.find(m.cache_identity);
-    if (it != a->resident.end()) {
-        it->second.last_used = ++a->clock;
-        *out = &it->second;
+    if (const auto hit = a->resident.find(m.cache_identity); hit != a->resident.end()) {
+        vl_accel::Resident& r = hit->second;
+        auto& q = a->queue[r.recurring];
+        q.splice(q.end(), q, r.queue_pos);
+        *out = &r;
         return VL_OK;
     }
     if (!m.encoded) return fail(VL_INVALID_ARGUMENT, "matrix %llu has no payload", (unsigned long long)m.cache_identity);
     vl_tiled_layout L;
-    if (m.rows > 0x7fffffffu || m.storage_columns > 0x7fffffffu ||
-        !vl_make_layout(m.ggml_type, (uint32_t)m.rows, (uint32_t)m.storage_columns, &L))
+    const bool fits32 = m.rows <= 0x7fffffffu && m.storage_columns <= 0x7fffffffu;
+    if (!fits32 || !vl_make_layout(m.ggml_type, (uint32_t)m.rows, (uint32_t)m.storage_columns, &L) ||
+        m.encoded_bytes != L.gguf_bytes)
         return VL_OK;
-    if (m.encoded_bytes != L.gguf_bytes) return VL_OK;
-    const uint64_t total = L.bytes;
-    if (total > a->opt.maximum_resident_bytes) return VL_OK;
-    // Room: evict what will not recur first, then the least recently used.
-    while ((a->stats.resident_bytes + total > a->opt.maximum_resident_bytes ||
-            a->resident.size() >= a->opt.maximum_matrices) &&
-           !a->resident.empty()) {
-        auto victim = std::min_element(a->resident.begin(), a->resident.end(),
-                                       [](const auto& l, const auto& r) {
-                                           if (l.second.recurring != r.second.recurring) return !l.second.recurring;
-                                           return l.second.last_used < r.second.last_used;
-                                       });
-        const uint64_t reclaimed = victim->second.total_bytes;
-        const int rc = release_resident(a, victim->second);
-        a->resident.erase(victim);
-        a->stats.resident_bytes -= std::min(reclaimed, a->stats.resident_bytes);
-        a->stats.resident_matrices = a->resident.size();
-        ++a->stats.evicted;
-        if (rc != VL_OK) return rc;
-    }
-    if (total > a->opt.maximum_resident_bytes - a->stats.resident_bytes) return VL_OK;
-    vl_accel::Held h;
-    // Out of budget or device memory is a reason to stop offering, not to fail the pass.
-    if (acquire(a, VL_KIND_VRAM, total, "vl-accel-resident", &h) != VL_OK) return VL_OK;
-    const auto t0 = std::chrono::steady_clock::now();
-    int rc = a->be.upload(a->be.ctx, m.ggml_type, m.rows, m.storage_columns, m.encoded, h.ptr,
-                          a->staging.ptr, a->scratch.ptr, a->opt.staging_bytes);
-    a->stats.upload_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    if (rc != VL_OK) {
-        const int rel = give_back(a, VL_KIND_VRAM, &h);
-        return rel != VL_OK ? rel : rc;
-    }
+    const uint64_t need = L.bytes, cap = a->opt.maximum_resident_bytes;
+    if (need > cap) return VL_OK;
+    auto crowded = [&] {
+        return a->stats.resident_bytes + need > cap || a->resident.size() >= a->opt.maximum_matrices;
+    };
+    while (crowded() && !a->resident.empty())
+        if (const int rc = evict_one(a)) return rc;
+    if (need > cap - a->stats.resident_bytes) return VL_OK;
     vl_accel::Resident r;
-    r.tiled = h.ptr;
-    r.reservation = h.reservation;
-    r.total_bytes = total;
-    r.matrix_bytes = L.gguf_bytes;
-    r.last_used = ++a->clock;
+    // A Governor or free-memory refusal declines the matrix; it does not fail the pass.
+    if (acquire(a, VL_KIND_VRAM, need, "vl-accel-resident", &r.mem) != VL_OK) return VL_OK;
+    const auto t0 = std::chrono::steady_clock::now();
+    const int up = a->be.upload(a->be.ctx, m.ggml_type, m.rows, m.storage_columns, m.encoded, r.mem.ptr,
+                                a->staging.ptr, a->scratch.ptr, a->opt.staging_bytes);
+    a->stats.upload_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    if (up != VL_OK) {
+        const int rel = give_back(a, VL_KIND_VRAM, &r.mem);
+        return rel != VL_OK ? rel : up;
+    }
     r.rows = m.rows;
     r.cols = m.storage_columns;
     r.type = m.ggml_type;
     r.recurring = m.recurring != 0;
     try {
-        it = a->resident.emplace(m.cache_identity, r).first;
+        auto& q = a->queue[r.recurring];
+        q.push_back(m.cache_identity);
+        r.queue_pos = std::prev(q.end());
+        try {
+            *out = &a->resident.emplace(m.cache_identity, r).first->second;
+        } catch (...) {
+            q.pop_back();
+            throw;
+        }
     } catch (const std::bad_alloc&) {
-        (void)give_back(a, VL_KIND_VRAM, &h);
+        (void)give_back(a, VL_KIND_VRAM, &r.mem);
         return fail(VL_RESOURCE_EXHAUSTED, "unable to record a resident matrix");
     }
     a->stats.uploaded_bytes += L.gguf_bytes;
-    a->stats.resident_bytes += total;
+    a->stats.resident_bytes += need;
     a->stats.resident_matrices = a->resident.size();
-    *out = &it->second;
     return VL_OK;
 }
 
@@ -828,10 +864,12 @@ int vl_accel_destroy(vl_accel* a) {
     if (a->hip) hb_synchronize(a->hip);
     int rc = VL_OK;
     for (auto& kv : a->resident) {
-        const int r = release_resident(a, kv.second);
+        const int r = give_back(a, VL_KIND_VRAM, &kv.second.mem);
         if (rc == VL_OK) rc = r;
     }
     a->resident.clear();
+    a->queue[0].clear();
+    a->queue[1].clear();
     for (vl_accel::Held* h : {&a->io, &a->scratch}) {
         const int r = give_back(a, VL_KIND_VRAM, h);
         if (rc == VL_OK) rc = r;
@@ -866,7 +904,7 @@ int vl_accel_matvec(vl_accel* a, const vl_packed_matrix* m, const float* input, 
         return fail(VL_DECLINED, "no device memory for the matvec buffers");
     }
     const auto t0 = std::chrono::steady_clock::now();
-    rc = a->be.matvec(a->be.ctx, r->type, r->rows, r->cols, r->tiled, input, output, a->io.ptr, a->io.bytes);
+    rc = a->be.matvec(a->be.ctx, r->type, r->rows, r->cols, r->mem.ptr, input, output, a->io.ptr, a->io.bytes);
     if (rc != VL_OK) return rc;
     a->stats.kernel_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     ++a->stats.accelerated;
@@ -890,7 +928,7 @@ int vl_accel_resident_matrix(const vl_accel* a, uint64_t identity, const void** 
     auto it = a->resident.find(identity);
     if (identity == 0 || it == a->resident.end())
         return fail(VL_NOT_FOUND, "matrix %llu is not resident", (unsigned long long)identity);
-    *tiled = it->second.tiled;
+    *tiled = it->second.mem.ptr;
     return VL_OK;
 }
 

@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cmath>
 
 #include "vl_kernels.h"
 #include "vl_moe.h"
@@ -70,6 +71,10 @@ bool moe_shape_ok(const MoeShape& s) {
     if (!vl_block_shape(s.gate_type, &be, &bb) || s.width % be || s.width % 256u) return false;
     if (!vl_block_shape(s.down_type, &be, &bb) || s.inter % be || s.inter % 32u) return false;
     if (s.semantics > kSemPlain || s.routing > kRouteGiven || s.score_fn > kScoreSigmoid) return false;
+    // Learned and table routes scale their weights by route_scale, which the reference requires
+    // to be finite and positive (route_from_indices, deepseek_v4_reference.cpp:80-90).
+    const bool scaled = s.routing == kRouteLearned || s.routing == kRouteTable;
+    if (scaled && !(std::isfinite(s.route_scale) && s.route_scale > 0.0f)) return false;
     return true;
 }
 

@@ -247,16 +247,28 @@ def read_status(workspace: torch.Tensor, stream: int) -> int:
     return bits.value
 
 
-def raise_on_status(workspace: torch.Tensor, stream: int, what: str) -> None:
-    """The reference refuses non-finite inputs (invalid_argument) and non-finite results
-    (invalid_format); the kernels record both in the workspace status word."""
-    bits = read_status(workspace, stream)
+def status_error(bits: int, what: str) -> VlError | None:
+    """The error a device status word stands for, or None. The reference refuses non-finite
+    inputs (invalid_argument), non-finite results (invalid_format) and routes it cannot form
+    (invalid_argument: an out-of-range expert, a non-finite logit or bias, weights that cannot be
+    normalised); a bounded wait that timed out inside a kernel is an internal error."""
+    if bits & _lib.STATUS_INTERNAL:
+        return VlError(10, what, "a device-side wait timed out; the output is not valid")
     if bits & _lib.STATUS_NONFINITE_INPUT:
-        raise VlError(1, what, "input contains a non-finite value")
+        return VlError(1, what, "input contains a non-finite value")
     if bits & _lib.STATUS_NONFINITE_OUTPUT:
-        raise VlError(2, what, "produced a non-finite result")
+        return VlError(2, what, "produced a non-finite result")
     if bits & _lib.STATUS_BAD_ROUTE:
-        raise VlError(2, what, "router selected an out-of-range expert")
+        return VlError(1, what, "the routing cannot be formed (out-of-range expert, non-finite "
+                                "logit or bias, or weights that cannot be normalised)")
+    return None
+
+
+def raise_on_status(workspace: torch.Tensor, stream: int, what: str) -> None:
+    """Raises the error the kernels recorded in the workspace status word, if any."""
+    err = status_error(read_status(workspace, stream), what)
+    if err is not None:
+        raise err
 
 
 __all__ = ["DeviceMatrix", "device_count", "matrix_layout", "lib", "VlError", "QUANT_TYPES"]

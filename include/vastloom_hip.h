@@ -206,6 +206,22 @@ int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes);
 int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
                  uint64_t workspace_bytes, void* stream);
 
+/* vl_moe_layer without a caller-owned workspace, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The workspace is a fixed 64 MiB array in the library's device
+ * memory, one per device, looked up (never allocated) on the first call on that device; layers
+ * whose workspace would exceed it are refused with VL_RESOURCE_EXHAUSTED before anything is
+ * launched (single-token and small multi-token layers fit; large prefill batches do not). Every
+ * call on one device shares that device's array, so calls that overlap on one device (on
+ * different streams or from different threads without ordering) race and give undefined results.
+ * Each call clears what it needs zeroed itself, on the stream. */
+int vl_moe_layer_noalloc(const vl_moe_config* config, const vl_moe_inputs* inputs, void* stream);
+
+/* Synchronizes the stream and returns the status bits of the last vl_moe_layer_noalloc on the
+ * current device (as vl_read_status does for a caller's workspace). No counterpart in the
+ * reference; for the same callers. */
+int vl_moe_noalloc_status(void* stream, uint32_t* bits);
+
 /* Whether vl_moe_layer may run a layer as one cooperative launch where that applies (one or two
  * tokens, one storage type for gate/up and down); process-wide, off by default (on MI355X the
  * three-kernel sequence is faster). Both ways give bit-identical outputs; the switch exists for

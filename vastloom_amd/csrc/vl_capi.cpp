@@ -218,6 +218,35 @@ int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void*
     return e == hipSuccess ? VL_OK : hip_fail(e, "MoE launch");
 }
 
+int vl_moe_layer_noalloc(const vl_moe_config* config, const vl_moe_inputs* inputs, void* stream) {
+    vl::MoeShape s;
+    if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
+    const uint32_t blocks = blocks_or_fail();
+    if (!blocks) return VL_UNSUPPORTED;
+    const uint64_t need = vl::moe_workspace_bytes(s, blocks);
+    if (need > vl::kStaticWorkspaceBytes)
+        return fail(VL_RESOURCE_EXHAUSTED,
+                    "this layer needs a %llu-byte workspace; the static workspace holds %llu bytes "
+                    "(use vl_moe_layer with a caller-owned workspace)",
+                    (unsigned long long)need, (unsigned long long)vl::kStaticWorkspaceBytes);
+    void* ws_ptr = nullptr;
+    const hipError_t se = vl::static_workspace(&ws_ptr);
+    if (se != hipSuccess) return hip_fail(se, "static workspace lookup");
+    vl::MoeInputs in;
+    vl::MoeWorkspace ws;
+    if (const int rc = prepare_moe(config, inputs, ws_ptr, vl::kStaticWorkspaceBytes, &s, &in, &ws)) return rc;
+    const hipError_t e = vl::launch_moe(s, in, ws, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? VL_OK : hip_fail(e, "MoE launch");
+}
+
+int vl_moe_noalloc_status(void* stream, uint32_t* bits) {
+    if (!bits) return fail(VL_INVALID_ARGUMENT, "bits is null");
+    void* ws_ptr = nullptr;
+    const hipError_t se = vl::static_workspace(&ws_ptr);
+    if (se != hipSuccess) return hip_fail(se, "static workspace lookup");
+    return vl_read_status(ws_ptr, stream, bits);
+}
+
 }  // extern "C"
 
 struct vl_timeline {

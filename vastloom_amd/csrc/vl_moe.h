@@ -103,6 +103,13 @@ hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace
                       hipStream_t stream, hipEvent_t* events = nullptr,
                       hipEvent_t* kernel_events = nullptr);
 
+// Bytes of the per-device workspace that vl_moe_layer_noalloc uses instead of a caller's buffer.
+constexpr uint64_t kStaticWorkspaceBytes = 64ull << 20;
+
+// Device address of the current device's static workspace (kStaticWorkspaceBytes), looked up on
+// the first call for each device; nothing is allocated.
+hipError_t static_workspace(void** ptr);
+
 }  // namespace vl
 
 #endif  // VL_MOE_H

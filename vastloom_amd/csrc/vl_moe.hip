@@ -21,6 +21,7 @@
 #include <stdint.h>
 
 #include <cmath>
+#include <mutex>
 
 #include "vl_kernels.h"
 #include "vl_moe.h"
@@ -2494,6 +2495,38 @@ hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace
     }
     mark(kStageCount);
     return e;
+}
+
+// ------------------------------------------------------------------------------------------
+// Workspace for callers that cannot allocate: one array per device, in the code object's own
+// device memory, shared by every call on that device.
+// ------------------------------------------------------------------------------------------
+
+static __device__ __align__(256) uint8_t scratch[kStaticWorkspaceBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// The address of the current device's scratch array, looked up once per device (the array's name
+// is a host-side stand-in, not a device address).
+hipError_t static_workspace(void** ptr) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return hipSuccess;
 }
 
 }  // namespace vl

@@ -50,7 +50,7 @@ typedef enum vl_status {
 #define VL_STATUS_NONFINITE_INPUT 1u
 #define VL_STATUS_NONFINITE_OUTPUT 2u
 #define VL_STATUS_BAD_ROUTE 4u
-#define VL_STATUS_INTERNAL 8u /* a bounded wait inside a single-launch layer timed out */
+#define VL_STATUS_INTERNAL 8u /* reserved: a bounded device-side wait gave up; the output is not valid */
 
 /* Thread-local message describing the last non-zero status returned on this thread. */
 const char* vl_last_error(void);
@@ -221,12 +221,6 @@ int vl_moe_layer_noalloc(const vl_moe_config* config, const vl_moe_inputs* input
  * current device (as vl_read_status does for a caller's workspace). No counterpart in the
  * reference; for the same callers. */
 int vl_moe_noalloc_status(void* stream, uint32_t* bits);
-
-/* Whether vl_moe_layer may run a layer as one cooperative launch where that applies (one or two
- * tokens, one storage type for gate/up and down); process-wide, off by default (on MI355X the
- * three-kernel sequence is faster). Both ways give bit-identical outputs; the switch exists for
- * comparison and measurement. No counterpart in the reference. */
-int vl_moe_set_fused(int enabled);
 
 /* Routing chosen by the last vl_moe_layer on this workspace: ids and weights [tokens][top_k]
  * copied to host memory (synchronizes the stream). */

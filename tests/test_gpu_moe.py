@@ -300,37 +300,3 @@ def test_workload_grouped_moe(ops, lib, oracle):
     _check_layer(ops, lib, oracle, wl, experts, shared, "deepseek", "table", lib.ROUTE_TABLE,
                  wl.x(), SCORE_SIGMOID, table=wl.zipf_table(),
                  sample=[0, 1, 77, 255, 256, 400, 511])
-
-
-# -- Single-launch layer ----------------------------------------------------------------------------
-
-@pytest.mark.parametrize("tokens,gt", [(1, IQ2_XXS), (2, IQ2_XXS), (1, Q8_0), (2, IQ3_XXS), (1, IQ1_S)])
-def test_fused_layer_bit_identical_to_launch_sequence(ops, lib, oracle, tokens, gt):
-    """One or two tokens with one storage type run as a single cooperative launch; the outputs
-    and routes must equal the three-launch sequence's bit for bit, and the oracle's within the
-    tolerance."""
-    print(f"[moe fused] tokens={tokens} type={gt}", flush=True)
-    rng = np.random.default_rng(100 + tokens + gt)
-    from vastloom_amd.workloads import MoeWorkload
-    E, K, H, F = 24, 4, 1024, 512
-    wl = MoeWorkload("fused_small", 17, H, F, E, K, tokens, gt, gt, 0.01, "deepseek")
-    experts = [make_expert(rng, gt, gt, H, F) for _ in range(E)]
-    shared = make_expert(rng, gt, gt, H, F)
-    x = rng.standard_normal((tokens, H)).astype(np.float32)
-    try:
-        lib.call("vl_moe_set_fused", 1)
-        layer = _check_layer(ops, lib, oracle, wl, experts, shared, "deepseek", "learned",
-                             lib.ROUTE_LEARNED, x, SCORE_SIGMOID, route_scale=1.5,
-                             routed_limit=0.3, shared_limit=0.2)
-        xt = torch.from_numpy(x).cuda()
-        fused = [layer.forward(xt).cpu().numpy() for _ in range(3)]
-        # The launch's grid barrier works from whatever the workspace holds.
-        ws = layer.workspace(tokens)
-        ws.copy_(torch.from_numpy(rng.integers(0, 256, ws.numel(), dtype=np.uint8)).cuda())
-        fused.append(layer.forward(xt).cpu().numpy())
-        lib.call("vl_moe_set_fused", 0)
-        seq = layer.forward(xt).cpu().numpy()
-    finally:
-        lib.call("vl_moe_set_fused", 0)
-    for f in fused:
-        assert np.array_equal(f.view(np.uint32), seq.view(np.uint32))

@@ -56,7 +56,6 @@ _SIGNATURES = {
     "vl_moe_layer_noalloc": [_P, _P, _P],
     "vl_moe_noalloc_status": [_P, _P],
     "vl_moe_read_routes": [_P, _P, _P, _P, _P],
-    "vl_moe_set_fused": [_I32],
     "vl_timeline_create": [_U32, C.POINTER(C.c_void_p)],
     "vl_timeline_destroy": [_P],
     "vl_moe_layer_profiled": [_P, _P, _P, _U64, _P, _P, _U32],

@@ -179,11 +179,6 @@ int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes) {
     return VL_OK;
 }
 
-int vl_moe_set_fused(int enabled) {
-    vl::set_moe_fused(enabled != 0);
-    return VL_OK;
-}
-
 // Everything a layer call checks before it launches: the configuration, the pointers its routing
 // and semantics read, and the workspace size. Fills the launch arguments on success.
 static int prepare_moe(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,

@@ -15,13 +15,14 @@
 // column order (bytes 0..7 the first sub-block, 8..15 the second).
 //
 // Decode tables live in LDS. The 256- and 128-entry tables of IQ2_XXS and IQ3_XXS are held in
-// 16 copies, entry e of copy c at byte e * 256 + c * 8 (the upper half of each 256-byte row is
-// unused), and lane l reads copy l % 16: the 16 lanes an LDS cycle serves for a b64 read then
+// 16 copies, and lane l reads copy l % 16: the 16 lanes an LDS cycle serves for a b64 read then
 // touch 16 different bank pairs whatever entries they look up, which removes the bank conflicts
-// of random lookups (MI355X measures the same with 32 copies, and slower with 8). The table
+// of random lookups (MI355X measures the same with 32 copies, and slower with 8). The two tables
+// share 256-byte rows: grid entry e, copy c at byte e * 256 + c * 8 (the row's lower half) and
+// sign entry e at e * 256 + 128 + c * 8 (the upper half of rows 0..127), 64 KiB in all. The
 // address of entry e for a lane is (e << 8) | lane_off with lane_off = (l % 16) * 8, formed by
 // one v_perm_b32 when e is a byte of a payload word and by a shift and a v_and_or_b32
-// otherwise.
+// otherwise; the sign table's 128 rides in the DS instruction's immediate offset.
 //
 // LDS is addressed by plain byte addresses: the kernels that use these tables declare no static
 // LDS (the launch code checks), so their dynamic LDS starts at address 0, the tables sit at its
@@ -39,12 +40,12 @@ namespace vl {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-// LDS byte offsets of the replicated tables: B (128 entries) first, then A (256 entries), so
-// that both bases fit a DS instruction's 16-bit immediate offset.
+// LDS byte offsets of the replicated tables: A (256 grid entries) in the lower halves of 256
+// rows of 256 bytes, B (128 sign entries) in the upper halves of the first 128 rows.
 constexpr uint32_t kTabCopies = 16;
-constexpr uint32_t kTabB = 0;
-constexpr uint32_t kTabA = 128u * 256u;
-constexpr uint32_t kReplTableBytes = kTabA + 256u * 256u;  // 96 KiB
+constexpr uint32_t kTabA = 0;
+constexpr uint32_t kTabB = 128;
+constexpr uint32_t kReplTableBytes = 256u * 256u;  // 64 KiB
 constexpr uint32_t kIq1TableBytes = 2048u * 8u;            // 16 KiB, one copy
 
 __device__ __forceinline__ uint32_t lo32(uint64_t v) { return (uint32_t)v; }

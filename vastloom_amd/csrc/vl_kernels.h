@@ -14,7 +14,7 @@ namespace vl {
 constexpr uint32_t kStatusNonFiniteInput = 1u;
 constexpr uint32_t kStatusNonFiniteOutput = 2u;
 constexpr uint32_t kStatusBadRoute = 4u;
-constexpr uint32_t kStatusInternal = 8u;  // a bounded wait inside a layer kernel timed out
+constexpr uint32_t kStatusInternal = 8u;  // reserved: a bounded wait inside a layer kernel gave up
 
 // Int8 limb encoding of float activations: per token and 256-column block, x * 2^e rounded to
 // an int32 of at most 2^30 in magnitude, split into four signed base-256 digits. Stored

@@ -72,7 +72,7 @@ struct MoeWorkspace {
     uint64_t bytes;
     uint64_t off_header, off_logits, off_scores, off_keys, off_route_idx, off_route_w, off_active, off_combine,
         off_xexp, off_xflags, off_xlimbs, off_counters, off_rec_gu, off_rec_dn, off_h,
-        off_hslab, off_ypart, off_gweights, off_hlimbs, off_hscale, off_gbar, off_lgpart;
+        off_hslab, off_ypart, off_gweights, off_lgpart, off_trec;
     uint32_t grouped;                                 // more than kMoeMaxTokens tokens
     uint32_t lg_slices;                               // column slices of the grouped router product
     uint32_t max_active, slots, waves, blocks;        // slots: MFMA token slots of a job
@@ -90,9 +90,6 @@ MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base
 // Stages of one layer call, in launch order; a profiled call records an event before each
 // stage and one after the last.
 enum MoeStage : uint32_t { kStageRouter = 0, kStageGateUp, kStageDown, kStageCount };
-
-// Whether single-launch layers may be used where they apply (process-wide; default on).
-void set_moe_fused(bool enabled);
 
 // Issues the whole layer on the stream. When events is non-null it holds kStageCount + 1 events
 // recorded between the stages; when kernel_events is non-null, a start and a stop event per stage

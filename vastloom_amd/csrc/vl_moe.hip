@@ -25,31 +25,11 @@
 
 #include "vl_kernels.h"
 #include "vl_moe.h"
+#include "vl_moe_dev.h"
+#include "vl_moe_token.h"
 #include "vl_stream.h"
 
 namespace vl {
-
-struct ActiveExpert {
-    uint32_t expert;   // expert id; the shared expert is `experts`
-    uint32_t ntok;     // tokens routed to it (slots 0..ntok-1)
-    uint32_t apply_w;  // multiply h by the slot's route weight before the down projection
-    float limit;       // SwiGLU clamp (0 = none)
-    uint32_t tok[kMoeMaxTokens];
-    float route_w[kMoeMaxTokens];
-};
-
-struct MoeHeader {
-    uint32_t status;
-    uint32_t n_active;
-    uint32_t reserved[14];
-};
-
-struct CombineEntry {
-    uint32_t src;  // (active index << 3) | slot
-    float w;
-};
-
-constexpr uint32_t kMaxActive = kMoeMaxTokens * kMoeMaxTopK + 1;
 
 static inline uint64_t align256(uint64_t v) { return (v + 255u) & ~uint64_t(255); }
 
@@ -82,11 +62,6 @@ bool moe_shape_ok(const MoeShape& s) {
 static uint32_t max_active(const MoeShape& s) {
     const uint32_t routed = s.tokens * s.top_k < s.experts ? s.tokens * s.top_k : s.experts;
     return routed + (s.has_shared ? 1u : 0u);
-}
-
-// Bytes of one expert's h limbs, [inter/32][slots][4][32].
-__host__ __device__ inline uint32_t down_expert_bytes(uint32_t inter, uint32_t slots) {
-    return (inter / 32u) * slots * 128u;
 }
 
 // Router logits of grouped layers as a tiled product: kLgT tokens x kLgE experts per block,
@@ -124,8 +99,7 @@ MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base
     const uint64_t per_block = blocks ? (A * w.tiles_dn * UJ + blocks - 1u) / blocks : 1u;
     const uint64_t stage = (per_block > 0 ? per_block - 1u : 0u) / (w.tiles_dn * UJ) + 2u;
     w.stage = (uint32_t)(stage < A ? stage : A);
-    w.counters = (uint32_t)(A * w.tiles_gu + A * w.tiles_dn + w.tiles_dn + A * w.hblocks * 8u +
-                            A * w.hblocks + A);
+    w.counters = (uint32_t)(A * w.tiles_gu + A * w.tiles_dn + w.tiles_dn + A * w.hblocks * 8u);
     uint64_t o = 0;
     w.off_header = o; o = align256(o + sizeof(MoeHeader));
     w.off_logits = o; o = align256(o + T * s.experts * 4u);
@@ -145,14 +119,11 @@ MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base
     w.off_hslab = o; o = align256(o + (uint64_t)blocks * w.stage * down_expert_bytes(s.inter, w.slots));
     w.off_ypart = o; o = align256(o + A * NT * (uint64_t)s.width * 4u);
     w.off_gweights = o; o = align256(o + (w.grouped ? A * sizeof(MoeExpert) : 0u));
-    // Single-launch layers: h limbs of every active expert and their 2^-e scales.
-    w.off_hlimbs = o; o = align256(o + (w.grouped ? 0u : A * down_expert_bytes(s.inter, w.slots)));
-    w.off_hscale = o; o = align256(o + (w.grouped ? 0u : A * w.hblocks * 8u * 4u));
-    // Grid barrier words: generation, then one arrival word per block.
-    w.off_gbar = o; o = align256(o + (w.grouped ? 0u : (1u + (uint64_t)blocks) * 4u));
     // Grouped layers: f64 partial router logits of each column slice, [slice][token][expert].
     w.lg_slices = w.grouped ? router_slices(s, blocks) : 0u;
     w.off_lgpart = o; o = align256(o + (uint64_t)w.lg_slices * T * s.experts * 8u);
+    // Single-token layers: the hand-off records of jobs split between blocks.
+    w.off_trec = o; o = align256(o + tok_record_bytes(s, blocks));
     w.bytes = o;
     return w;
 }
@@ -161,65 +132,13 @@ uint64_t moe_workspace_bytes(const MoeShape& s, uint32_t blocks) {
     return moe_workspace_layout(s, blocks, nullptr).bytes;
 }
 
-template <typename T>
-__device__ __forceinline__ T* ws_ptr(const MoeWorkspace& w, uint64_t off) {
-    return reinterpret_cast<T*>(w.base + off);
-}
-
-// Counter regions (u32 words at off_counters).
-struct MoeCounters {
-    uint32_t* gu;    // [A][tiles_gu]   gate/up tile handoff
-    uint32_t* dn;    // [A][tiles_dn]   down tile handoff
-    uint32_t* tile;  // [tiles_dn]      experts done per output tile
-    uint32_t* hmax;  // [A][hblocks][8] max |h| bits per 256-row block of h and slot
-    uint32_t* hb;    // [A][hblocks]    gate/up tiles done per 256-row block of h (single launch)
-    uint32_t* ready; // [A]             256-row blocks of h converted to limbs (single launch)
-};
-
-__device__ __forceinline__ MoeCounters counters_of(const MoeWorkspace& w) {
-    MoeCounters c;
-    uint32_t* p = ws_ptr<uint32_t>(w, w.off_counters);
-    const uint32_t A = w.max_active;
-    c.gu = p;
-    c.dn = c.gu + A * w.tiles_gu;
-    c.tile = c.dn + A * w.tiles_dn;
-    c.hmax = c.tile + w.tiles_dn;
-    c.hb = c.hmax + A * w.hblocks * 8u;
-    c.ready = c.hb + A * w.hblocks;
-    return c;
-}
-
 // ------------------------------------------------------------------------------------------
 // Scores and selection keys.
 // ------------------------------------------------------------------------------------------
 
-__device__ __forceinline__ float score_of(float logit, uint32_t fn) {
-    const double p = (double)logit;
-    if (fn == kScoreSigmoid) {
-        if (p >= 0.0) return (float)(1.0 / (1.0 + exp(-p)));
-        const double q = exp(p);
-        return (float)(q / (1.0 + q));
-    }
-    const double sp = (p > 0.0 ? p : 0.0) + log1p(exp(-fabs(p)));
-    return (float)sqrt(sp);
-}
-
-// Order-preserving map of a float to uint32: a larger float gives a larger key, and every key of
-// a finite float is above 1 (non-finite keys are 1; such a token is refused anyway).
-__device__ __forceinline__ uint32_t float_key(float f) {
-    if (!isfinite(f)) return 1u;
-    const uint32_t b = __float_as_uint(f);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
 // ------------------------------------------------------------------------------------------
 // Router logits and activation limbs.
 // ------------------------------------------------------------------------------------------
-
-__device__ __forceinline__ double wave_sum_f64(double v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
 
 // Threads 0..255: the first 8 float4 of their share of expert row b (its first 8192 weights)
 // and the same columns of token t0's activations, requested together and early by the caller,
@@ -301,6 +220,9 @@ __device__ __forceinline__ void router_logit_store(const MoeShape& s, const MoeI
         score = score_of(logit, s.score_fn);
         key = float_key(score + ((s.routing == kRouteLearned && in.bias) ? *gp(in.bias + b) : 0.0f));
     }
+    // A non-finite logit refuses the token even where its score is finite (a sigmoid of +inf):
+    // its key is the refusal key 1, like a non-finite score or selection bias.
+    if (!isfinite(logit)) key = 1u;
     store_shared(ws_ptr<float>(w, w.off_logits) + i, logit);
     store_shared(ws_ptr<float>(w, w.off_scores) + i, score);
     store_shared_u32(ws_ptr<uint32_t>(w, w.off_keys) + i, key);
@@ -429,31 +351,6 @@ __global__ void __launch_bounds__(256) k_moe_router(const MoeShape s, const MoeI
 // ------------------------------------------------------------------------------------------
 // Routing (run by every gate/up block; block 0 publishes the result).
 // ------------------------------------------------------------------------------------------
-
-// Maximum over the wave, by DPP row operations (all lanes active); the result is uniform.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    // The DPP source's "old" value is 0, the identity of the maximum, so rows a step leaves out
-    // add nothing and each step folds into one v_max_u32 with a DPP operand.
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, false));   // quad [1,0,3,2]
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, false));   // quad [2,3,0,1]
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, false));  // row half mirror
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, false));  // row mirror
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));  // row bcast 15
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));  // row bcast 31
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-    // As wave_max_u32, with 0xffffffff, the identity of the minimum, as the DPP "old" value.
-    constexpr int kId = -1;
-    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0xb1, 0xf, 0xf, false));
-    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x4e, 0xf, 0xf, false));
-    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x141, 0xf, 0xf, false));
-    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x140, 0xf, 0xf, false));
-    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x142, 0xa, 0xf, false));
-    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x143, 0xc, 0xf, false));
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
 
 // Per-token selection scratch in LDS.
 struct TopKLds {
@@ -815,35 +712,6 @@ __device__ __forceinline__ void build_active(const MoeShape& s, const MoeWorkspa
 // SwiGLU.
 // ------------------------------------------------------------------------------------------
 
-__device__ __forceinline__ float silu_f(float v) {
-    // sigmoid_f / silu_f of qwen3_8_flash_next_reference.cpp:244-255, in float.
-    float sg;
-    if (v >= 0.0f) {
-        sg = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-v)));
-    } else {
-        const float z = expf(v);
-        sg = __fdiv_rn(z, __fadd_rn(1.0f, z));
-    }
-    return __fmul_rn(v, sg);
-}
-
-__device__ __forceinline__ float swiglu(uint32_t sem, float g, float u, float limit,
-                                        bool apply_w, float route_w) {
-    if (sem == kSemDeepseek) {
-        double gv = (double)g, uv = (double)u;
-        if (limit > 0.0f) {
-            const double L = (double)limit;
-            gv = gv < L ? gv : L;
-            uv = uv < -L ? -L : (uv > L ? L : uv);
-        }
-        double v = __dmul_rn(__ddiv_rn(gv, __dadd_rn(1.0, exp(-gv))), uv);
-        if (apply_w) v = __dmul_rn(v, (double)route_w);
-        return (float)v;
-    }
-    if (sem == kSemQwen) return __fmul_rn(silu_f(g), u);
-    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
-}
-
 // ------------------------------------------------------------------------------------------
 // Stream policies.
 // ------------------------------------------------------------------------------------------
@@ -893,90 +761,6 @@ __device__ __attribute__((noinline)) void gateup_fixup(const float* rec, float* 
     if (__any(bad) && lane == 0) or_bits(status, kStatusNonFiniteOutput);
 }
 
-// Single-launch layers: after tile job j's h rows are stored, the tile is counted into its 256-row
-// block of h; the last tile of a block turns the block's h into limbs (hlimbs
-// [A][inter/32][NT][4][32]) with the exponent of the block's maximum (hscale [A][hblocks][8] =
-// 2^-e) and counts the block ready for its expert.
-template <int NT>
-__device__ __attribute__((noinline)) void hblock_done(const float* h, const uint32_t* hmax,
-                                                      uint32_t* hb_cnt, uint32_t* ready, int8_t* hlimbs,
-                                                      float* hscale, uint32_t j, uint32_t tiles,
-                                                      uint32_t hblocks, uint32_t inter, uint32_t ntok) {
-    const uint32_t a = j / tiles, t = j - a * tiles, b = t / 8u;
-    const uint32_t kc = tiles - 8u * b < 8u ? tiles - 8u * b : 8u;
-    if (!arrive(hb_cnt + a * hblocks + b, kc)) return;
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t col = b * 256u + lane * 4u;
-    const uint64_t hi = (uint64_t)a * hblocks + b;
-    for (uint32_t sl = 0; sl < ntok; ++sl) {
-        const int e = limb_exponent(__uint_as_float(load_shared_u32(hmax + hi * 8u + sl)));
-        if (lane == 0) store_shared(hscale + hi * 8u + sl, __builtin_amdgcn_ldexpf(1.0f, -e));
-        if (col < inter) {
-            float v[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = load_shared(h + ((uint64_t)a * NT + sl) * inter + col + k);
-            uint32_t packed[4];
-            limbs4(v, e, packed);
-            int8_t* d = hlimbs + (uint64_t)a * down_expert_bytes(inter, NT) +
-                        ((uint64_t)(col / 32u) * NT + sl) * 128u + (col % 32u);
-#pragma unroll
-            for (int l = 0; l < 4; ++l) store_shared_u32(reinterpret_cast<uint32_t*>(d + 32u * l), packed[l]);
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // the limbs and scales are stored before the block counts
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (lane == 0) __hip_atomic_fetch_add(gp(ready + a), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Waits (agent-scope polls with short sleeps) until *p >= want; false after about a second,
-// which only a failed producer can cause.
-constexpr uint32_t kSpinLimit = 1u << 20;
-__device__ __forceinline__ bool wait_at_least(const uint32_t* p, uint32_t want) {
-    for (uint32_t i = 0; i < kSpinLimit; ++i) {
-        if (load_shared_u32(p) >= want) return true;
-        __builtin_amdgcn_s_sleep(2);
-    }
-    return false;
-}
-
-// Grid barrier of a cooperative launch that needs no cache maintenance: values that cross it are
-// stored with agent-scope stores and read with agent-scope loads. bar[0] is a generation and
-// bar[1 + b] block b's arrival word; gen is bar[0] as wave 0 of the block read it at kernel start
-// (no block changes it before every block has arrived). Block b stores gen + 1 into its word;
-// block 0 waits for all of them and then stores gen + 1 into bar[0], which the other blocks wait
-// for. Any initial contents work except every arrival word holding gen + 1 already. A wait gives
-// up after about a second, which only a grid that is not co-resident can cause, and marks the
-// call failed in *status.
-__device__ __forceinline__ void grid_barrier(uint32_t* bar, uint32_t gen, uint32_t* status) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    const uint32_t next = gen + 1u;
-    if (threadIdx.x == 0) store_shared_u32(bar + 1u + blockIdx.x, next);
-    bool ok = true;
-    if (blockIdx.x == 0) {
-        if (threadIdx.x < 64u) {
-            uint32_t i = 0;
-            for (; i < kSpinLimit; ++i) {
-                bool here = true;
-                for (uint32_t b = threadIdx.x; b < gridDim.x; b += 64u) here &= load_shared_u32(bar + 1u + b) == next;
-                if (__all(here)) break;
-                __builtin_amdgcn_s_sleep(1);
-            }
-            ok = i < kSpinLimit;
-            __builtin_amdgcn_s_waitcnt(0);
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            if (threadIdx.x == 0) store_shared_u32(bar, next);
-        }
-    } else if (threadIdx.x == 0) {
-        uint32_t i = 0;
-        for (; i < kSpinLimit && load_shared_u32(bar) != next; ++i) __builtin_amdgcn_s_sleep(1);
-        ok = i < kSpinLimit;
-    }
-    if (!ok && threadIdx.x == 0) or_bits(status, kStatusInternal);
-    __syncthreads();
-}
-
 // Gate and up projections: job j = (active expert a, tile t) = (j / tiles, j % tiles), two
 // matrices per job.
 template <uint32_t FMT, int NT, bool LDS>
@@ -997,7 +781,6 @@ struct GateUp {
     const uint8_t* const* wptr;  // [a][2] gate, up
     uint32_t ntok;
     uint32_t tok[NT];
-    bool fused;                  // single launch: convert finished 256-row blocks of h to limbs
 
     __device__ TileRef tref(uint32_t j, uint32_t mat) const {
         const uint32_t a = j / tiles, t = j - a * tiles;
@@ -1048,10 +831,6 @@ struct GateUp {
         gateup_fixup<NT>(rec, ws_ptr<float>(w, w.off_h), cn.hmax,
                          &ws_ptr<MoeHeader>(w, w.off_header)->status, j, first, last, tiles,
                          w.hblocks, s.inter, s.semantics, route_off, nullptr);
-        if (fused)
-            hblock_done<NT>(ws_ptr<const float>(w, w.off_h), cn.hmax, cn.hb, cn.ready,
-                            ws_ptr<int8_t>(w, w.off_hlimbs), ws_ptr<float>(w, w.off_hscale), j, tiles,
-                            w.hblocks, s.inter, uni(rt->act[j / tiles].ntok));
     }
 };
 
@@ -1197,7 +976,6 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_gateup(const MoeSh
     pol.wptr = wptr;
     pol.hscale = (threadIdx.x & 32u) ? 65536.0f : 1.0f;
     pol.ntok = 0;
-    pol.fused = false;
     stream_range<FMT, NT, LDS>(pol, range_begin(pol.wid, pol.NW, pol.TU),
                                range_begin(pol.wid + 1u, pol.NW, pol.TU));
 }
@@ -1279,9 +1057,6 @@ struct Down {
     const ActiveExpert* act;
     const uint8_t* const* wptr;
     uint32_t cur_a, ntok;
-    // Single launch: h limbs and scales come from global memory once the expert's blocks of h
-    // are counted ready; a wait that times out marks the call failed and is not repeated.
-    bool fused, timed_out;
 
     __device__ TileRef tref(uint32_t j, uint32_t) const {
         const uint32_t a = j / tiles, t = j - a * tiles;
@@ -1290,10 +1065,6 @@ struct Down {
 
     __device__ void job_begin(uint32_t j) {
         cur_a = j / tiles;
-        if (fused && !timed_out && !wait_at_least(counters_of(w).ready + cur_a, w.hblocks)) {
-            timed_out = true;
-            if ((threadIdx.x & 63u) == 0) or_bits(&ws_ptr<MoeHeader>(w, w.off_header)->status, kStatusInternal);
-        }
         ntok = uni(act[cur_a].ntok);
         const uint32_t m = threadIdx.x & 31u, kh = (threadIdx.x >> 5) & 1u;
         const uint32_t sl = a_slot(m), limb = a_limb(m);
@@ -1304,12 +1075,6 @@ struct Down {
 
     __device__ void scales(uint32_t, uint32_t c, float (&fs)[NT]) const {
         const uint32_t eb = FMT == VL_TYPE_Q8_0 ? c / 2u : c;
-        if (fused) {
-            const float* sc = ws_ptr<const float>(w, w.off_hscale) + ((uint64_t)cur_a * w.hblocks + eb) * 8u;
-#pragma unroll
-            for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? *gp(sc + s2) : 0.0f;
-            return;
-        }
         const uint32_t sc = scale_off + 32u * ((cur_a - a0) * w.hblocks + eb);
 #pragma unroll
         for (int s2 = 0; s2 < NT; ++s2) fs[s2] = (uint32_t)s2 < ntok ? lds_load<float>(sc + 4u * s2) : 0.0f;
@@ -1528,194 +1293,7 @@ __global__ void __launch_bounds__(stream_threads<NT>()) k_moe_down(const MoeShap
     pol.hscale = (threadIdx.x & 32u) ? 65536.0f : 1.0f;
     pol.cur_a = 0;
     pol.ntok = 0;
-    pol.fused = false;
-    pol.timed_out = false;
     stream_range<FMT, NT, LDS>(pol, range_begin(pol.wid, NW, TU), range_begin(pol.wid + 1u, NW, TU));
-}
-
-// ------------------------------------------------------------------------------------------
-// Single-launch layer (up to two tokens, gate/up and down of one storage type).
-//
-// One cooperative launch of one block per CU does the three stages of the launch sequence
-// without their launch gaps and prologues:
-//   A  router rows, activation limbs, handoff counters (grid-stride over blocks), decode tables;
-//      then one grid barrier, whose agent-scope fences publish phase A's stores
-//   R  every block routes and builds the active list (block 0 publishes routes and status)
-//   G  gate/up streaming; a tile's fixup also counts it into its 256-row block of h, and the
-//      last tile of a block converts it to limbs and counts it ready for its expert
-//   D  down streaming; a wave starting an expert's tile waits until that expert's blocks of h
-//      are ready (their producers never wait, so the wait ends) and reads the limbs from L2
-// ------------------------------------------------------------------------------------------
-
-// Dynamic LDS, from byte 0: decode tables, staged activation limbs, their 2^-e scales, per-wave
-// flags, router partial sums, routing state, gate/up and down weight pointers, combine table.
-struct FusedLds {
-    uint32_t stage, scale, flags, red, route, wptr, dptr, comb, bytes;
-};
-__host__ __device__ inline FusedLds fused_lds(uint32_t table_bytes, uint32_t stage_bytes,
-                                              uint32_t xblocks) {
-    FusedLds l;
-    l.stage = table_bytes;
-    l.scale = l.stage + stage_bytes;
-    l.flags = l.scale + xblocks * 8u * 4u;
-    l.red = (l.flags + kStreamWaves * 4u + 15u) & ~15u;
-    l.route = l.red + kMoeMaxTokens * 4u * 8u;
-    l.wptr = (l.route + (uint32_t)sizeof(RouteLds) + 15u) & ~15u;
-    l.dptr = l.wptr + kMaxActive * 2u * 8u;
-    l.comb = l.dptr + kMaxActive * 8u;
-    l.bytes = l.comb + kMoeMaxTokens * (kMoeMaxTopK + 1u) * (uint32_t)sizeof(CombineEntry);
-    return l;
-}
-
-template <uint32_t FMT, int NT>
-__global__ void __launch_bounds__(stream_threads<NT>()) k_moe_fused(const MoeShape s, const MoeInputs in,
-                                                                    const MoeWorkspace w) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    constexpr uint32_t TB = table_bytes<FMT>();
-    constexpr uint32_t WV = stream_waves<NT>();
-    static_assert(WV == 16, "phase A assigns roles to 16 waves");
-    const uint32_t stage_bytes = (s.width / 32u) * NT * 128u;
-    const FusedLds lay = fused_lds(TB, stage_bytes, w.xblocks);
-    RouteLds& rt = *reinterpret_cast<RouteLds*>(lds + lay.route);
-    double (*red)[4] = reinterpret_cast<double (*)[4]>(lds + lay.red);
-    const uint8_t** wptr = reinterpret_cast<const uint8_t**>(lds + lay.wptr);
-    const uint8_t** dptr = reinterpret_cast<const uint8_t**>(lds + lay.dptr);
-    CombineEntry* comb = reinterpret_cast<CombineEntry*>(lds + lay.comb);
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, nth = blockDim.x;
-    MoeHeader* hdr = ws_ptr<MoeHeader>(w, w.off_header);
-    uint32_t* bar = ws_ptr<uint32_t>(w, w.off_gbar);
-    const uint32_t gen = wave == 0 ? (uint32_t)__builtin_amdgcn_readfirstlane((int)load_shared_u32(bar)) : 0u;
-
-    // ---- A: waves 0..3 router rows, waves 4.. one per token x limbs, waves 8..15 tables. Every
-    // value the other blocks read later is stored at agent scope.
-    {
-        uint32_t* cnt = ws_ptr<uint32_t>(w, w.off_counters);
-        for (uint32_t i = blockIdx.x * nth + tid; i < w.counters; i += gridDim.x * nth) store_shared_u32(cnt + i, 0u);
-        if (blockIdx.x == 0 && tid < 2) store_shared_u32(&hdr->status + tid, 0u);
-    }
-    if (wave >= 8) fill_tables<FMT>(lds, tid - 512u, nth - 512u);
-    if (wave >= 4 && wave < 4u + s.tokens)
-        for (uint32_t xb = blockIdx.x; xb < w.xblocks; xb += gridDim.x)
-            prep_x_token(in.x, s.width, s.width, wave - 4u, w.xslots, w.estride, xb,
-                         ws_ptr<int8_t>(w, w.off_xlimbs), ws_ptr<int>(w, w.off_xexp),
-                         ws_ptr<uint32_t>(w, w.off_xflags));
-    if (s.routing != kRouteGiven) {
-        for (uint32_t r = blockIdx.x; r < s.experts; r += gridDim.x) {
-            if (wave < 4) {
-                RouterRow rr;
-                router_row_load(s, in, r, 0u, rr);
-                router_row_partials(s, in, r, 0u, s.tokens, red, rr);
-            }
-            __syncthreads();
-            if (tid < s.tokens) router_logit_finish(s, in, w, r, tid, red[tid]);
-            __syncthreads();
-        }
-    }
-    grid_barrier(bar, gen, &hdr->status);
-
-    // ---- R: routing (waves 0..tokens-1) while the others stage the activation limbs, all with
-    // agent-scope loads of phase A's values.
-    int nonfinite = 0;
-    if (wave < s.tokens) {
-        route_token_wave(s, in, w, wave, rt, true);
-    } else {
-        const uint32_t t0 = tid - 64u * s.tokens, nt0 = nth - 64u * s.tokens;
-        const uint32_t* src = ws_ptr<const uint32_t>(w, w.off_xlimbs);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(lds + lay.stage);
-        for (uint32_t i = t0; i < stage_bytes / 16u; i += nt0) {
-            uint32_t v[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = load_shared_u32(src + 4u * i + k);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) dst[4u * i + k] = v[k];
-        }
-        const uint32_t* xe = ws_ptr<const uint32_t>(w, w.off_xexp);
-        const uint32_t* xf = ws_ptr<const uint32_t>(w, w.off_xflags);
-        float* sc = reinterpret_cast<float*>(lds + lay.scale);
-        for (uint32_t i = t0; i < w.xblocks * 8u; i += nt0) {
-            const bool live = (i & 7u) < s.tokens;
-            sc[i] = live ? __builtin_amdgcn_ldexpf(1.0f, -(int)load_shared_u32(xe + i)) : 0.0f;
-            if (live && load_shared_u32(xf + i)) nonfinite = 1;
-        }
-    }
-    const bool any_nonfinite = block_any(nonfinite != 0, reinterpret_cast<uint32_t*>(lds + lay.flags));
-    build_active(s, w, blockIdx.x == 0, any_nonfinite, rt, comb);
-    for (uint32_t i = tid; i < rt.n_active; i += nth) {
-        const MoeExpert& ex = in.experts[rt.act[i].expert];
-        wptr[2u * i] = ex.gate;
-        wptr[2u * i + 1u] = ex.up;
-        dptr[i] = ex.down;
-    }
-    __syncthreads();
-    const uint32_t n_active = uni(rt.n_active);
-    if (n_active == 0) {
-        if (blockIdx.x == 0)
-            for (uint32_t i = tid; i < s.tokens * s.width; i += nth) *gp(in.out + i) = 0.0f;
-        return;
-    }
-
-    // ---- G
-    {
-        GateUp<FMT, NT, true> pol;
-        pol.s = s;
-        pol.in = in;
-        pol.w = w;
-        vl_make_layout(FMT, s.inter, s.width, &pol.L);
-        pol.chunks = units_per_row(FMT, s.width);
-        pol.nmat = 2;
-        pol.ng = pol.L.groups;
-        pol.tiles = w.tiles_gu;
-        pol.UJ = 2u * pol.chunks;
-        pol.TU = n_active * w.tiles_gu * pol.UJ;
-        pol.NW = active_waves(gridDim.x * WV, pol.TU);
-        pol.wid = blockIdx.x * WV + uni(wave);
-        pol.stage_off = lay.stage;
-        pol.scale_off = lay.scale;
-        pol.route_off = lay.route;
-        pol.lds = lds;
-        pol.rt = &rt;
-        pol.wptr = wptr;
-        pol.hscale = (tid & 32u) ? 65536.0f : 1.0f;
-        pol.ntok = 0;
-        pol.fused = true;
-        stream_range<FMT, NT, true>(pol, range_begin(pol.wid, pol.NW, pol.TU),
-                                    range_begin(pol.wid + 1u, pol.NW, pol.TU));
-    }
-
-    // ---- D
-    {
-        const uint32_t tiles = w.tiles_dn, UJ = units_per_row(FMT, s.inter);
-        const uint32_t TU = n_active * tiles * UJ, NW = active_waves(gridDim.x * WV, TU);
-        Down<FMT, NT, false> pol;
-        pol.s = s;
-        pol.in = in;
-        pol.w = w;
-        pol.n_active = n_active;
-        vl_make_layout(FMT, s.width, s.inter, &pol.L);
-        pol.chunks = UJ;
-        pol.nmat = 1;
-        pol.ng = pol.L.groups;
-        pol.tiles = tiles;
-        pol.UJ = UJ;
-        pol.TU = TU;
-        pol.NW = NW;
-        pol.wid = blockIdx.x * WV + uni(wave);
-        pol.a0 = 0;
-        pol.expert_bytes = down_expert_bytes(s.inter, NT);
-        pol.stage_off = 0;
-        pol.scale_off = 0;
-        pol.comb_off = lay.comb;
-        pol.slab = ws_ptr<const int8_t>(w, w.off_hlimbs);
-        pol.lds = lds;
-        pol.act = rt.act;
-        pol.wptr = dptr;
-        pol.hscale = (tid & 32u) ? 65536.0f : 1.0f;
-        pol.cur_a = 0;
-        pol.ntok = 0;
-        pol.fused = true;
-        pol.timed_out = false;
-        stream_range<FMT, NT, false>(pol, range_begin(pol.wid, NW, TU), range_begin(pol.wid + 1u, NW, TU));
-    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -2380,62 +1958,6 @@ static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, con
     return hipSuccess;
 }
 
-static bool g_fused_enabled = false;
-void set_moe_fused(bool enabled) { g_fused_enabled = enabled; }
-
-// The single-launch layer when it applies: up to two tokens, one storage type for gate/up and
-// down, its LDS within budget and one block per CU co-resident. Returns hipErrorNotSupported
-// (nothing launched) otherwise.
-template <uint32_t FMT, int NT>
-static hipError_t launch_fused_nt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
-                                  hipStream_t st) {
-    const FusedLds lay = fused_lds(table_bytes<FMT>(), (s.width / 32u) * NT * 128u, w.xblocks);
-    if (lay.bytes > kLdsBudget) return hipErrorNotSupported;
-    const void* kernel = (const void*)k_moe_fused<FMT, NT>;
-    hipError_t e = ensure_dynamic_lds(kernel, lay.bytes);
-    if (e != hipSuccess) return e;
-    int per_cu = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, stream_threads<NT>(), lay.bytes);
-    if (e != hipSuccess || per_cu < 1) return hipErrorNotSupported;
-    MoeShape sa = s;
-    MoeInputs ia = in;
-    MoeWorkspace wa = w;
-    void* args[] = {&sa, &ia, &wa};
-    e = hipLaunchCooperativeKernel(kernel, dim3(w.blocks), dim3(stream_threads<NT>()), args,
-                                   lay.bytes, st);
-    if (e != hipSuccess) {
-        (void)hipGetLastError();  // nothing was launched: the launch sequence runs instead
-        return hipErrorNotSupported;
-    }
-    return hipSuccess;
-}
-
-template <uint32_t FMT>
-static hipError_t launch_fused_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
-                                   hipStream_t st) {
-    switch (w.slots) {
-        case 1: return launch_fused_nt<FMT, 1>(s, in, w, st);
-        case 2: return launch_fused_nt<FMT, 2>(s, in, w, st);
-        default: return hipErrorNotSupported;
-    }
-}
-
-static bool fused_applies(const MoeShape& s, const MoeWorkspace& w) {
-    return g_fused_enabled && !w.grouped && s.gate_type == s.down_type;
-}
-
-static hipError_t launch_fused(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
-                               hipStream_t st) {
-    if (!fused_applies(s, w)) return hipErrorNotSupported;
-    switch (s.gate_type) {
-        case VL_TYPE_IQ2_XXS: return launch_fused_fmt<VL_TYPE_IQ2_XXS>(s, in, w, st);
-        case VL_TYPE_IQ3_XXS: return launch_fused_fmt<VL_TYPE_IQ3_XXS>(s, in, w, st);
-        case VL_TYPE_IQ1_S: return launch_fused_fmt<VL_TYPE_IQ1_S>(s, in, w, st);
-        case VL_TYPE_Q8_0: return launch_fused_fmt<VL_TYPE_Q8_0>(s, in, w, st);
-        default: return hipErrorNotSupported;
-    }
-}
-
 hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
                       hipStream_t st, hipEvent_t* ev, hipEvent_t* kev) {
     if (!moe_shape_ok(s) || w.blocks == 0) return hipErrorInvalidValue;
@@ -2448,33 +1970,19 @@ hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace
         if (ev) rec(ev[stage]);
     };
     mark(kStageRouter);
-    if (fused_applies(s, w)) {
-        // One cooperative launch: its time is reported as the gate/up stage (and kernel), the
-        // others as empty.
-        if (kev) {
-            rec(ke[kStageRouter].start);
-            rec(ke[kStageRouter].stop);
-            rec(ke[kStageGateUp].start);
-        }
-        mark(kStageGateUp);
-        const hipError_t fe = launch_fused(s, in, w, st);
-        if (fe != hipSuccess && fe != hipErrorNotSupported) return fe;
-        if (fe == hipSuccess) {
-            if (kev) {
-                rec(ke[kStageGateUp].stop);
-                rec(ke[kStageDown].start);
-                rec(ke[kStageDown].stop);
-            }
-            mark(kStageDown);
-            mark(kStageCount);
-            return hipSuccess;
-        }
-    }
     const uint32_t router_blocks = (s.routing == kRouteGiven ? 0u : s.experts) + w.xblocks;
     hipError_t e = launch_timed(kev ? &ke[kStageRouter] : nullptr, k_moe_router, dim3(router_blocks),
                                 dim3(256), 0u, st, s, in, w);
     if (e != hipSuccess) return e;
     mark(kStageGateUp);
+    if (tok_applies(s, w.blocks)) {
+        e = launch_tok_gateup(s, in, w, st, kev ? kev + 2u * kStageGateUp : nullptr);
+        if (e != hipSuccess) return e;
+        mark(kStageDown);
+        e = launch_tok_down(s, in, w, st, kev ? kev + 2u * kStageDown : nullptr);
+        mark(kStageCount);
+        return e;
+    }
     const KernelEvents* kg = kev ? &ke[kStageGateUp] : nullptr;
     switch (s.gate_type) {
         case VL_TYPE_IQ2_XXS: e = launch_gateup_fmt<VL_TYPE_IQ2_XXS>(s, in, w, st, kg); break;

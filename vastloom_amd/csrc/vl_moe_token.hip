@@ -126,12 +126,12 @@ TokPlan tok_plan_down(const MoeShape& s, uint32_t blocks) {
 }
 
 // LDS of the gate/up kernel, from byte 0: decode tables, the token's limbs, its 2^-e per 256
-// columns, chunk partials, counters and flags, the routing, the active list, combine entries,
-// weight pointers of the active experts.
+// columns, chunk partials, counters and flags, the active list, combine entries, weight pointers
+// of the active experts.
 constexpr uint32_t kTokPtrTab = 256;
 constexpr uint32_t kTokRareBytes = 256;  // TokRare, rounded up
 struct TokGuLds {
-    uint32_t xstage, xscale, part, desc, misc, sel, act, comb, wptr, rare, bytes;
+    uint32_t xstage, xscale, part, desc, misc, act, comb, wptr, rare, bytes;
 };
 // misc words
 // misc words: the chunk counter, chunks done per segment of the S and R pieces, the chunks each
@@ -147,8 +147,7 @@ __host__ __device__ inline TokGuLds tok_lds_gu(uint32_t table_bytes, uint32_t wi
     l.part = (l.xscale + ((width + 255u) / 256u) * 4u + 15u) & ~15u;
     l.desc = l.part + max_chunks * 256u;
     l.misc = l.desc + max_chunks * 8u;
-    l.sel = l.misc + kMiscWords * 4u;
-    l.act = (l.sel + kMoeMaxTopK * 8u + 15u) & ~15u;
+    l.act = (l.misc + kMiscWords * 4u + 15u) & ~15u;
     l.comb = l.act + kTokMaxActive * (uint32_t)sizeof(ActiveExpert);
     l.wptr = (l.comb + (kMoeMaxTopK + 1u) * (uint32_t)sizeof(CombineEntry) + 15u) & ~15u;
     l.rare = l.wptr + kTokMaxActive * 16u;
@@ -202,6 +201,8 @@ bool tok_applies(const MoeShape& s, uint32_t blocks) {
     if (cg % tok_chunk_units(s.gate_type) || cd % tok_chunk_units(s.down_type)) return false;
     const TokPlan g = tok_plan_gateup(s, blocks), d = tok_plan_down(s, blocks);
     if (!segments_fit(g.S, g.UJ) || !segments_fit(g.R, g.UJ) || !segments_fit(d.R, d.UJ)) return false;
+    // The data-parallel finishes keep their sums where the activations were staged.
+    if (2ull * g.q * 256u > 4ull * s.width || (uint64_t)d.q * A * 256u > 4ull * A * s.inter) return false;
     if (tok_lds_gu(tab_bytes(s.gate_type), s.width, g.max_chunks).bytes > kLdsLimit) return false;
     if (tok_lds_dn(tab_bytes(s.down_type), A, s.inter, d.max_chunks).bytes > kLdsLimit) return false;
     return true;
@@ -654,80 +655,96 @@ __device__ __forceinline__ void load_keys(const MoeWorkspace& w, uint32_t E, boo
     }
 }
 
-// Learned and softmax routing of the token by wave 0, from every expert's key and score in
-// registers (lane l of register i: expert l + 64 i): the K largest keys, ties to the lower id, in
-// rank order, then their weights with the reference's float64 arithmetic. Returns the refusal; sel
-// then holds ids [K] and weights [K]. A key of 1 or less marks a non-finite logit, score or
-// selection bias, which refuses the token (activate_gate_logits and require_finite,
-// deepseek_v4_reference.cpp:155-165, :236-239; qwen38_moe_route's logits).
+// The route of the token in wave 0: lane k < K holds the expert of rank k and its weight.
+struct TokRoute {
+    uint32_t id;
+    float wt;
+    bool bad;  // the token is refused (wave-uniform)
+};
+
+// Learned and softmax routing of the token by wave 0 (every lane active), from every expert's key
+// and score in registers (lane l of register i: expert l + 64 i): the K largest keys, ties to the
+// lower id, in rank order, then their weights with the reference's float64 arithmetic. A key of 1
+// or less marks a non-finite logit, score or selection bias, which refuses the token
+// (activate_gate_logits and require_finite, deepseek_v4_reference.cpp:155-165, :236-239;
+// qwen38_moe_route's logits).
 //
-// Selection: T, the K-th largest of the 64 lane maxima, bounds the K-th largest key from below (at
-// least K keys are >= T), so only keys >= T can be selected or beat a selected key. The rank of a
-// key >= T counts the keys >= T above it and the equal ones of lower ids.
+// Selection: each lane first orders its own experts by key, descending (a stable sort, so equal
+// keys keep ascending ids); round k then takes the largest head of the wave, ties to the lowest id,
+// and its lane moves on to its next expert.
 template <int PER>
-__device__ bool route_select(const MoeShape& s, const uint32_t (&key)[PER], const float (&score)[PER],
-                             uint32_t sel) {
+__device__ TokRoute route_select(const MoeShape& s, const uint32_t (&key0)[PER], const float (&score)[PER]) {
     const uint32_t lane = threadIdx.x & 63u, K = s.top_k, E = s.experts;
     const bool softmax = s.routing == kRouteSoftmax;
-    bool bad = false;
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-        if (lane + 64u * i < E) {
-            bad |= key[i] <= 1u;
-            m = key[i] > m ? key[i] : m;
-        }
-    uint32_t cm = 0;
-    for (uint32_t j = 0; j < 64u; ++j) {
-        const uint32_t mj = (uint32_t)__builtin_amdgcn_readlane((int)m, j);
-        cm += (mj > m || (mj == m && j < lane)) ? 1u : 0u;
-    }
-    // The ranks cm of the lanes are a permutation of 0..63, so exactly one lane has rank K - 1.
-    const uint32_t T = (uint32_t)__builtin_amdgcn_readlane((int)m, __builtin_ctzll(__ballot(cm == K - 1u)));
-    uint32_t cnt[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) cnt[i] = 0;
-#pragma unroll
-    for (int r = 0; r < PER; ++r) {
-        uint64_t mask = __ballot(lane + 64u * r < E && key[r] >= T);
-        while (mask) {
-            const uint32_t l = (uint32_t)__builtin_ctzll(mask);
-            mask &= mask - 1u;
-            const uint32_t kc = (uint32_t)__builtin_amdgcn_readlane((int)key[r], l);
-#pragma unroll
-            for (int i = 0; i < PER; ++i) {
-                const bool lower = r < i || (r == i && l < lane);
-                cnt[i] += (kc > key[i] || (kc == key[i] && lower)) ? 1u : 0u;
-            }
-        }
-    }
+    uint32_t key[PER], hid[PER];
     float val[PER];
+    bool bad = false;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const uint32_t e = lane + 64u * i;
-        val[i] = softmax ? (key[i] > 1u ? key_float(key[i]) : 0.0f) : score[i];
-        if (e < E && key[i] >= T && cnt[i] < K) {
-            lds_st_u32(sel + 4u * cnt[i], e);
-            lds_st_f32(sel + 4u * (kMoeMaxTopK + cnt[i]), val[i]);
-        }
+        const bool live = e < E;
+        bad |= live && key0[i] <= 1u;
+        key[i] = live ? key0[i] : 0u;
+        hid[i] = e;
+        val[i] = softmax ? (key0[i] > 1u ? key_float(key0[i]) : 0.0f) : score[i];
     }
-    const float vk = lane < K ? lds_f32(sel + 4u * (kMoeMaxTopK + lane)) : 0.0f;
+#pragma unroll
+    for (int i = 1; i < PER; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j) {
+            const bool up = key[j] > key[j - 1];
+            const uint32_t k0 = key[j - 1], h0 = hid[j - 1];
+            const float v0 = val[j - 1];
+            key[j - 1] = up ? key[j] : k0;
+            hid[j - 1] = up ? hid[j] : h0;
+            val[j - 1] = up ? val[j] : v0;
+            key[j] = up ? k0 : key[j];
+            hid[j] = up ? h0 : hid[j];
+            val[j] = up ? v0 : val[j];
+        }
+    uint32_t id = 0;
+    float vk = 0.0f, v_first = 0.0f;
+    double sum = 0.0;  // the selected values in rank order
+    for (uint32_t k = 0; k < K; ++k) {
+        const uint32_t m = wave_max_u32(key[0]);
+        const bool top = key[0] == m;
+        const uint64_t hit = __ballot(top);
+        uint32_t wl = (uint32_t)__builtin_ctzll(hit);
+        if (hit & (hit - 1u)) {
+            const uint32_t mid = wave_min_u32(top ? hid[0] : 0xffffffffu);
+            wl = (uint32_t)__builtin_ctzll(__ballot(top && hid[0] == mid));
+        }
+        const uint32_t wid = (uint32_t)__builtin_amdgcn_readlane((int)hid[0], wl);
+        const float wv = readlane_f32(val[0], wl);
+        if (lane == k) {
+            id = wid;
+            vk = wv;
+        }
+        if (k == 0) v_first = wv;
+        sum += (double)wv;
+        const bool me = lane == wl;
+#pragma unroll
+        for (int i = 0; i + 1 < PER; ++i) {
+            key[i] = me ? key[i + 1] : key[i];
+            hid[i] = me ? hid[i + 1] : hid[i];
+            val[i] = me ? val[i + 1] : val[i];
+        }
+        key[PER - 1] = me ? 0u : key[PER - 1];
+    }
     float wk = 0.0f;
     if (!softmax) {
         // Selected scores over their float64 sum in rank order, times route_scale
         // (route_from_indices, deepseek_v4_reference.cpp:80-121).
-        double sum = 0.0;
-        for (uint32_t k = 0; k < K; ++k) sum += (double)readlane_f32(vk, k);
         bad |= !(sum > 0.0) || isinf(sum);
         wk = (float)((double)vk / sum * (double)s.route_scale);
     } else {
         // float64 softmax over every logit, the top-k probabilities, optional renormalisation
         // (qwen38_moe_route, qwen3_8_flash_next_reference.cpp:1186-1240).
-        const double mx = (double)readlane_f32(vk, 0);
+        const double mx = (double)v_first;
         double all = 0.0;
 #pragma unroll
         for (int i = 0; i < PER; ++i)
-            if (lane + 64u * i < E) all += exp((double)val[i] - mx);
+            if (lane + 64u * i < E) all += exp((double)(key0[i] > 1u ? key_float(key0[i]) : 0.0f) - mx);
         all = wave_sum_f64(all);
         const double pk = exp((double)vk - mx) * (all > 0.0 ? 1.0 / all : 0.0);
         double selsum = 0.0;
@@ -735,13 +752,12 @@ __device__ bool route_select(const MoeShape& s, const uint32_t (&key)[PER], cons
         wk = (float)pk;
         if (s.renormalize && selsum > 0.0) wk = (float)((double)wk * (1.0 / selsum));
     }
-    if (lane < K) lds_st_f32(sel + 4u * (kMoeMaxTopK + lane), wk);
-    return __any(bad);
+    return TokRoute{lane < K ? id : 0u, lane < K ? wk : 0.0f, __any(bad) != 0};
 }
 
-// Table and given routing of the token by wave 0: ids and weights into sel. An id out of range
-// or repeated, any non-finite logit (table) and weights that cannot be normalised refuse the token.
-__device__ bool route_listed(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w, uint32_t sel) {
+// Table and given routing of the token by wave 0. An id out of range or repeated, any non-finite
+// logit (table) and weights that cannot be normalised refuse the token.
+__device__ TokRoute route_listed(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w) {
     const uint32_t lane = threadIdx.x & 63u, K = s.top_k, E = s.experts;
     bool bad = false;
     uint32_t id = 0;
@@ -766,21 +782,18 @@ __device__ bool route_listed(const MoeShape& s, const MoeInputs& in, const MoeWo
     } else if (lane < K && in.given_weights) {
         wk = *gp(in.given_weights + lane);
     }
-    if (lane < K) {
-        lds_st_u32(sel + 4u * lane, id);
-        lds_st_f32(sel + 4u * (kMoeMaxTopK + lane), wk);
-    }
-    return __any(bad);
+    return TokRoute{id, lane < K ? wk : 0.0f, __any(bad) != 0};
 }
 
 // Wave 0, after routing: the active list (routed experts in ascending id, then the shared
 // expert), the combine entries, and their publication by block 0. Returns the position in the
 // active list of the expert of rank `lane` (lanes < K).
-__device__ uint32_t tok_active(const MoeShape& s, const MoeWorkspace& w, uint32_t sel, uint32_t act,
-                               uint32_t comb, bool bad, bool publish) {
+__device__ uint32_t tok_active(const MoeShape& s, const MoeWorkspace& w, const TokRoute& rt, uint32_t act,
+                               uint32_t comb, bool publish) {
     const uint32_t lane = threadIdx.x & 63u, K = s.top_k, E = s.experts;
-    const uint32_t id = lane < K ? lds_u32(sel + 4u * lane) : 0u;
-    const float wt = lane < K ? lds_f32(sel + 4u * (kMoeMaxTopK + lane)) : 0.0f;
+    const uint32_t id = rt.id;
+    const float wt = rt.wt;
+    const bool bad = rt.bad;
     uint32_t a = 0;
     for (uint32_t k = 0; k < K; ++k) a += (uint32_t)__builtin_amdgcn_readlane((int)id, k) < id ? 1u : 0u;
     VL_LDS ActiveExpert* A = lptr<ActiveExpert>(act);
@@ -982,11 +995,12 @@ struct GuCtx {
 // The block's chunk table and the chunk count of each stream-K segment of its pieces, into LDS.
 template <uint32_t CU>
 __device__ __forceinline__ void fill_work(const TokPlan p, uint32_t b, const TokPiece ps, const TokPiece pr,
-                                          uint32_t nchunks, uint32_t desc, uint32_t misc, bool gate_up) {
-    for (uint32_t k = threadIdx.x; k < nchunks; k += blockDim.x)
+                                          uint32_t nchunks, uint32_t desc, uint32_t misc, bool gate_up,
+                                          uint32_t t, uint32_t nt) {
+    for (uint32_t k = t; k < nchunks; k += nt)
         *lptr<u32x2>(desc + 8u * k) = encode_work(tok_chunk<CU>(p, b, ps, pr, k), p.tiles, p.C, gate_up);
-    if (threadIdx.x < 2u * kTokMaxSeg) {
-        const uint32_t r = threadIdx.x / kTokMaxSeg, sg = threadIdx.x % kTokMaxSeg;
+    if (t < 2u * kTokMaxSeg) {
+        const uint32_t r = t / kTokMaxSeg, sg = t % kTokMaxSeg;
         TokPiece P;  // field by field: a per-lane choice of struct would be made through memory
         P.lo = r == 0 ? ps.lo : pr.lo;
         P.hi = r == 0 ? ps.hi : pr.hi;
@@ -994,7 +1008,7 @@ __device__ __forceinline__ void fill_work(const TokPlan p, uint32_t b, const Tok
         P.c0 = r == 0 ? ps.c0 : pr.c0;
         uint32_t first = 0, n = 0;
         if (P.hi > P.lo && sg <= (P.hi - 1u) / p.UJ - P.lo / p.UJ) seg_chunks<CU>(p, P, sg, first, n);
-        lds_st_u32(misc + 4u * (kMiscSegN + threadIdx.x), n);
+        lds_st_u32(misc + 4u * (kMiscSegN + t), n);
     }
 }
 
@@ -1019,32 +1033,36 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
     ctx.wptr = lay.wptr;
     const uint32_t nS = ps.n, nstatic = nS < nw ? nS : nw;
 
-    // 1. Requests, all before the first LDS store: decode tables, the token's limbs, exponents and
-    //    flags, every expert's gate/up pointers, then the shared expert's pointers and this wave's
+    // Wave 0 routes the token; waves 1.. (the helpers, thread h of nh) stage everything else.
+    const bool helper = wave != 0;
+    const uint32_t h = tid - 64u, nh = blockDim.x - 64u;
+
+    // 1. Requests, all before the first LDS store: wave 0's routing keys; the helpers' decode
+    //    tables, token limbs, exponents and flags, the shared expert's pointers; then each wave's
     //    first chunk of the shared expert.
+    const bool ranked = s.routing == kRouteLearned || s.routing == kRouteSoftmax;
+    uint32_t key[PER];
+    float score[PER];
+    if (ranked && !helper) load_keys<PER>(w, E, s.routing == kRouteLearned, key, score);
     TableFill<FMT> tf;
-    const bool one = TableFill<FMT>::single(blockDim.x);
-    if (one) tf.load(tid, blockDim.x);
+    const bool one = TableFill<FMT>::single(nh);
+    if (helper && one) tf.load(h, nh);
     const uint32_t xn = (s.width / 32u) * 128u / 16u;  // 16-byte words of the token's limbs
     const uint4* xsrc = ws_ptr<const uint4>(w, w.off_xlimbs);
     constexpr uint32_t XB = 2;
     uint4 xv[XB];
 #pragma unroll
     for (uint32_t j = 0; j < XB; ++j)
-        if (tid + j * blockDim.x < xn) xv[j] = ld_u4(xsrc + tid + j * blockDim.x);
+        if (helper && h + j * nh < xn) xv[j] = ld_u4(xsrc + h + j * nh);
     int ev = 0;
     uint32_t fv = 0;
-    if (tid < w.xblocks) {
-        ev = *gp(ws_ptr<const int>(w, w.off_xexp) + (uint64_t)w.estride * tid);
-        fv = *gp(ws_ptr<const uint32_t>(w, w.off_xflags) + (uint64_t)w.estride * tid);
+    if (helper && h < w.xblocks) {
+        ev = *gp(ws_ptr<const int>(w, w.off_xexp) + (uint64_t)w.estride * h);
+        fv = *gp(ws_ptr<const uint32_t>(w, w.off_xflags) + (uint64_t)w.estride * h);
     }
     const bool shared = s.has_shared != 0;
     uint64_t shp = 0;
-    if (tid < 2u && shared) shp = reinterpret_cast<uint64_t>(tid ? in.experts[E].up : in.experts[E].gate);
-    const bool ranked = s.routing == kRouteLearned || s.routing == kRouteSoftmax;
-    uint32_t key[PER];
-    float score[PER];
-    if (ranked) load_keys<PER>(w, E, s.routing == kRouteLearned, key, score);
+    if (helper && h < 2u && shared) shp = reinterpret_cast<uint64_t>(h ? in.experts[E].up : in.experts[E].gate);
     Chunk bufA[CU];
     TokWork ca{0, 0, 0, 0, 0, 2, 0};
     const uint32_t ka = wave;
@@ -1056,58 +1074,62 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
         for (uint32_t i = 0; i < CU; ++i)
             tok_load<FMT>(i < ca.count ? tr : idle_tile(), i < ca.count ? ca.col + i : 0u, ctx.ng, bufA[i]);
     }
-    // 2. LDS stores.
-    if (one) tf.store(lds_base(), tid, blockDim.x);
-    else fill_tables<FMT>(lds_base());
-    uint4* xdst = reinterpret_cast<uint4*>(lds_base() + lay.xstage);
-#pragma unroll
-    for (uint32_t j = 0; j < XB; ++j)
-        if (tid + j * blockDim.x < xn) xdst[tid + j * blockDim.x] = xv[j];
-    for (uint32_t i = tid + XB * blockDim.x; i < xn; i += blockDim.x) xdst[i] = ld_u4(xsrc + i);
-    if (tid < w.xblocks) lds_st_f32(lay.xscale + 4u * tid, __builtin_amdgcn_ldexpf(1.0f, -ev));
-    if (tid < 2u && shared) *lptr<uint64_t>(lay.wptr + 16u * K + 8u * tid) = shp;
-    if (tid < kMiscSegN) lds_st_u32(lay.misc + 4u * tid, tid == kMiscGrab ? nstatic : 0u);
-    const bool xflag = __any(tid < w.xblocks && fv != 0u);
-    if (lane == 0) lds_st_u32(lay.misc + 4u * (kMiscWaveFlags + wave), xflag ? 1u : 0u);
-    fill_work<CU>(p, b, ps, pr, ctx.nchunks, lay.desc, lay.misc, true);
-    if (tid == 0) {
-        TokRare r;
-        r.p = p;
-        r.ps = ps;
-        r.pr = pr;
-        r.b = b;
-        r.act = lay.act;
-        r.comb = lay.comb;
-        r.inter = s.inter;
-        r.hblocks = w.hblocks;
-        r.semantics = s.semantics;
-        r.K = K;
-        r.has_shared = s.has_shared;
-        r.width = s.width;
-        r.h = ws_ptr<float>(w, w.off_h);
-        r.hmax = counters_of(w).hmax;
-        r.status = &ws_ptr<MoeHeader>(w, w.off_header)->status;
-        r.counters = counters_of(w).gu;
-        r.rec = ws_ptr<float>(w, w.off_trec);
-        r.out = in.out;
-        lds_put(lay.rare, r);
-    }
-    // 3. Routing by wave 0, while the other waves' stores complete: the selection and its weights,
-    //    the routed experts' pointers (requested as soon as their ids are known), the active list.
-    if (wave == 0) {
-        const bool bad = ranked ? route_select<PER>(s, key, score, lay.sel) : route_listed(s, in, w, lay.sel);
-        const uint32_t id = lane < K ? lds_u32(lay.sel + 4u * lane) : 0u;
+    if (!helper) {
+        // 2. Routing: the selection and its weights, the routed experts' pointers (requested as
+        //    soon as their ids are known), the active list.
+        const TokRoute rt = ranked ? route_select<PER>(s, key, score) : route_listed(s, in, w);
+        const bool bad = rt.bad;
         uint64_t pg = 0, pu = 0;
         if (lane < K && !bad) {
-            pg = reinterpret_cast<uint64_t>(in.experts[id].gate);
-            pu = reinterpret_cast<uint64_t>(in.experts[id].up);
+            pg = reinterpret_cast<uint64_t>(in.experts[rt.id].gate);
+            pu = reinterpret_cast<uint64_t>(in.experts[rt.id].up);
         }
-        const uint32_t a = tok_active(s, w, lay.sel, lay.act, lay.comb, bad, b == 0);
+        const uint32_t a = tok_active(s, w, rt, lay.act, lay.comb, b == 0);
         if (lane < K) {
             *lptr<uint64_t>(lay.wptr + 16u * a) = pg;
             *lptr<uint64_t>(lay.wptr + 16u * a + 8u) = pu;
         }
-        if (lane == 0) lds_st_u32(lay.misc + 4u * kMiscBad, bad ? 1u : 0u);
+        if (lane == 0) {
+            lds_st_u32(lay.misc + 4u * kMiscBad, bad ? 1u : 0u);
+            lds_st_u32(lay.misc + 4u * kMiscWaveFlags, 0u);
+        }
+    } else {
+        // 3. The helpers' LDS stores.
+        if (one) tf.store(lds_base(), h, nh);
+        else fill_tables<FMT>(lds_base(), h, nh);
+        uint4* xdst = reinterpret_cast<uint4*>(lds_base() + lay.xstage);
+#pragma unroll
+        for (uint32_t j = 0; j < XB; ++j)
+            if (h + j * nh < xn) xdst[h + j * nh] = xv[j];
+        for (uint32_t i = h + XB * nh; i < xn; i += nh) xdst[i] = ld_u4(xsrc + i);
+        if (h < w.xblocks) lds_st_f32(lay.xscale + 4u * h, __builtin_amdgcn_ldexpf(1.0f, -ev));
+        if (h < 2u && shared) *lptr<uint64_t>(lay.wptr + 16u * K + 8u * h) = shp;
+        if (h < kMiscSegN) lds_st_u32(lay.misc + 4u * h, h == kMiscGrab ? nstatic : 0u);
+        const bool xflag = __any(h < w.xblocks && fv != 0u);
+        if (lane == 0) lds_st_u32(lay.misc + 4u * (kMiscWaveFlags + wave), xflag ? 1u : 0u);
+        fill_work<CU>(p, b, ps, pr, ctx.nchunks, lay.desc, lay.misc, true, h, nh);
+        if (h == 0) {
+            TokRare r;
+            r.p = p;
+            r.ps = ps;
+            r.pr = pr;
+            r.b = b;
+            r.act = lay.act;
+            r.comb = lay.comb;
+            r.inter = s.inter;
+            r.hblocks = w.hblocks;
+            r.semantics = s.semantics;
+            r.K = K;
+            r.has_shared = s.has_shared;
+            r.width = s.width;
+            r.h = ws_ptr<float>(w, w.off_h);
+            r.hmax = counters_of(w).hmax;
+            r.status = &ws_ptr<MoeHeader>(w, w.off_header)->status;
+            r.counters = counters_of(w).gu;
+            r.rec = ws_ptr<float>(w, w.off_trec);
+            r.out = in.out;
+            lds_put(lay.rare, r);
+        }
     }
     __syncthreads();
     if (b == 0 && tid == 0) {
@@ -1119,12 +1141,16 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
     // 4. Stream: this wave's chunk of the shared expert, then chunks from the counter.
     tok_stream<FMT, CU>(ctx, ka, ca, bufA);
     __syncthreads();
-    // 5. Data-parallel jobs: a wave per job adds the job's chunks in order and finishes it.
+    // 5. Data-parallel jobs: the sums of each job's gate and of its up chunks in chunk order, a wave
+    //    per matrix (into the token's limb area, no longer read), then a wave per job finishes it.
     const TokRare r = lds_get<TokRare>(lay.rare);
     const uint32_t nd0 = r.ps.n + r.pr.n, cpm = r.p.C / CU;
+    for (uint32_t m = wave; m < 2u * r.p.q; m += nw)
+        lds_st_f32(lay.xstage + m * 256u + lane * 4u, sum_parts(lay.part, nd0 + m * cpm, cpm));
+    __syncthreads();
     for (uint32_t jj = wave; jj < r.p.q; jj += nw) {
-        const uint32_t k0 = nd0 + jj * (r.p.UJ / CU);
-        const float g = sum_parts(lay.part, k0, cpm), u = sum_parts(lay.part, k0 + cpm, cpm);
+        const float g = lds_f32(lay.xstage + 2u * jj * 256u + lane * 4u);
+        const float u = lds_f32(lay.xstage + (2u * jj + 1u) * 256u + lane * 4u);
         const uint32_t job = r.b * r.p.q + jj, a = job / r.p.tiles, t = job - a * r.p.tiles;
         const VL_LDS ActiveExpert* ae = lptr<ActiveExpert>(r.act) + a;
         gu_finish(g, u, a, t, r.inter, r.hblocks, r.semantics, ae->limit, ae->apply_w, ae->route_w[0], r.h, r.hmax,
@@ -1136,29 +1162,36 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
 // Down.
 // ------------------------------------------------------------------------------------------
 
-// Output rows t*32 + n (n = lane < 32) of the token: the active experts' rows added in the combine
-// order. Expert a's per-lane sum (lane n + 32 holds the high limbs' share) is, with records null,
-// the n LDS chunk partials from k0 + a*n on; otherwise the sum over blocks fb..lb of their records'
-// rows a (record of block bb: rec + ((bb * kTokMaxSeg + seg(bb)) * A + a) * 64).
-__device__ __attribute__((noinline)) void dn_finish(uint32_t t, uint32_t part, uint32_t k0, uint32_t n,
-                                                    const float* rec, uint32_t fb, uint32_t lb, uint32_t job0,
+// Output rows t*32 + n (n = lane < 32) of a stream-K tile: each active expert's rows (lane n + 32
+// holding the high limbs' share) summed over the records of the contributing blocks fb..lb in block
+// order (record of block bb: rec + ((bb * kTokMaxSeg + seg(bb)) * A + a) * 64), then added in the
+// combine order.
+// Combine entry k's sum y of an output row into acc: Qwen weighs the routed experts' rows by their
+// route weights, DeepSeek adds them as they are (the weights were applied to h).
+__device__ __forceinline__ float dn_combine(float acc, float y, uint32_t k, uint32_t K, uint32_t semantics,
+                                            const VL_LDS CombineEntry* C) {
+    return (semantics == kSemQwen && k < K) ? __fadd_rn(acc, __fmul_rn(y, C[k].w)) : __fadd_rn(acc, y);
+}
+
+// Output rows t*32 + lane (lanes < 32) and the non-finite output flag.
+__device__ __forceinline__ void dn_store(uint32_t t, float acc, uint32_t width, float* out, uint32_t* status) {
+    const uint32_t lane = threadIdx.x & 63u, row = t * 32u + (lane & 31u);
+    const bool live = lane < 32u && row < width;
+    if (live) *gp(out + row) = acc;
+    if (__any(live && !isfinite(acc)) && lane == 0) or_bits(status, kStatusNonFiniteOutput);
+}
+
+__device__ __attribute__((noinline)) void dn_finish(uint32_t t, const float* rec, uint32_t fb, uint32_t lb,
+                                                    uint32_t job0,
                                                     uint32_t total, uint32_t blocks, uint32_t UJ, uint32_t A,
                                                     uint32_t comb, uint32_t K, uint32_t has_shared,
                                                     uint32_t semantics, uint32_t width, float* out, uint32_t* status) {
-    const uint32_t lane = threadIdx.x & 63u, row = t * 32u + (lane & 31u);
+    const uint32_t lane = threadIdx.x & 63u;
     const VL_LDS CombineEntry* C = lptr<CombineEntry>(comb);
     const uint32_t nent = K + (has_shared ? 1u : 0u);
     float acc = 0.0f;
-    auto combine = [&](float v, uint32_t k) {
-        const float y = v + __shfl_xor(v, 32);
-        acc = (semantics == kSemQwen && k < K) ? __fadd_rn(acc, __fmul_rn(y, C[k].w)) : __fadd_rn(acc, y);
-    };
-    if (!rec) {
-        for (uint32_t k = 0; k < nent; ++k) {
-            const uint32_t a = C[k].src >> 3;
-            combine(sum_parts(part, k0 + a * n, n), k);
-        }
-    } else {
+    auto combine = [&](float v, uint32_t k) { acc = dn_combine(acc, v + __shfl_xor(v, 32), k, K, semantics, C); };
+    {
         // Pairs (entry k, contributor bb) in order, k-major: each entry's records added in block
         // order, then combined; the loads of B pairs in flight at once.
         constexpr uint32_t B = 16;
@@ -1194,9 +1227,7 @@ __device__ __attribute__((noinline)) void dn_finish(uint32_t t, uint32_t part, u
                 }
         }
     }
-    const bool live = lane < 32u && row < width;
-    if (live) *gp(out + row) = acc;
-    if (__any(live && !isfinite(acc)) && lane == 0) or_bits(status, kStatusNonFiniteOutput);
+    dn_store(t, acc, width, out, status);
 }
 
 // The last chunk of a stream-K segment of a down block is done: the segment's chunks k0 .. k0+n-1 of
@@ -1229,7 +1260,7 @@ __device__ __attribute__((noinline)) void dn_segment(uint32_t part, uint32_t k0,
     const TokRegion X{total, blocks, job0};
     const uint32_t lo = (t - job0) * UJ, fb = tok_block_of(X, lo), lb = tok_block_of(X, lo + UJ - 1u);
     if (!arrive(counters + t, lb - fb + 1u)) return;
-    dn_finish(t, 0u, 0u, 0u, rec, fb, lb, job0, total, blocks, UJ, A, comb, K, has_shared, semantics, width, out, status);
+    dn_finish(t, rec, fb, lb, job0, total, blocks, UJ, A, comb, K, has_shared, semantics, width, out, status);
 }
 
 template <uint32_t FMT>
@@ -1287,7 +1318,7 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     constexpr uint32_t TB = table_bytes<FMT>(), CU = tok_chunk_units(FMT);
     const uint32_t A = p.A, F = s.inter, K = s.top_k, E = s.experts, HB = w.hblocks;
     const TokDnLds lay = tok_lds_dn(TB, A, F, p.max_chunks);
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nw = blockDim.x >> 6;
     const uint32_t b = blockIdx.x;
     const TokPiece ps = tok_piece(p.S, b, CU), pr = tok_piece(p.R, b, CU);
     DnCtx<FMT> ctx;
@@ -1338,7 +1369,7 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     if (tid < pn) *lptr<uint64_t>(lay.ptab + 8u * tid) = pv;
     if (tid < 2u * (K + 1u)) lds_st_u32(lay.comb + 4u * tid, cw);
     if (tid < kMiscSegN) lds_st_u32(lay.misc + 4u * tid, tid == kMiscGrab ? nw : 0u);
-    fill_work<CU>(p, b, ps, pr, ctx.nchunks, lay.desc, lay.misc, false);
+    fill_work<CU>(p, b, ps, pr, ctx.nchunks, lay.desc, lay.misc, false, tid, blockDim.x);
     if (tid == 0) {
         TokRare r;
         r.p = p;
@@ -1412,12 +1443,23 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     // 4. Stream.
     tok_stream<FMT, CU>(ctx, ka, ca, bufA);
     __syncthreads();
-    // 5. Data-parallel tiles: per tile, each expert's chunks in order, then the combine.
+    // 5. Data-parallel tiles: each (tile, combine entry)'s expert sum over its chunks in order, a
+    //    wave per pair (into the h limb area, no longer read), then a wave per tile combines.
     const TokRare r = lds_get<TokRare>(lay.rare);
-    const uint32_t nd0 = r.ps.n + r.pr.n, cpe = r.p.C / CU;
-    for (uint32_t jj = wave; jj < r.p.q; jj += nw)
-        dn_finish(r.b * r.p.q + jj, lay.part, nd0 + jj * (r.p.UJ / CU), cpe, nullptr, 0u, 0u, 0u, 0u, 1u, r.p.UJ,
-                  r.p.A, r.comb, r.K, r.has_shared, r.semantics, r.width, r.out, r.status);
+    const uint32_t nd0 = r.ps.n + r.pr.n, cpe = r.p.C / CU, nent = r.K + (r.has_shared ? 1u : 0u);
+    const VL_LDS CombineEntry* C = lptr<CombineEntry>(r.comb);
+    for (uint32_t i = wave; i < r.p.q * nent; i += nw) {
+        const uint32_t jj = i / nent, k = i - jj * nent, a = C[k].src >> 3;
+        const float v = sum_parts(lay.part, nd0 + jj * (r.p.UJ / CU) + a * cpe, cpe);
+        lds_st_f32(lay.hstage + i * 256u + lane * 4u, v + __shfl_xor(v, 32));
+    }
+    __syncthreads();
+    for (uint32_t jj = wave; jj < r.p.q; jj += nw) {
+        float acc = 0.0f;
+        for (uint32_t k = 0; k < nent; ++k)
+            acc = dn_combine(acc, lds_f32(lay.hstage + (jj * nent + k) * 256u + lane * 4u), k, r.K, r.semantics, C);
+        dn_store(r.b * r.p.q + jj, acc, r.width, r.out, r.status);
+    }
 }
 
 // ------------------------------------------------------------------------------------------

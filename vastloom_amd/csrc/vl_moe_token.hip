@@ -127,20 +127,27 @@ TokPlan tok_plan_down(const MoeShape& s, uint32_t blocks) {
 
 // LDS of the gate/up kernel, from byte 0: decode tables, the token's limbs, its 2^-e per 256
 // columns, chunk partials, counters and flags, the active list, combine entries, weight pointers
-// of the active experts.
+// of the active experts, the rare-path record, then the routing area: every expert's gate and up
+// pointers (pools of up to kTokPtrTab experts), every expert's value, group maxima, the candidate
+// list and the top-k by rank.
 constexpr uint32_t kTokPtrTab = 256;
 constexpr uint32_t kTokRareBytes = 256;  // TokRare, rounded up
+constexpr uint32_t kTokMaxGroups = 64;   // group maxima of the routing threshold
 struct TokGuLds {
-    uint32_t xstage, xscale, part, desc, misc, act, comb, wptr, rare, bytes;
+    uint32_t xstage, xscale, part, desc, misc, act, comb, wptr, rare, ptab, val, gmax, cand, sel, bytes;
 };
-// misc words
 // misc words: the chunk counter, chunks done per segment of the S and R pieces, the chunks each
-// such segment has, the refusal flag, one flag word per wave.
+// such segment has, the refusal flag, one x-flag word per wave, the candidate count, one
+// non-finite-key flag word per wave.
 constexpr uint32_t kMiscGrab = 0, kMiscSeg = 1, kMiscSegN = kMiscSeg + 2 * kTokMaxSeg,
                    kMiscBad = kMiscSegN + 2 * kTokMaxSeg, kMiscWaveFlags = kMiscBad + 1,
-                   kMiscWords = kMiscWaveFlags + kTokWaves;
+                   kMiscCand = kMiscWaveFlags + kTokWaves, kMiscKeyFlags = kMiscCand + 1,
+                   kMiscWords = kMiscKeyFlags + kTokWaves;
 
-__host__ __device__ inline TokGuLds tok_lds_gu(uint32_t table_bytes, uint32_t width, uint32_t max_chunks) {
+__host__ __device__ inline bool tok_has_ptab(uint32_t experts) { return experts + 1u <= kTokPtrTab + 1u; }
+
+__host__ __device__ inline TokGuLds tok_lds_gu(uint32_t table_bytes, uint32_t width, uint32_t max_chunks,
+                                               uint32_t experts) {
     TokGuLds l;
     l.xstage = table_bytes;
     l.xscale = l.xstage + (width / 32u) * 128u;
@@ -151,7 +158,12 @@ __host__ __device__ inline TokGuLds tok_lds_gu(uint32_t table_bytes, uint32_t wi
     l.comb = l.act + kTokMaxActive * (uint32_t)sizeof(ActiveExpert);
     l.wptr = (l.comb + (kMoeMaxTopK + 1u) * (uint32_t)sizeof(CombineEntry) + 15u) & ~15u;
     l.rare = l.wptr + kTokMaxActive * 16u;
-    l.bytes = l.rare + kTokRareBytes;
+    l.ptab = l.rare + kTokRareBytes;
+    l.val = l.ptab + (tok_has_ptab(experts) ? (experts + 1u) * 16u : 0u);
+    l.gmax = (l.val + experts * 4u + 15u) & ~15u;
+    l.cand = l.gmax + kTokMaxGroups * 4u;
+    l.sel = l.cand + experts * 16u;
+    l.bytes = l.sel + kMoeMaxTopK * 8u;
     return l;
 }
 
@@ -159,7 +171,7 @@ __host__ __device__ inline TokGuLds tok_lds_gu(uint32_t table_bytes, uint32_t wi
 // partials, counters, combine entries, down pointers of the active experts, every expert's down
 // pointer (pools of up to kTokPtrTab experts).
 struct TokDnLds {
-    uint32_t hstage, hscale, part, desc, misc, comb, dptr, rare, ptab, bytes;
+    uint32_t hstage, hscale, part, desc, misc, comb, dptr, rare, ptab, eid, bytes;
 };
 __host__ __device__ inline TokDnLds tok_lds_dn(uint32_t table_bytes, uint32_t A, uint32_t inter,
                                                uint32_t max_chunks) {
@@ -173,7 +185,8 @@ __host__ __device__ inline TokDnLds tok_lds_dn(uint32_t table_bytes, uint32_t A,
     l.dptr = (l.comb + (kMoeMaxTopK + 1u) * (uint32_t)sizeof(CombineEntry) + 15u) & ~15u;
     l.rare = l.dptr + kTokMaxActive * 8u;
     l.ptab = l.rare + kTokRareBytes;
-    l.bytes = l.ptab + (kTokPtrTab + 1u) * 8u;
+    l.eid = l.ptab + (kTokPtrTab + 1u) * 8u;
+    l.bytes = l.eid + kTokMaxActive * 4u;
     return l;
 }
 
@@ -183,6 +196,54 @@ static uint32_t tab_bytes(uint32_t type) {
     return type == VL_TYPE_IQ2_XXS || type == VL_TYPE_IQ3_XXS ? kReplTableBytes
          : type == VL_TYPE_IQ1_S ? kIq1TableBytes : 0u;
 }
+
+// Keeps the compiler from moving the loads issued before it to after it (it would otherwise
+// sink each load to its first use, and a prologue would wait one memory latency per load).
+__device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
+// A load from a constant table that stays where it is written: the pointer passes through an
+// empty asm, so the compiler no longer knows it addresses constant memory (loads from which it may
+// move past issue_fence).
+__device__ __forceinline__ uint64_t ld_pinned(const uint64_t* p) {
+    asm volatile("" : "+v"(p));
+    return *gp(p);
+}
+
+// Decode tables of FMT for the token kernels: one 8-byte source entry per thread, loaded
+// unconditionally (a clamped index; threads past the last entry store nothing), then replicated
+// into LDS. IQ2_XXS and IQ3_XXS: 128 sign entries (rows 0..127, upper halves) and 256 grid entries
+// (rows 0..255, lower halves), 16 copies each (vl_decode.h); IQ1_S: 2048 entries, one copy, two
+// per thread.
+template <uint32_t FMT>
+struct TokTables {
+    static constexpr bool kRepl = FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_IQ3_XXS;
+    static constexpr uint32_t kEntries = kRepl ? 384u : FMT == VL_TYPE_IQ1_S ? 2048u : 0u;
+    uint64_t v0, v1;
+    __device__ __forceinline__ void load(uint32_t t) {
+        if (kRepl) {
+            const uint32_t i = t < kEntries ? t : kEntries - 1u;
+            const uint64_t* src = FMT == VL_TYPE_IQ2_XXS ? (i < 128u ? g_tables.sign_sel + i : g_tables.iq2_codes + (i - 128u))
+                                                         : (i < 128u ? g_tables.iq3_sel + i : g_tables.iq3_pm + (i - 128u));
+            v0 = ld_pinned(src);
+        } else if (FMT == VL_TYPE_IQ1_S) {
+            v0 = ld_pinned(g_tables.iq1_codes + (t & 2047u));
+            v1 = ld_pinned(g_tables.iq1_codes + ((t + 1024u) & 2047u));
+        }
+    }
+    __device__ __forceinline__ void store(uint8_t* lds, uint32_t t) const {
+        if (kRepl) {
+            if (t >= kEntries) return;
+            const uint32_t row = t < 128u ? t * 256u + kTabB : (t - 128u) * 256u + kTabA;
+            const uint4 q = make_uint4(lo32(v0), hi32(v0), lo32(v0), hi32(v0));
+#pragma unroll
+            for (uint32_t c = 0; c < kTabCopies / 2u; ++c) *reinterpret_cast<uint4*>(lds + row + 16u * c) = q;
+        } else if (FMT == VL_TYPE_IQ1_S) {
+            if (t < 1024u) {
+                reinterpret_cast<uint64_t*>(lds)[t] = v0;
+                reinterpret_cast<uint64_t*>(lds)[t + 1024u] = v1;
+            }
+        }
+    }
+};
 
 // Whether every block's piece of each stream-K region touches at most kTokMaxSeg jobs.
 static bool segments_fit(const TokRegion& X, uint32_t UJ) {
@@ -203,7 +264,7 @@ bool tok_applies(const MoeShape& s, uint32_t blocks) {
     if (!segments_fit(g.S, g.UJ) || !segments_fit(g.R, g.UJ) || !segments_fit(d.R, d.UJ)) return false;
     // The data-parallel finishes keep their sums where the activations were staged.
     if (2ull * g.q * 256u > 4ull * s.width || (uint64_t)d.q * A * 256u > 4ull * A * s.inter) return false;
-    if (tok_lds_gu(tab_bytes(s.gate_type), s.width, g.max_chunks).bytes > kLdsLimit) return false;
+    if (tok_lds_gu(tab_bytes(s.gate_type), s.width, g.max_chunks, s.experts).bytes > kLdsLimit) return false;
     if (tok_lds_dn(tab_bytes(s.down_type), A, s.inter, d.max_chunks).bytes > kLdsLimit) return false;
     return true;
 }
@@ -470,6 +531,14 @@ __device__ __forceinline__ void issue(const Ctx& ctx, const TokWork& c, Chunk (&
     }
 }
 
+// A fragment of one token's limbs from LDS into v. The token occupies A rows 0, 1, 4 and 5 (its
+// four limbs). Row m of the product depends on A row m alone, and the rows of other token slots
+// are never read from the result, so only the eight lanes that supply the token's rows read LDS
+// (an eighth of a full-wave read) and the other lanes keep whatever v held.
+__device__ __forceinline__ void tok_afrag(i32x4& v, uint32_t addr) {
+    if (((threadIdx.x & 31u) & ~5u) == 0u) v = lds_load<i32x4>(addr);
+}
+
 // One unit of one token: the lane's share of the partial dot products of its row (the high limbs'
 // share in lanes 32..63, scaled by hs = 65536 there) over the unit's columns, times fs = 2^-e of the
 // token's exponent block. The A fragments come from LDS (aoff: this lane's limb row; groups 128
@@ -484,13 +553,14 @@ __device__ __forceinline__ float tok_unit(const Chunk& ch, uint32_t c, uint32_t 
     const i32x16 zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     if (FMT == VL_TYPE_Q8_0) {
         float acc = 0.0f;
-        i32x4 anext = lds_load<i32x4>(aoff + 4u * c * 128u);
+        i32x4 anext = {0, 0, 0, 0};
+        tok_afrag(anext, aoff + 4u * c * 128u);
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const uint32_t G = 4u * c + b;
             if (G >= ng) break;
             const i32x4 afr = anext;
-            if (b + 1 < 4 && G + 1 < ng) anext = lds_load<i32x4>(aoff + (G + 1u) * 128u);
+            if (b + 1 < 4 && G + 1 < ng) tok_afrag(anext, aoff + (G + 1u) * 128u);
             const uint4& q = b == 0 ? ch.q0 : b == 1 ? ch.q1 : b == 2 ? ch.q2 : ch.q3;
             i32x4 bfr;
             bfr[0] = (int)q.x; bfr[1] = (int)q.y; bfr[2] = (int)q.z; bfr[3] = (int)q.w;
@@ -502,7 +572,8 @@ __device__ __forceinline__ float tok_unit(const Chunk& ch, uint32_t c, uint32_t 
         return acc;
     }
     int acc0 = 0, acc1 = 0;
-    i32x4 anext = lds_load<i32x4>(aoff + 8u * c * 128u);
+    i32x4 anext = {0, 0, 0, 0};
+    tok_afrag(anext, aoff + 8u * c * 128u);
     if (FMT == VL_TYPE_IQ2_XXS) {
         ChunkDecoder<FMT> dec;
         dec.init(ch);
@@ -512,7 +583,7 @@ __device__ __forceinline__ float tok_unit(const Chunk& ch, uint32_t c, uint32_t 
             const i32x4 afr = anext;
             const Iq2Fetch t = tnext;
             if (g + 1 < 8) {
-                anext = lds_load<i32x4>(aoff + (8u * c + g + 1u) * 128u);
+                tok_afrag(anext, aoff + (8u * c + g + 1u) * 128u);
                 tnext = fetch_iq2_xxs(dec.w, g + 1, lane_off);
             }
             const int sc = (int)bfe(g < 4 ? dec.sc_lo : dec.sc_hi, 8u * (uint32_t)(g & 3), 8);
@@ -529,7 +600,7 @@ __device__ __forceinline__ float tok_unit(const Chunk& ch, uint32_t c, uint32_t 
             const i32x4 afr = anext;
             const Iq1Fetch t = tnext;
             if (g + 1 < 8) {
-                anext = lds_load<i32x4>(aoff + (8u * c + g + 1u) * 128u);
+                tok_afrag(anext, aoff + (8u * c + g + 1u) * 128u);
                 tnext = fetch_iq1_s(qs(g + 1), qh(g + 1), hh);
             }
             const int sc = 2 * (int)((qh(g) >> 12) & 7u) + 1;
@@ -557,64 +628,44 @@ __device__ __forceinline__ bool consume(const Ctx& ctx, const TokWork& c, uint32
     return ctx.done(c);
 }
 
-// Segments a stream pass completed, to be handed off with no chunk in flight; `next` is a chunk
-// index taken from the counter and not yet loaded.
+// The segment a stream pass completed (n = 1), to be handed off with no chunk in flight; `next` is
+// a chunk index taken from the counter and not yet loaded.
 struct TokPass {
     uint32_t n, next;
-    TokWork s0, s1;  // the first n of them
+    TokWork s0;
 };
 
 // One pass of the wave loop: chunk ka (already issued into bufA when `issued`; count 0: none),
-// then chunks from the block's counter, each loaded one chunk ahead of its processing. A pass ends
-// when the counter passes the block's last chunk (n = 0), or after a chunk completed a stream-K
-// segment: the chunk in flight is processed too, and the pass returns the completed segments.
-// Counter values only grow, so the chunk loaded later is always the later one.
+// then chunks from the block's counter. Each chunk is loaded after the previous one is processed,
+// so a wave has one chunk in flight: sixteen waves per CU with one unit each keep the memory
+// system busiest on MI355X, while deeper per-wave queues let the CU's oldest waves take more than
+// their share and lengthen the block's tail. The next chunk index is taken before the current
+// chunk is processed, so the LDS counter's latency is hidden. A pass ends when the counter passes
+// the block's last chunk (n = 0), or after a chunk completed a stream-K segment; the pass then
+// returns the segment and the chunk index taken next.
 template <uint32_t FMT, uint32_t CU, typename Ctx>
 __device__ __forceinline__ TokPass tok_pass(const Ctx& ctx, uint32_t ka, TokWork ca, Chunk (&bufA)[CU], bool issued) {
     TokPass r;
     r.n = 0;
     r.next = 0;
-    Chunk bufB[CU];
     if (!issued) issue<FMT, CU>(ctx, ca, bufA);
     if (!ca.count) {
         ka = grab(ctx.misc);
         ca = ctx.chunk(ka);
         issue<FMT, CU>(ctx, ca, bufA);
     }
-    uint32_t kb = grab(ctx.misc);
-    TokWork cb = ctx.chunk(kb);
-    issue<FMT, CU>(ctx, cb, bufB);
     for (;;) {
         if (!ca.count) break;
         const uint32_t kn = grab(ctx.misc);
         if (consume<FMT, CU>(ctx, ca, ka, bufA)) {
             r.n = 1;
             r.s0 = ca;
-            if (cb.count && consume<FMT, CU>(ctx, cb, kb, bufB)) {
-                r.n = 2;
-                r.s1 = cb;
-            }
             r.next = kn;
             return r;
         }
         ka = kn;
         ca = ctx.chunk(ka);
         issue<FMT, CU>(ctx, ca, bufA);
-        if (!cb.count) break;
-        const uint32_t km = grab(ctx.misc);
-        if (consume<FMT, CU>(ctx, cb, kb, bufB)) {
-            r.n = 1;
-            r.s0 = cb;
-            if (ca.count && consume<FMT, CU>(ctx, ca, ka, bufA)) {
-                r.n = 2;
-                r.s1 = ca;
-            }
-            r.next = km;
-            return r;
-        }
-        kb = km;
-        cb = ctx.chunk(kb);
-        issue<FMT, CU>(ctx, cb, bufB);
     }
     return r;
 }
@@ -628,7 +679,6 @@ __device__ __forceinline__ void tok_stream(const Ctx& ctx, uint32_t ka, TokWork 
         const TokPass r = tok_pass<FMT, CU>(ctx, ka, ca, bufA, issued);
         if (!r.n) return;
         ctx.segment(r.s0);
-        if (r.n > 1) ctx.segment(r.s1);
         ka = r.next;
         ca = ctx.chunk(ka);
         issued = false;
@@ -639,22 +689,6 @@ __device__ __forceinline__ void tok_stream(const Ctx& ctx, uint32_t ka, TokWork 
 // Routing of the token (gate/up prologue).
 // ------------------------------------------------------------------------------------------
 
-// Selection keys of the learned and softmax routes, loaded by every wave: lane l of register i
-// holds expert l + 64 i's key (0 past the last expert) and, for the learned route, its score.
-template <int PER>
-__device__ __forceinline__ void load_keys(const MoeWorkspace& w, uint32_t E, bool scores, uint32_t (&key)[PER],
-                                          float (&val)[PER]) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t* keys = ws_ptr<const uint32_t>(w, w.off_keys);
-    const float* scs = ws_ptr<const float>(w, w.off_scores);
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const uint32_t e = lane + 64u * i;
-        key[i] = e < E ? *gp(keys + e) : 0u;
-        val[i] = e < E && scores ? *gp(scs + e) : 0.0f;
-    }
-}
-
 // The route of the token in wave 0: lane k < K holds the expert of rank k and its weight.
 struct TokRoute {
     uint32_t id;
@@ -662,89 +696,148 @@ struct TokRoute {
     bool bad;  // the token is refused (wave-uniform)
 };
 
-// Learned and softmax routing of the token by wave 0 (every lane active), from every expert's key
-// and score in registers (lane l of register i: expert l + 64 i): the K largest keys, ties to the
-// lower id, in rank order, then their weights with the reference's float64 arithmetic. A key of 1
-// or less marks a non-finite logit, score or selection bias, which refuses the token
-// (activate_gate_logits and require_finite, deepseek_v4_reference.cpp:155-165, :236-239;
-// qwen38_moe_route's logits).
+// Learned and softmax routing of the token by the whole block. The reference takes the K largest
+// selection keys, ties to the lower id, in rank order (deepseek_v4_reference.cpp:243-247,
+// qwen3_8_flash_next_reference.cpp:1217-1221); here every expert's key is paired with its
+// complemented id into a 64-bit key, so that rank order is descending 64-bit order, and the rank
+// of a candidate is the number of candidates with a larger 64-bit key.
 //
-// Selection: each lane first orders its own experts by key, descending (a stable sort, so equal
-// keys keep ascending ids); round k then takes the largest head of the wave, ties to the lowest id,
-// and its lane moves on to its next expert.
-template <int PER>
-__device__ TokRoute route_select(const MoeShape& s, const uint32_t (&key0)[PER], const float (&score)[PER]) {
+// Only keys at or above a threshold compete: the maxima of groups of G consecutive experts bound
+// the top-k from below (the K-th largest group maximum is at most the K-th largest key, since K
+// groups each hold a key at least that large). With fewer than 2K groups every expert competes.
+__host__ __device__ inline uint32_t tok_group(uint32_t E, uint32_t K) {
+    return E >= 32u * K ? 16u : E >= 16u * K ? 8u : E >= 8u * K ? 4u : 0u;
+}
+
+// Maximum over aligned groups of G = 4, 8 or 16 lanes (every lane active); every lane of a group
+// receives its group's maximum. The DPP "old" value 0 is the identity of the maximum.
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v, uint32_t G) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, false));  // quad [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, false));  // quad [2,3,0,1]
+    if (G >= 8u) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, false));  // half-row mirror
+    if (G >= 16u) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, false));  // row mirror
+    return v;
+}
+
+__device__ __forceinline__ uint64_t route_key64(uint32_t key, uint32_t id) { return ((uint64_t)key << 32) | (uint32_t)~id; }
+
+// A candidate in LDS: its 64-bit key and its value (learned: the score; softmax: the logit).
+struct TokCand {
+    uint64_t ck;
+    float val;
+    uint32_t pad;
+};
+
+// Before the first barrier, every thread (thread tid holds expert tid's key and score): the
+// expert's value into LDS, its group's maximum, and per wave whether any key marks a non-finite
+// logit, score or selection bias (a key of 1 or less; activate_gate_logits and require_finite,
+// deepseek_v4_reference.cpp:155-165, :236-239). Returns the expert's value.
+__device__ __forceinline__ float route_stage(const MoeShape& s, uint32_t key, float score, uint32_t val,
+                                             uint32_t gmax, uint32_t misc, uint32_t G) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, E = s.experts;
+    const bool live = tid < E;
+    const uint32_t k = live ? key : 0u;
+    const float v = s.routing == kRouteSoftmax ? (k > 1u ? key_float(k) : 0.0f) : score;
+    if (live) lds_st_f32(val + 4u * tid, v);
+    const bool bad = __any(live && k <= 1u);
+    if (lane == 0) lds_st_u32(misc + 4u * (kMiscKeyFlags + wave), bad ? 1u : 0u);
+    if (G && (tid & ~63u) < E) {
+        const uint32_t m = group_max_u32(k, G);
+        if (live && tid % G == 0u) lds_st_u32(gmax + 4u * (tid / G), m);
+    }
+    return v;
+}
+
+// After the first barrier, the waves that hold experts: the threshold (the K-th largest group
+// maximum, equal maxima ranked by group) and the candidates, the experts whose key reaches it,
+// appended to the candidate list in any order (their ranks do not depend on it). Lane i reads
+// group i's maximum once; the comparisons go through readlane, not LDS.
+__device__ __forceinline__ void route_candidates(const MoeShape& s, uint32_t key, float v, uint32_t gmax,
+                                                 uint32_t cand, uint32_t misc, uint32_t G) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, E = s.experts, K = s.top_k;
+    if ((tid & ~63u) >= E) return;
+    uint32_t t0 = 0;
+    if (G) {
+        const uint32_t ng = (E + G - 1u) / G;  // 2K <= ng <= 64
+        const uint32_t gm = lane < ng ? lds_u32(gmax + 4u * lane) : 0u;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < ng; ++j) {
+            const uint32_t gj = (uint32_t)__builtin_amdgcn_readlane((int)gm, j);
+            rank += (gj > gm || (gj == gm && j < lane)) ? 1u : 0u;
+        }
+        const uint64_t hit = __ballot(lane < ng && rank == K - 1u);
+        t0 = (uint32_t)__builtin_amdgcn_readlane((int)gm, (uint32_t)__builtin_ctzll(hit));
+    }
+    if (tid < E && key >= t0) {
+        const uint32_t i = lds_add(misc + 4u * kMiscCand, 1u);
+        VL_LDS TokCand* c = lptr<TokCand>(cand + 16u * i);
+        c->ck = route_key64(key, tid);
+        c->val = v;
+    }
+}
+
+// Ranks of the candidates; those of rank < K go to the top-k list (sel: id and value by rank).
+// Up to 64 candidates: wave 0, lane i holding candidate i and comparing through readlane. More:
+// thread i of the block for candidate i, comparing against LDS.
+__device__ __forceinline__ void route_rank_wave(uint32_t n, uint32_t K, uint32_t cand, uint32_t sel) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint64_t c = 0;
+    float v = 0.0f;
+    if (lane < n) {
+        const VL_LDS TokCand* e = lptr<TokCand>(cand + 16u * lane);
+        c = e->ck;
+        v = e->val;
+    }
+    const uint32_t clo = (uint32_t)c, chi = (uint32_t)(c >> 32);
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < n; ++j) {
+        const uint64_t cj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)chi, j) << 32) |
+                            (uint32_t)__builtin_amdgcn_readlane((int)clo, j);
+        rank += cj > c ? 1u : 0u;
+    }
+    if (lane < n && rank < K) {
+        lds_st_u32(sel + 8u * rank, ~clo);
+        lds_st_f32(sel + 8u * rank + 4u, v);
+    }
+}
+__device__ __forceinline__ void route_rank_block(uint32_t n, uint32_t K, uint32_t cand, uint32_t sel) {
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const VL_LDS TokCand* e = lptr<TokCand>(cand + 16u * i);
+        const uint64_t c = e->ck;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < n; ++j) rank += lptr<TokCand>(cand + 16u * j)->ck > c ? 1u : 0u;
+        if (rank < K) {
+            lds_st_u32(sel + 8u * rank, ~(uint32_t)c);
+            lds_st_f32(sel + 8u * rank + 4u, e->val);
+        }
+    }
+}
+
+// Wave 0 once the top-k list is complete: lane k < K takes the expert of rank k and forms its
+// weight with the reference's float64 arithmetic. Learned: the selected scores over their sum in
+// rank order, times route_scale (route_from_indices, deepseek_v4_reference.cpp:80-121). Softmax:
+// float64 softmax over every logit, the top-k probabilities, optional renormalisation
+// (qwen38_moe_route, qwen3_8_flash_next_reference.cpp:1186-1240).
+__device__ TokRoute route_weights(const MoeShape& s, uint32_t sel, uint32_t val, uint32_t misc) {
     const uint32_t lane = threadIdx.x & 63u, K = s.top_k, E = s.experts;
-    const bool softmax = s.routing == kRouteSoftmax;
-    uint32_t key[PER], hid[PER];
-    float val[PER];
-    bool bad = false;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const uint32_t e = lane + 64u * i;
-        const bool live = e < E;
-        bad |= live && key0[i] <= 1u;
-        key[i] = live ? key0[i] : 0u;
-        hid[i] = e;
-        val[i] = softmax ? (key0[i] > 1u ? key_float(key0[i]) : 0.0f) : score[i];
-    }
-#pragma unroll
-    for (int i = 1; i < PER; ++i)
-#pragma unroll
-        for (int j = i; j > 0; --j) {
-            const bool up = key[j] > key[j - 1];
-            const uint32_t k0 = key[j - 1], h0 = hid[j - 1];
-            const float v0 = val[j - 1];
-            key[j - 1] = up ? key[j] : k0;
-            hid[j - 1] = up ? hid[j] : h0;
-            val[j - 1] = up ? val[j] : v0;
-            key[j] = up ? k0 : key[j];
-            hid[j] = up ? h0 : hid[j];
-            val[j] = up ? v0 : val[j];
-        }
     uint32_t id = 0;
-    float vk = 0.0f, v_first = 0.0f;
-    double sum = 0.0;  // the selected values in rank order
-    for (uint32_t k = 0; k < K; ++k) {
-        const uint32_t m = wave_max_u32(key[0]);
-        const bool top = key[0] == m;
-        const uint64_t hit = __ballot(top);
-        uint32_t wl = (uint32_t)__builtin_ctzll(hit);
-        if (hit & (hit - 1u)) {
-            const uint32_t mid = wave_min_u32(top ? hid[0] : 0xffffffffu);
-            wl = (uint32_t)__builtin_ctzll(__ballot(top && hid[0] == mid));
-        }
-        const uint32_t wid = (uint32_t)__builtin_amdgcn_readlane((int)hid[0], wl);
-        const float wv = readlane_f32(val[0], wl);
-        if (lane == k) {
-            id = wid;
-            vk = wv;
-        }
-        if (k == 0) v_first = wv;
-        sum += (double)wv;
-        const bool me = lane == wl;
-#pragma unroll
-        for (int i = 0; i + 1 < PER; ++i) {
-            key[i] = me ? key[i + 1] : key[i];
-            hid[i] = me ? hid[i + 1] : hid[i];
-            val[i] = me ? val[i + 1] : val[i];
-        }
-        key[PER - 1] = me ? 0u : key[PER - 1];
+    float vk = 0.0f;
+    if (lane < K) {
+        id = lds_u32(sel + 8u * lane);
+        vk = lds_f32(sel + 8u * lane + 4u);
     }
+    bool bad = false;
+    for (uint32_t i = 0; i < kTokWaves; ++i) bad |= lds_u32(misc + 4u * (kMiscKeyFlags + i)) != 0u;
     float wk = 0.0f;
-    if (!softmax) {
-        // Selected scores over their float64 sum in rank order, times route_scale
-        // (route_from_indices, deepseek_v4_reference.cpp:80-121).
+    if (s.routing != kRouteSoftmax) {
+        double sum = 0.0;  // the selected scores in rank order
+        for (uint32_t k = 0; k < K; ++k) sum += (double)readlane_f32(vk, k);
         bad |= !(sum > 0.0) || isinf(sum);
         wk = (float)((double)vk / sum * (double)s.route_scale);
     } else {
-        // float64 softmax over every logit, the top-k probabilities, optional renormalisation
-        // (qwen38_moe_route, qwen3_8_flash_next_reference.cpp:1186-1240).
-        const double mx = (double)v_first;
+        const double mx = (double)readlane_f32(vk, 0);
         double all = 0.0;
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (lane + 64u * i < E) all += exp((double)(key0[i] > 1u ? key_float(key0[i]) : 0.0f) - mx);
+        for (uint32_t e = lane; e < E; e += 64u) all += exp((double)lds_f32(val + 4u * e) - mx);
         all = wave_sum_f64(all);
         const double pk = exp((double)vk - mx) * (all > 0.0 ? 1.0 / all : 0.0);
         double selsum = 0.0;
@@ -752,7 +845,7 @@ __device__ TokRoute route_select(const MoeShape& s, const uint32_t (&key0)[PER],
         wk = (float)pk;
         if (s.renormalize && selsum > 0.0) wk = (float)((double)wk * (1.0 / selsum));
     }
-    return TokRoute{lane < K ? id : 0u, lane < K ? wk : 0.0f, __any(bad) != 0};
+    return TokRoute{lane < K ? id : 0u, lane < K ? wk : 0.0f, bad};
 }
 
 // Table and given routing of the token by wave 0. An id out of range or repeated, any non-finite
@@ -1012,11 +1105,11 @@ __device__ __forceinline__ void fill_work(const TokPlan p, uint32_t b, const Tok
     }
 }
 
-template <uint32_t FMT, int PER>
+template <uint32_t FMT>
 __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s, const MoeInputs in,
                                                                 const MoeWorkspace w, const TokPlan p) {
     constexpr uint32_t TB = table_bytes<FMT>(), CU = tok_chunk_units(FMT);
-    const TokGuLds lay = tok_lds_gu(TB, s.width, p.max_chunks);
+    const TokGuLds lay = tok_lds_gu(TB, s.width, p.max_chunks, s.experts);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nw = blockDim.x >> 6;
     const uint32_t b = blockIdx.x, K = s.top_k, E = s.experts;
     const TokPiece ps = tok_piece(p.S, b, CU), pr = tok_piece(p.R, b, CU);
@@ -1032,104 +1125,133 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
     ctx.xscale = lay.xscale;
     ctx.wptr = lay.wptr;
     const uint32_t nS = ps.n, nstatic = nS < nw ? nS : nw;
-
-    // Wave 0 routes the token; waves 1.. (the helpers, thread h of nh) stage everything else.
-    const bool helper = wave != 0;
-    const uint32_t h = tid - 64u, nh = blockDim.x - 64u;
-
-    // 1. Requests, all before the first LDS store: wave 0's routing keys; the helpers' decode
-    //    tables, token limbs, exponents and flags, the shared expert's pointers; then each wave's
-    //    first chunk of the shared expert.
     const bool ranked = s.routing == kRouteLearned || s.routing == kRouteSoftmax;
-    uint32_t key[PER];
-    float score[PER];
-    if (ranked && !helper) load_keys<PER>(w, E, s.routing == kRouteLearned, key, score);
-    TableFill<FMT> tf;
-    const bool one = TableFill<FMT>::single(nh);
-    if (helper && one) tf.load(h, nh);
+    const bool ptab = tok_has_ptab(E);
+    const uint32_t G = tok_group(E, K);
+
+    // 1. Requests, every one issued unconditionally (clamped indices), so that they are waited for
+    //    as one group: every expert's selection key and score (thread e: expert e) and gate/up
+    //    pointers, the shared expert's pointers, the decode tables, the token's limbs, exponents and
+    //    flags. The first weight chunk is requested only after these have arrived and been stored:
+    //    loads complete in order, and a chunk from HBM ahead of them would delay every wait of the
+    //    prologue.
+    const uint32_t ek = tid < E ? tid : E - 1u;
+    const uint32_t key = *gp(ws_ptr<const uint32_t>(w, w.off_keys) + ek);
+    const float score = *gp(ws_ptr<const float>(w, w.off_scores) + ek);
+    const uint32_t elast = s.has_shared ? E : E - 1u;
+    const MoeExpert* ex = in.experts + (tid < elast ? tid : elast);
+    const uint64_t pg = reinterpret_cast<uint64_t>(ex->gate), pu = reinterpret_cast<uint64_t>(ex->up);
+    const MoeExpert* exs = in.experts + elast;
+    const uint64_t shg = reinterpret_cast<uint64_t>(exs->gate), shu = reinterpret_cast<uint64_t>(exs->up);
+    TokTables<FMT> tt;
+    tt.load(tid);
     const uint32_t xn = (s.width / 32u) * 128u / 16u;  // 16-byte words of the token's limbs
     const uint4* xsrc = ws_ptr<const uint4>(w, w.off_xlimbs);
     constexpr uint32_t XB = 2;
     uint4 xv[XB];
 #pragma unroll
-    for (uint32_t j = 0; j < XB; ++j)
-        if (helper && h + j * nh < xn) xv[j] = ld_u4(xsrc + h + j * nh);
-    int ev = 0;
-    uint32_t fv = 0;
-    if (helper && h < w.xblocks) {
-        ev = *gp(ws_ptr<const int>(w, w.off_xexp) + (uint64_t)w.estride * h);
-        fv = *gp(ws_ptr<const uint32_t>(w, w.off_xflags) + (uint64_t)w.estride * h);
+    for (uint32_t j = 0; j < XB; ++j) {
+        const uint32_t i = tid + j * blockDim.x;
+        xv[j] = ld_u4(xsrc + (i < xn ? i : xn - 1u));
     }
-    const bool shared = s.has_shared != 0;
-    uint64_t shp = 0;
-    if (helper && h < 2u && shared) shp = reinterpret_cast<uint64_t>(h ? in.experts[E].up : in.experts[E].gate);
+    const uint32_t xb = tid < w.xblocks ? tid : w.xblocks - 1u;
+    const int ev = *gp(ws_ptr<const int>(w, w.off_xexp) + (uint64_t)w.estride * xb);
+    const uint32_t fv = *gp(ws_ptr<const uint32_t>(w, w.off_xflags) + (uint64_t)w.estride * xb);
+    issue_fence();
+
+    // 2. LDS stores: tables, limbs, 2^-e, pointers, counters and flags, the chunk table, the
+    //    rare-path record, the routing keys and group maxima.
+    tt.store(lds_base(), tid);
+    uint4* xdst = reinterpret_cast<uint4*>(lds_base() + lay.xstage);
+#pragma unroll
+    for (uint32_t j = 0; j < XB; ++j)
+        if (tid + j * blockDim.x < xn) xdst[tid + j * blockDim.x] = xv[j];
+    for (uint32_t i = tid + XB * blockDim.x; i < xn; i += blockDim.x) xdst[i] = ld_u4(xsrc + i);
+    if (tid < w.xblocks) lds_st_f32(lay.xscale + 4u * tid, __builtin_amdgcn_ldexpf(1.0f, -ev));
+    if (ptab && tid <= E) {
+        *lptr<uint64_t>(lay.ptab + 16u * tid) = pg;
+        *lptr<uint64_t>(lay.ptab + 16u * tid + 8u) = pu;
+    }
+    // Counters start at zero (the chunk counter past the statically taken chunks); the flag words
+    // are written by their own waves.
+    if (tid < kMiscWaveFlags) lds_st_u32(lay.misc + 4u * tid, tid == kMiscGrab ? nstatic : 0u);
+    if (tid == kMiscWaveFlags) lds_st_u32(lay.misc + 4u * kMiscCand, 0u);
+    const bool xflag = __any(tid < w.xblocks && fv != 0u);
+    if (lane == 0) lds_st_u32(lay.misc + 4u * (kMiscWaveFlags + wave), xflag ? 1u : 0u);
+    const float rv = ranked ? route_stage(s, key, score, lay.val, lay.gmax, lay.misc, G) : 0.0f;
+    fill_work<CU>(p, b, ps, pr, ctx.nchunks, lay.desc, lay.misc, true, tid, blockDim.x);
+    if (tid == 0) {
+        TokRare r;
+        r.p = p;
+        r.ps = ps;
+        r.pr = pr;
+        r.b = b;
+        r.act = lay.act;
+        r.comb = lay.comb;
+        r.inter = s.inter;
+        r.hblocks = w.hblocks;
+        r.semantics = s.semantics;
+        r.K = K;
+        r.has_shared = s.has_shared;
+        r.width = s.width;
+        r.h = ws_ptr<float>(w, w.off_h);
+        r.hmax = counters_of(w).hmax;
+        r.status = &ws_ptr<MoeHeader>(w, w.off_header)->status;
+        r.counters = counters_of(w).gu;
+        r.rec = ws_ptr<float>(w, w.off_trec);
+        r.out = in.out;
+        lds_put(lay.rare, r);
+    }
+    // Listed routes (wave 0) and this wave's first chunk of the shared expert.
+    TokRoute rt{0, 0.0f, false};
+    if (!ranked && wave == 0) rt = route_listed(s, in, w);
     Chunk bufA[CU];
     TokWork ca{0, 0, 0, 0, 0, 2, 0};
     const uint32_t ka = wave;
     if (wave < nstatic) {
         ca = decode_work(encode_work(tok_chunk<CU>(p, b, ps, pr, ka), p.tiles, p.C, true));
-        const uint8_t* mp = uni_ptr(ca.m ? in.experts[E].up : in.experts[E].gate);
-        const TileRef tr = tile_ref<FMT>(ctx.L, mp, ca.t);
+        const uint8_t* mp = reinterpret_cast<const uint8_t*>(ca.m ? shu : shg);
+        const TileRef tr = tile_ref<FMT>(ctx.L, uni_ptr(mp), ca.t);
 #pragma unroll
         for (uint32_t i = 0; i < CU; ++i)
             tok_load<FMT>(i < ca.count ? tr : idle_tile(), i < ca.count ? ca.col + i : 0u, ctx.ng, bufA[i]);
     }
-    if (!helper) {
-        // 2. Routing: the selection and its weights, the routed experts' pointers (requested as
-        //    soon as their ids are known), the active list.
-        const TokRoute rt = ranked ? route_select<PER>(s, key, score) : route_listed(s, in, w);
+    __syncthreads();
+
+    // 3. Routing: candidates, their ranks, then wave 0 forms the weights, the active list and the
+    //    active experts' pointers.
+    if (ranked) {
+        route_candidates(s, key, rv, lay.gmax, lay.cand, lay.misc, G);
+        __syncthreads();
+        const uint32_t n = uni(lds_u32(lay.misc + 4u * kMiscCand));
+        if (n <= 64u) {
+            if (wave == 0) route_rank_wave(n, K, lay.cand, lay.sel);
+        } else {
+            route_rank_block(n, K, lay.cand, lay.sel);
+            __syncthreads();
+        }
+    }
+    if (wave == 0) {
+        if (ranked) {
+            lds_settle();
+            rt = route_weights(s, lay.sel, lay.val, lay.misc);
+        }
         const bool bad = rt.bad;
-        uint64_t pg = 0, pu = 0;
-        if (lane < K && !bad) {
-            pg = reinterpret_cast<uint64_t>(in.experts[rt.id].gate);
-            pu = reinterpret_cast<uint64_t>(in.experts[rt.id].up);
-        }
         const uint32_t a = tok_active(s, w, rt, lay.act, lay.comb, b == 0);
-        if (lane < K) {
-            *lptr<uint64_t>(lay.wptr + 16u * a) = pg;
-            *lptr<uint64_t>(lay.wptr + 16u * a + 8u) = pu;
+        if (lane < K && !bad) {
+            uint64_t g = 0, u = 0;
+            if (ptab) {
+                g = *lptr<uint64_t>(lay.ptab + 16u * rt.id);
+                u = *lptr<uint64_t>(lay.ptab + 16u * rt.id + 8u);
+            } else {
+                g = reinterpret_cast<uint64_t>(in.experts[rt.id].gate);
+                u = reinterpret_cast<uint64_t>(in.experts[rt.id].up);
+            }
+            *lptr<uint64_t>(lay.wptr + 16u * a) = g;
+            *lptr<uint64_t>(lay.wptr + 16u * a + 8u) = u;
         }
-        if (lane == 0) {
-            lds_st_u32(lay.misc + 4u * kMiscBad, bad ? 1u : 0u);
-            lds_st_u32(lay.misc + 4u * kMiscWaveFlags, 0u);
-        }
-    } else {
-        // 3. The helpers' LDS stores.
-        if (one) tf.store(lds_base(), h, nh);
-        else fill_tables<FMT>(lds_base(), h, nh);
-        uint4* xdst = reinterpret_cast<uint4*>(lds_base() + lay.xstage);
-#pragma unroll
-        for (uint32_t j = 0; j < XB; ++j)
-            if (h + j * nh < xn) xdst[h + j * nh] = xv[j];
-        for (uint32_t i = h + XB * nh; i < xn; i += nh) xdst[i] = ld_u4(xsrc + i);
-        if (h < w.xblocks) lds_st_f32(lay.xscale + 4u * h, __builtin_amdgcn_ldexpf(1.0f, -ev));
-        if (h < 2u && shared) *lptr<uint64_t>(lay.wptr + 16u * K + 8u * h) = shp;
-        if (h < kMiscSegN) lds_st_u32(lay.misc + 4u * h, h == kMiscGrab ? nstatic : 0u);
-        const bool xflag = __any(h < w.xblocks && fv != 0u);
-        if (lane == 0) lds_st_u32(lay.misc + 4u * (kMiscWaveFlags + wave), xflag ? 1u : 0u);
-        fill_work<CU>(p, b, ps, pr, ctx.nchunks, lay.desc, lay.misc, true, h, nh);
-        if (h == 0) {
-            TokRare r;
-            r.p = p;
-            r.ps = ps;
-            r.pr = pr;
-            r.b = b;
-            r.act = lay.act;
-            r.comb = lay.comb;
-            r.inter = s.inter;
-            r.hblocks = w.hblocks;
-            r.semantics = s.semantics;
-            r.K = K;
-            r.has_shared = s.has_shared;
-            r.width = s.width;
-            r.h = ws_ptr<float>(w, w.off_h);
-            r.hmax = counters_of(w).hmax;
-            r.status = &ws_ptr<MoeHeader>(w, w.off_header)->status;
-            r.counters = counters_of(w).gu;
-            r.rec = ws_ptr<float>(w, w.off_trec);
-            r.out = in.out;
-            lds_put(lay.rare, r);
-        }
+        if (lane < 2u && s.has_shared) *lptr<uint64_t>(lay.wptr + 16u * K + 8u * lane) = lane ? shu : shg;
+        if (lane == 0) lds_st_u32(lay.misc + 4u * kMiscBad, bad ? 1u : 0u);
     }
     __syncthreads();
     if (b == 0 && tid == 0) {
@@ -1335,21 +1457,19 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     ctx.hb = HB;
     ctx.ebytes = (F / 32u) * 128u;
     const MoeHeader* hdr = ws_ptr<const MoeHeader>(w, w.off_header);
-    // 1. Requests: the active count, the active experts' ids, the combine entries, every expert's
-    //    down pointer, the decode tables.
+    // 1. Requests, issued unconditionally (clamped indices) and together: the active count, the
+    //    active experts' ids, the combine entries, every expert's down pointer, the decode tables,
+    //    the active experts' h with the maxima of its 256-row blocks.
     const uint32_t n_active_raw = *gp(&hdr->n_active);
     const ActiveExpert* act = ws_ptr<const ActiveExpert>(w, w.off_active);
-    uint32_t eid = 0;
-    if (tid < A) eid = *gp(&act[tid].expert);
-    uint32_t cw = 0;
-    if (tid < 2u * (K + 1u)) cw = *gp(ws_ptr<const uint32_t>(w, w.off_combine) + tid);
+    const uint32_t eid = *gp(&act[tid < A ? tid : A - 1u].expert);
+    const uint32_t nc = 2u * (K + 1u);
+    const uint32_t cw = *gp(ws_ptr<const uint32_t>(w, w.off_combine) + (tid < nc ? tid : nc - 1u));
     const uint32_t pn = E + 1u <= kTokPtrTab + 1u ? E + 1u : 0u;
-    uint64_t pv = 0;
-    if (tid < pn) pv = reinterpret_cast<uint64_t>(in.experts[tid].down);
-    TableFill<FMT> tf;
-    const bool one = TableFill<FMT>::single(blockDim.x);
-    if (one) tf.load(tid, blockDim.x);
-    // The active experts' h (quads of rows) with their 256-row maxima, and the maxima for 2^-e.
+    const uint32_t elast = s.has_shared ? E : E - 1u;
+    const uint64_t pv = reinterpret_cast<uint64_t>(in.experts[tid < elast ? tid : elast].down);
+    TokTables<FMT> tt;
+    tt.load(tid);
     const float* h = ws_ptr<const float>(w, w.off_h);
     const uint32_t* hmax = counters_of(w).hmax;
     const uint32_t quads = F / 4u, hq_total = A * quads;
@@ -1358,15 +1478,17 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     uint32_t hvm[HQ];
 #pragma unroll
     for (uint32_t j = 0; j < HQ; ++j) {
-        const uint32_t i = tid + j * blockDim.x;
-        if (i < hq_total) {
-            const uint32_t a = i / quads, col = 4u * (i - a * quads);
-            hv[j] = ld_f4(h + (uint64_t)a * F + col);
-            hvm[j] = *gp(hmax + ((uint64_t)a * HB + col / 256u) * 8u);
-        }
+        if (j * blockDim.x >= hq_total) break;  // uniform
+        const uint32_t i = tid + j * blockDim.x < hq_total ? tid + j * blockDim.x : hq_total - 1u;
+        const uint32_t a = i / quads, col = 4u * (i - a * quads);
+        hv[j] = ld_f4(h + (uint64_t)a * F + col);
+        hvm[j] = *gp(hmax + ((uint64_t)a * HB + col / 256u) * 8u);
     }
-    const uint32_t hm = tid < A * HB ? *gp(hmax + (uint64_t)tid * 8u) : 0u;
-    if (tid < pn) *lptr<uint64_t>(lay.ptab + 8u * tid) = pv;
+    const uint32_t hb = A * HB;
+    const uint32_t hm = *gp(hmax + (uint64_t)(tid < hb ? tid : hb - 1u) * 8u);
+    issue_fence();
+    if (tid <= elast && tid < pn) *lptr<uint64_t>(lay.ptab + 8u * tid) = pv;
+    if (tid < A) lds_st_u32(lay.eid + 4u * tid, eid);
     if (tid < 2u * (K + 1u)) lds_st_u32(lay.comb + 4u * tid, cw);
     if (tid < kMiscSegN) lds_st_u32(lay.misc + 4u * tid, tid == kMiscGrab ? nw : 0u);
     fill_work<CU>(p, b, ps, pr, ctx.nchunks, lay.desc, lay.misc, false, tid, blockDim.x);
@@ -1392,6 +1514,7 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
         r.out = in.out;
         lds_put(lay.rare, r);
     }
+    tt.store(lds_base(), tid);
     __syncthreads();
     const uint32_t n_active = uni(n_active_raw);
     if (n_active == 0) {
@@ -1399,16 +1522,23 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
         for (uint32_t i = b * blockDim.x + tid; i < s.width; i += gridDim.x * blockDim.x) *gp(in.out + i) = 0.0f;
         return;
     }
-    if (tid < A) {
-        const uint64_t ptr = pn ? *lptr<uint64_t>(lay.ptab + 8u * eid) : reinterpret_cast<uint64_t>(in.experts[eid].down);
-        *lptr<uint64_t>(lay.dptr + 8u * tid) = ptr;
-    }
-    __syncthreads();
-    // 2. This wave's first chunk is requested before the h conversion, whose latency it hides.
+    // 2. The active experts' down pointers; this wave's first chunk is requested at once (its
+    //    pointer looked up through the LDS tables), before the h conversion whose latency it hides.
+    auto down_ptr = [&](uint32_t a) -> uint64_t {
+        const uint32_t e = lds_u32(lay.eid + 4u * a);
+        return pn ? *lptr<uint64_t>(lay.ptab + 8u * e) : reinterpret_cast<uint64_t>(in.experts[e].down);
+    };
+    if (tid < A) *lptr<uint64_t>(lay.dptr + 8u * tid) = down_ptr(tid);
     Chunk bufA[CU];
     const uint32_t ka = wave;
     const TokWork ca = ctx.chunk(ka);
-    issue<FMT, CU>(ctx, ca, bufA);
+    {
+        const TileRef tr = ca.count ? tile_ref<FMT>(ctx.L, uni_ptr(reinterpret_cast<const uint8_t*>(down_ptr(ca.a))), ca.t)
+                                    : idle_tile();
+#pragma unroll
+        for (uint32_t i = 0; i < CU; ++i)
+            tok_load<FMT>(i < ca.count ? tr : idle_tile(), i < ca.count ? ca.col + i : 0u, ctx.ng, bufA[i]);
+    }
     // 3. The active experts' h -> limbs with one exponent per 256 rows, into LDS (the h requested
     //    at entry; a layer with more than HQ quads per thread loads the rest here); tables.
     {
@@ -1424,6 +1554,7 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
 #pragma unroll
         for (uint32_t j = 0; j < HQ; ++j) {
             const uint32_t i = tid + j * blockDim.x;
+            if (j * blockDim.x >= hq_total) break;
             if (i < hq_total) convert(i, hv[j], hvm[j]);
         }
         for (uint32_t i = tid + HQ * blockDim.x; i < hq_total; i += blockDim.x) {
@@ -1437,8 +1568,6 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
             lds_st_f32(lay.hscale + 4u * i, __builtin_amdgcn_ldexpf(1.0f, -e));
         }
     }
-    if (one) tf.store(lds_base(), tid, blockDim.x);
-    else fill_tables<FMT>(lds_base());
     __syncthreads();
     // 4. Stream.
     tok_stream<FMT, CU>(ctx, ka, ca, bufA);
@@ -1480,13 +1609,8 @@ template <uint32_t FMT>
 static hipError_t tok_gateup_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
                                  hipStream_t st, hipEvent_t* ev) {
     const TokPlan p = tok_plan_gateup(s, w.blocks);
-    const uint32_t shm = tok_lds_gu(table_bytes<FMT>(), s.width, p.max_chunks).bytes;
-    const uint32_t E = s.experts;
-    if (E <= 64) return tok_launch(k_tok_gateup<FMT, 1>, p.grid, shm, st, ev, s, in, w, p);
-    if (E <= 128) return tok_launch(k_tok_gateup<FMT, 2>, p.grid, shm, st, ev, s, in, w, p);
-    if (E <= 256) return tok_launch(k_tok_gateup<FMT, 4>, p.grid, shm, st, ev, s, in, w, p);
-    if (E <= 512) return tok_launch(k_tok_gateup<FMT, 8>, p.grid, shm, st, ev, s, in, w, p);
-    return tok_launch(k_tok_gateup<FMT, 16>, p.grid, shm, st, ev, s, in, w, p);
+    const uint32_t shm = tok_lds_gu(table_bytes<FMT>(), s.width, p.max_chunks, s.experts).bytes;
+    return tok_launch(k_tok_gateup<FMT>, p.grid, shm, st, ev, s, in, w, p);
 }
 
 template <uint32_t FMT>

@@ -564,18 +564,28 @@ __device__ __forceinline__ bool arrive(uint32_t* counter, uint32_t kc) {
 
 // Four limbs (signed base-256 digits, the top one carrying the sign) of round(v * 2^e) for
 // four consecutive values, one 32-bit word per limb. Non-finite values encode as zero.
+//
+// For |X| < 2^30, Y = X + 0x808080 has bytes y0, y1, y2 in [0, 255] and a top byte y3 = Y >> 24 in
+// [-64, 63], and X = (y0 - 128) + 2^8 (y1 - 128) + 2^16 (y2 - 128) + 2^24 y3: the digits in
+// [-128, 127] are y_l ^ 0x80 as int8, the unique signed base-256 digits of X. So the bytes of
+// Y ^ 0x808080 are the value's four limbs, and a 4x4 byte transpose groups them by limb.
 __device__ __forceinline__ void limbs4(const float (&v)[4], int e, uint32_t (&packed)[4]) {
-    packed[0] = packed[1] = packed[2] = packed[3] = 0;
+    uint32_t z[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        int X = isfinite(v[k]) ? (int)rintf(ldexpf(v[k], e)) : 0;
-#pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            const int digit = l < 3 ? (int)(int8_t)(X & 0xff) : X;
-            packed[l] |= ((uint32_t)digit & 0xffu) << (8 * k);
-            X = (X - digit) >> 8;
-        }
+        const int X = isfinite(v[k]) ? (int)rintf(ldexpf(v[k], e)) : 0;
+        z[k] = ((uint32_t)X + 0x00808080u) ^ 0x00808080u;
     }
+    // Bytes (value k, limb l) -> word l, byte k: first pair bytes of equal limb parity, then
+    // interleave the pairs.
+    const uint32_t e01 = __builtin_amdgcn_perm(z[1], z[0], 0x06020400u);  // z0b0 z1b0 z0b2 z1b2
+    const uint32_t o01 = __builtin_amdgcn_perm(z[1], z[0], 0x07030501u);  // z0b1 z1b1 z0b3 z1b3
+    const uint32_t e23 = __builtin_amdgcn_perm(z[3], z[2], 0x06020400u);
+    const uint32_t o23 = __builtin_amdgcn_perm(z[3], z[2], 0x07030501u);
+    packed[0] = __builtin_amdgcn_perm(e23, e01, 0x05040100u);
+    packed[1] = __builtin_amdgcn_perm(o23, o01, 0x05040100u);
+    packed[2] = __builtin_amdgcn_perm(e23, e01, 0x07060302u);
+    packed[3] = __builtin_amdgcn_perm(o23, o01, 0x07060302u);
 }
 
 // Exponent that brings m = max |v| (finite, >= 0) to just below 2^30.

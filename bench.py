@@ -12,8 +12,12 @@ cache between their uses.
     python bench.py [--steps K] [--warmup W] [--workload iq2_moe] [--no-cpu-baseline]
     python bench.py --copy-calibration BYTES     plain device copies of BYTES (counter scale)
 
-roofline.traffic (HBM bytes per launch of the gate/up kernel) is read from the committed
-rocprofv3 counter summary profiles/k_moe_gateup.iq2_moe.traffic.txt when it exists.
+ms_per_step is the mean over the K bracketed steps; step_us gives the median and spread of
+per-step times from a second pass with an event between steps. roofline.traffic (HBM bytes per
+launch of the gate/up kernel) is read from the committed rocprofv3 counter summary
+profiles/<kernel>.<workload>.traffic.txt when it exists. The CPU baseline runs the reference's own
+kernels on the host in three modes (one thread, the reference runtime policy's thread count, every
+usable core), each the median of --cpu-samples tokens.
 """
 
 from __future__ import annotations
@@ -21,6 +25,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 from pathlib import Path
@@ -31,7 +36,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
-TRAFFIC_SUMMARY = ROOT / "profiles" / "k_moe_gateup.iq2_moe.traffic.txt"
+PROFILES = ROOT / "profiles"
 
 
 def parse() -> argparse.Namespace:
@@ -47,7 +52,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--token-pool", type=int, default=64)
     p.add_argument("--profile-steps", type=int, default=100)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--cpu-samples", type=int, default=10,
+                   help="tokens timed per CPU-baseline mode (the median is reported)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                    help="only run 20 device-to-device copies of BYTES (no layer)")
     return p.parse_args()
@@ -66,14 +72,44 @@ def copy_calibration(nbytes: int) -> int:
     return 0
 
 
-def measured_traffic() -> tuple[int | None, str | None]:
-    """HBM bytes per gate/up launch from the committed counter summary, if there is one."""
+def measured_traffic(kernel: str, workload: str) -> tuple[int | None, str | None]:
+    """HBM bytes per launch of `kernel` from the committed counter summary, if there is one."""
     import re
 
-    if not TRAFFIC_SUMMARY.exists():
+    path = PROFILES / f"{kernel}.{workload}.traffic.txt"
+    if not path.exists():
         return None, None
-    m = re.search(r"traffic_bytes_per_launch = (\d+)", TRAFFIC_SUMMARY.read_text())
-    return (int(m.group(1)), str(TRAFFIC_SUMMARY.relative_to(ROOT))) if m else (None, None)
+    m = re.search(r"traffic_bytes_per_launch = (\d+)", path.read_text())
+    return (int(m.group(1)), str(path.relative_to(ROOT))) if m else (None, None)
+
+
+def gateup_kernel(wl) -> str:
+    """The gate/up kernel a layer of this workload runs (single-token layers of the learned,
+    softmax and given routings take the single-token kernels, except IQ3_XXS; 2-8 tokens the
+    token-slot stream kernels; more tokens the grouped path)."""
+    if wl.tokens > 8:
+        return "k_moe_gateup_grouped"
+    if wl.tokens == 1 and wl.routing != "zipf_table" and 18 not in (wl.gate_type, wl.down_type):
+        return "k_tok_gateup"
+    return "k_moe_gateup"
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def usable_cpus() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
 
 
 def token_pool(wl, count: int) -> np.ndarray:
@@ -112,45 +148,41 @@ def build_layers(wl, instances: int):
     return experts, shared, layers
 
 
-def cpu_baseline(wl, experts, shared, pool, seconds: float, measured: float | None = None) -> dict:
-    """The reference's own CPU kernels (oracle/_ref, built from its sources) on a bounded
-    sample of the same workload: router logits and routing, then per selected expert the
-    reference matvecs (row-split over the runtime policy's threads), SwiGLU and combine."""
+def cpu_baseline(wl, experts, shared, pool, samples: int, measured: float | None = None) -> dict:
+    """The reference's own CPU kernels (oracle/_ref, built from its sources) on a bounded sample
+    of the same workload: for each token, router logits and routing, then per selected expert the
+    reference matvecs (row-split over the mode's threads; IQ1_S and IQ3_XXS stay serial, as in the
+    reference), SwiGLU and combine. Three modes: one thread, the reference runtime policy's thread
+    count (the reported value), every usable core; each the median of `samples` tokens."""
     from oracle.oracle import Oracle, Reference, default_threads
 
     orc = Oracle()
     kind = "reference" if Reference.available() else "port"
     ref = Reference() if kind == "reference" else None
-    threads = default_threads()
     H, F = wl.width, wl.intermediate
     router = wl.router()
-
-    def matvec(qtype, data, rows, cols, x):
-        if ref is not None:
-            return ref.matvec(qtype, data, rows, cols, x, threads=threads)
-        return orc.matvec(qtype, data, rows, cols, x, threads=threads)
-
-    def expert(e, x, w_route):
-        g = matvec(e.gate_type, e.gate, F, H, x)
-        u = matvec(e.gate_type, e.up, F, H, x)
-        if wl.semantics == "qwen":
-            h = (np.array([orc.silu_f(float(v)) for v in g], np.float32) * u).astype(np.float32)
-        else:
-            gv, uv = g.astype(np.float64), u.astype(np.float64)
-            h = gv / (1.0 + np.exp(-gv)) * uv
-            if w_route is not None:
-                h = h * np.float64(w_route)
-            h = h.astype(np.float32)
-        return matvec(e.down_type, e.down, H, F, h)
-
     table = wl.zipf_table() if wl.routing == "zipf_table" else None
-    # Tokens are independent: the sample is whole tokens of the layer, and the time per layer
-    # is the time per token times the layer's tokens.
-    done, t0 = 0, time.perf_counter()
-    while True:
-        batch = done // wl.tokens
-        t = done % wl.tokens
-        xt = pool[batch % len(pool)][t]
+
+    def token_time(xt, t, threads) -> float:
+        def matvec(qtype, data, rows, cols, x):
+            if ref is not None:
+                return ref.matvec(qtype, data, rows, cols, x, threads=threads)
+            return orc.matvec(qtype, data, rows, cols, x, threads=threads)
+
+        def expert(e, x, w_route):
+            g = matvec(e.gate_type, e.gate, F, H, x)
+            u = matvec(e.gate_type, e.up, F, H, x)
+            if wl.semantics == "qwen":
+                h = (np.array([orc.silu_f(float(v)) for v in g], np.float32) * u).astype(np.float32)
+            else:
+                gv, uv = g.astype(np.float64), u.astype(np.float64)
+                h = gv / (1.0 + np.exp(-gv)) * uv
+                if w_route is not None:
+                    h = h * np.float64(w_route)
+                h = h.astype(np.float32)
+            return matvec(e.down_type, e.down, H, F, h)
+
+        t0 = time.perf_counter()
         if wl.routing == "single":
             expert(experts[0], xt, None)
         else:
@@ -170,17 +202,28 @@ def cpu_baseline(wl, experts, shared, pool, seconds: float, measured: float | No
                 out += y * wr if wl.semantics == "qwen" else y
             if shared is not None:
                 out += expert(shared, xt, None)
-        done += 1
-        if time.perf_counter() - t0 >= seconds and done % min(wl.tokens, 8) == 0:
-            break
-    elapsed = time.perf_counter() - t0
-    per_layer = elapsed / done * wl.tokens
+        return time.perf_counter() - t0
+
     layer_bytes = layer_weight_bytes(wl, measured)
-    return {"value": round(layer_bytes / per_layer / 1e9, 4), "unit": "GB/s",
-            "cores": threads, "kind": kind,
-            "us_per_layer": round(per_layer * 1e6, 1),
-            "sample": f"{done} token(s) of the {wl.name} workload ({wl.tokens} per layer), "
-                      f"{elapsed:.1f} s on {threads} thread(s) of {os.cpu_count()} logical CPUs"}
+    modes = {}
+    for mode, threads in (("threads_1", 1), ("policy", default_threads()), ("all_cores", usable_cpus())):
+        per_token = []
+        for i in range(samples):
+            batch, t = i // wl.tokens, i % wl.tokens
+            per_token.append(token_time(pool[batch % len(pool)][t], t, threads))
+        per_layer = np.array(per_token) * wl.tokens  # tokens are independent
+        med = float(np.median(per_layer))
+        modes[mode] = {"threads": threads, "us_per_layer_median": round(med * 1e6, 1),
+                       "us_per_layer_min": round(float(per_layer.min()) * 1e6, 1),
+                       "us_per_layer_max": round(float(per_layer.max()) * 1e6, 1),
+                       "gbs_median": round(layer_bytes / med / 1e9, 4), "samples": samples}
+    pol = modes["policy"]
+    return {"value": pol["gbs_median"], "unit": "GB/s", "cores": pol["threads"], "kind": kind,
+            "us_per_layer": pol["us_per_layer_median"], "modes": modes,
+            "cpu_model": cpu_model(), "nproc": usable_cpus(),
+            "sample": f"{samples} token(s) per mode of the {wl.name} workload ({wl.tokens} per layer; "
+                      f"per-layer time = median per-token time x {wl.tokens}); value = the "
+                      f"reference runtime policy's {pol['threads']} threads of {usable_cpus()} usable CPUs"}
 
 
 def routed_experts(wl, measured: float | None = None) -> float:
@@ -255,6 +298,18 @@ def main() -> int:
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
     ms_per_step = total_ms / args.steps
+    # Per-step times: a second pass with an event recorded between consecutive steps.
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    evs[0].record()
+    for i in range(args.steps):
+        step(i)
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    per_step = np.array([evs[i].elapsed_time(evs[i + 1]) * 1000.0 for i in range(args.steps)])
+    step_us = {"median": round(float(np.median(per_step)), 2),
+               "p10": round(float(np.percentile(per_step, 10)), 2),
+               "p90": round(float(np.percentile(per_step, 90)), 2),
+               "min": round(float(per_step.min()), 2), "max": round(float(per_step.max()), 2)}
     stream = torch.cuda.current_stream().cuda_stream
     for layer in layers:
         for ws in layer._ws.values():
@@ -292,7 +347,8 @@ def main() -> int:
     # The kernels' own durations (events around their execution), as a kernel trace reports them.
     gateup_gbs = gateup_bytes / (kernel_us["gate_up"] * 1e-6) / 1e9
     down_gbs = n_exp * storage_bytes(wl.down_type, H, F) / (kernel_us["down"] * 1e-6) / 1e9
-    traffic, traffic_src = measured_traffic() if wl.name == "iq2_moe" else (None, None)
+    gu_kernel = gateup_kernel(wl)
+    traffic, traffic_src = measured_traffic(gu_kernel, wl.name)
 
     result = {
         "metric": "quant expert FFN effective HBM GB/s (% of peak) + us per MoE layer, 1 GPU",
@@ -303,6 +359,7 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "us_per_layer": round(ms_per_step * 1000.0, 2),
+        "step_us": step_us,
         "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -311,7 +368,7 @@ def main() -> int:
                  "i8xi8->i32 MFMA, f32 accumulate",
         "data": f"synthetic (seeded PCG64; uniform random {TYPE(wl.gate_type)}/{TYPE(wl.down_type)} "
                 f"payload bytes, |N(0,1)|*{wl.scale_factor} fp16 scales, N(0,0.02) router, N(0,1) tokens)",
-        "config": {"workload": f"{wl.name}: DeepSeek-class MoE layer, width {wl.width}, expert "
+        "config": {"workload": f"{wl.name}: {wl.model} {wl.kind}, width {wl.width}, expert "
                                f"width {wl.intermediate}, {wl.experts} routed experts top-"
                                f"{wl.top_k} + {int(wl.has_shared)} shared, {wl.tokens} token(s), "
                                f"{ROUTER_NAME[wl.routing]} router, {TYPE(wl.gate_type)} gate/up, "
@@ -323,7 +380,7 @@ def main() -> int:
                    "layer_instances": args.layers, "token_pool": args.token_pool},
         "stages_us": stage_us,
         "kernels_us": kernel_us,
-        "roofline": {"bound": "hbm", "kernel": "k_moe_gateup" if wl.tokens <= 8 else "k_moe_gateup_grouped",
+        "roofline": {"bound": "hbm", "kernel": gu_kernel,
                      "achieved": round(gateup_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gateup_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -334,7 +391,7 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(wl, experts, shared, pool_host, args.cpu_seconds,
+        result["cpu_baseline"] = cpu_baseline(wl, experts, shared, pool_host, args.cpu_samples,
                                               measured)
     print(json.dumps(result))
     return 0

@@ -201,6 +201,26 @@ def test_wide_expert_pools(ops, lib, oracle, experts_n, tokens, routing_name):
     _check_layer(ops, lib, oracle, wl, experts, shared, sem, routing_name, routing, x)
 
 
+@pytest.mark.parametrize("experts_n,top_k,tokens,routing_name", [
+    (64, 12, 1, "learned"), (64, 16, 1, "softmax"), (48, 16, 3, "learned"), (64, 12, 20, "learned"),
+    (40, 16, 9, "softmax")])
+def test_wide_top_k(ops, lib, oracle, experts_n, top_k, tokens, routing_name):
+    """top_k 12 and 16 (the header's limit), single token, token slots and the grouped path."""
+    print(f"[moe top_k] E={experts_n} K={top_k} tokens={tokens} {routing_name}", flush=True)
+    rng = np.random.default_rng(100 + experts_n + top_k + tokens)
+    from vastloom_amd.workloads import MoeWorkload
+    sem = "qwen" if routing_name == "softmax" else "deepseek"
+    H, F = 512, 256
+    wl = MoeWorkload("topk", 21, H, F, experts_n, top_k, tokens, IQ2_XXS, IQ2_XXS, 0.01, sem)
+    experts = [make_expert(rng, IQ2_XXS, IQ2_XXS, H, F) for _ in range(experts_n)]
+    shared = make_expert(rng, IQ2_XXS, IQ2_XXS, H, F) if sem == "deepseek" else None
+    x = rng.standard_normal((tokens, H)).astype(np.float32)
+    bias = (rng.standard_normal(experts_n) * 0.05).astype(np.float32) if routing_name == "learned" else None
+    routing = lib.ROUTE_SOFTMAX if routing_name == "softmax" else lib.ROUTE_LEARNED
+    _check_layer(ops, lib, oracle, wl, experts, shared, sem, routing_name, routing, x, SCORE_SIGMOID,
+                 bias, route_scale=1.25 if sem == "deepseek" else 1.0)
+
+
 def test_bad_table_route_is_refused(ops, lib, oracle):
     rng = np.random.default_rng(1)
     from vastloom_amd.workloads import MoeWorkload
@@ -293,10 +313,12 @@ def test_grouped_bad_route_is_refused(ops, lib, oracle):
 
 def test_workload_grouped_moe(ops, lib, oracle):
     """512 tokens, Zipf(1.1) table routing over 256 IQ2_XXS experts plus the shared expert:
-    every token's routes, and the outputs of a sample of tokens, against the oracle."""
+    every token's routes, and the outputs of 69 sampled tokens, against the oracle."""
     wl = workload("grouped_moe")
     print("[workload] grouped_moe", flush=True)
     experts, shared = _workload_case(wl)
+    # A seeded sample of 64 tokens plus the ends and the middle (each token's output depends on
+    # its own routes only; all 512 tokens' routes are checked).
+    sample = np.union1d(np.random.default_rng(4).choice(512, 64, replace=False), [0, 1, 255, 256, 511])
     _check_layer(ops, lib, oracle, wl, experts, shared, "deepseek", "table", lib.ROUTE_TABLE,
-                 wl.x(), SCORE_SIGMOID, table=wl.zipf_table(),
-                 sample=[0, 1, 77, 255, 256, 400, 511])
+                 wl.x(), SCORE_SIGMOID, table=wl.zipf_table(), sample=sample)

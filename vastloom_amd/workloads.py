@@ -148,6 +148,15 @@ class MoeWorkload:
             self._cache["table"] = table
         return self._cache["table"]
 
+    @property
+    def model(self) -> str:
+        """The model family whose shapes the workload mimics."""
+        return "OLMoE-1B-7B-shaped" if self.width == 2048 else "DeepSeek-class"
+
+    @property
+    def kind(self) -> str:
+        return "single-expert SwiGLU FFN" if self.routing == "single" else "MoE layer"
+
     # -- byte accounting ---------------------------------------------------------------
     def expert_bytes(self) -> int:
         H, F = self.width, self.intermediate

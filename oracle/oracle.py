@@ -43,6 +43,12 @@ def build() -> None:
     subprocess.run(["make", "-s", "-C", str(HERE), "ref"], check=True)
 
 
+def build_binding() -> None:
+    """Compile the reference-side binding's test driver (oracle/_ref/accel_binding) against the
+    built HIP library, when the reference tree is present."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "binding"], check=True)
+
+
 def _ptr(a: np.ndarray | None, ctype=C.c_void_p):
     if a is None:
         return None

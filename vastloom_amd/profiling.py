@@ -4,6 +4,9 @@
     python -m vastloom_amd.profiling pmc DIR [DIR ...]    per-kernel mean counter values (--pmc)
     python -m vastloom_amd.profiling traffic --fetch DIR --write DIR --calib-fetch DIR
                                              --calib-write DIR --calib-bytes N --kernel REGEX
+    python -m vastloom_amd.profiling counters --trace DIR --kernel REGEX DIR [DIR ...]
+                                             counter means per dispatch of the kernels matching
+                                             REGEX, with the wave-state split and int8 MFMA rate
 
 rocprofv3 is run with ``--output-format csv``; DIR is its ``-d`` directory. ``traffic`` turns the
 FETCH_SIZE and WRITE_SIZE counters (KiB per dispatch) of one kernel into HBM bytes per launch,
@@ -81,6 +84,36 @@ def traffic(fetch: str, write: str, calib_fetch: str, calib_write: str, calib_by
             "traffic_bytes": f_kib * 1024.0 * f_scale + w_kib * 1024.0 * w_scale}
 
 
+def counters(dirs: list[str], kernel: str, trace: str | None = None) -> list[str]:
+    """Mean counter values per dispatch of each kernel matching `kernel`, and what follows from them:
+    the share of wave cycles spent waiting on an instruction's operands (SQ_WAIT_INST_ANY, mostly
+    s_waitcnt) and issuing (SQ_ACTIVE_INST_ANY); int8 MFMA operations (SQ_INSTS_VALU_MFMA_MOPS_I8
+    counts units of 512) and, with the kernel's average duration from a trace, their rate."""
+    means = pmc_means(dirs, kernel)
+    durations = {r["name"]: r["avg_us"] for r in kernel_stats(trace)} if trace else {}
+    out = []
+    for k, cs in sorted(means.items()):
+        out.append(k)
+        for c, v in sorted(cs.items()):
+            out.append(f"    {c:34s} {v:18.2f}")
+        wc = cs.get("SQ_WAVE_CYCLES")
+        if wc:
+            if "SQ_WAIT_INST_ANY" in cs:
+                out.append(f"    {'-> waiting on operands':34s} {100.0 * cs['SQ_WAIT_INST_ANY'] / wc:17.1f}% of wave cycles")
+            if "SQ_ACTIVE_INST_ANY" in cs:
+                out.append(f"    {'-> issuing':34s} {100.0 * cs['SQ_ACTIVE_INST_ANY'] / wc:17.1f}% of wave cycles")
+            if "SQ_WAIT_INST_LDS" in cs:
+                out.append(f"    {'-> waiting on LDS':34s} {100.0 * cs['SQ_WAIT_INST_LDS'] / wc:17.1f}% of wave cycles")
+        if "SQ_INSTS_VALU_MFMA_MOPS_I8" in cs:
+            ops = cs["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512.0
+            line = f"    {'-> int8 MFMA ops per dispatch':34s} {ops:18.4e}"
+            us = next((d for n, d in durations.items() if n == k), None)
+            if us:
+                line += f"   at {us:.2f} us: {ops / (us * 1e-6) / 1e12:.1f} TOPS (dense int8 peak 5000)"
+            out.append(line)
+    return out
+
+
 def main(argv: list[str] | None = None) -> int:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = p.add_subparsers(dest="cmd", required=True)
@@ -94,12 +127,18 @@ def main(argv: list[str] | None = None) -> int:
         tr.add_argument(f"--{a}", required=True)
     tr.add_argument("--calib-bytes", type=int, required=True)
     tr.add_argument("--kernel", required=True)
+    cn = sub.add_parser("counters")
+    cn.add_argument("dirs", nargs="+")
+    cn.add_argument("--kernel", required=True)
+    cn.add_argument("--trace")
     a = p.parse_args(argv)
     if a.cmd == "trace":
         print(f"{'kernel':72s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'pct':>6s}")
         for r in kernel_stats(a.dir):
             print(f"{r['name'][:72]:72s} {r['calls']:6d} {r['avg_us']:9.2f} {r['min_us']:9.2f} "
                   f"{r['max_us']:9.2f} {r['pct']:6.2f}")
+    elif a.cmd == "counters":
+        print("\n".join(counters(a.dirs, a.kernel, a.trace)))
     elif a.cmd == "pmc":
         for k, cs in pmc_means(a.dirs, a.kernel).items():
             print(k)

@@ -56,6 +56,9 @@ def parse() -> argparse.Namespace:
                    help="tokens timed per CPU-baseline mode (the median is reported)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                    help="only run 20 device-to-device copies of BYTES (no layer)")
+    p.add_argument("--residency-mib", type=int, default=0, metavar="MIB",
+                   help="only run the layer with its experts in host memory and at most MIB of "
+                        "them resident (misses streamed through pinned staging); prints its own line")
     return p.parse_args()
 
 
@@ -254,6 +257,66 @@ def device_routed_experts(layer, pool, table) -> float:
     return float(np.mean(counts))
 
 
+def residency_run(args) -> int:
+    """The layer over experts held in host memory, made resident on demand under a residency
+    ceiling of args.residency_mib MiB (Governor-reserved): per-layer time including routing,
+    misses and their uploads, and the host-to-device rate of the uploads (staging copy, DMA and
+    repacking), next to the 7.2 GB/s the reference's CUDA tier measured for its pinned copies
+    (docs/reports/D2B_DEVICE_RESIDENCY_VALIDATION.md:49)."""
+    import torch
+
+    from vastloom_amd import _lib
+    from vastloom_amd.accel import Governor, default_limits
+    from vastloom_amd.residency import HostExpert, ResidentMoeLayer
+    from vastloom_amd.workloads import workload
+
+    wl = workload(args.workload)
+    if wl.routing in ("single", "zipf_table"):
+        raise SystemExit("the residency run needs a routed workload")
+    H, F = wl.width, wl.intermediate
+    def host_expert(ex):
+        return HostExpert(wl.gate_type, wl.down_type, H, F, ex.gate, ex.up, ex.down)
+
+    host = [host_expert(wl.expert(e)) for e in range(wl.experts)]
+    shared = wl.shared()
+    sh = host_expert(shared) if shared else None
+    ceiling = args.residency_mib << 20
+    gov = Governor(default_limits(vram_hard_limit=ceiling + (512 << 20), staging_hard_limit=1 << 30))
+    sem = _lib.SEM_QWEN if wl.semantics == "qwen" else _lib.SEM_DEEPSEEK
+    routing = _lib.ROUTE_SOFTMAX if wl.routing == "softmax" else _lib.ROUTE_LEARNED
+    layer = ResidentMoeLayer(gov, host, sh, width=H, intermediate=F, top_k=wl.top_k,
+                             gate_type=wl.gate_type, down_type=wl.down_type, semantics=sem,
+                             routing=routing, score_fn=wl.score_fn,
+                             router=torch.from_numpy(wl.router()),
+                             maximum_resident_bytes=ceiling, staging_bytes=64 << 20)
+    pool = torch.from_numpy(token_pool(wl, args.token_pool)).cuda()
+    for i in range(args.warmup):
+        layer.forward(pool[i % len(pool)])
+    s0 = layer.stats()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        layer.forward(pool[(args.warmup + i) % len(pool)])
+    elapsed = time.perf_counter() - t0
+    s1 = layer.stats()
+    up_bytes = s1["uploaded_bytes"] - s0["uploaded_bytes"]
+    up_ms = s1["upload_ms"] - s0["upload_ms"]
+    n_exp = routed_experts(wl) + (1 if wl.has_shared else 0)
+    print(json.dumps({
+        "metric": "MoE layer with experts streamed from host memory under a residency ceiling",
+        "workload": wl.name, "ceiling_mib": args.residency_mib, "steps": args.steps,
+        "us_per_layer": round(elapsed / args.steps * 1e6, 1),
+        "route_us": round((s1["route_ms"] - s0["route_ms"]) / args.steps * 1e3, 1),
+        "residency_us": round((s1["residency_ms"] - s0["residency_ms"]) / args.steps * 1e3, 1),
+        "layer_us": round((s1["layer_ms"] - s0["layer_ms"]) / args.steps * 1e3, 1),
+        "uploaded_bytes_per_layer": int(up_bytes / args.steps),
+        "miss_rate": round(up_bytes / args.steps / (n_exp * wl.expert_bytes()), 3),
+        "h2d_gbs": round(up_bytes / (up_ms * 1e-3) / 1e9, 2) if up_ms else None,
+        "reference_h2d_gbs": 7.2,
+        "evicted": s1["evicted"] - s0["evicted"], "resident_matrices": s1["resident_matrices"]}))
+    layer.close()
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -262,6 +325,8 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.residency_mib:
+        return residency_run(args)
     import torch
 
     from vastloom_amd import ops

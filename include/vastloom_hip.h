@@ -206,6 +206,17 @@ int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes);
 int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
                  uint64_t workspace_bytes, void* stream);
 
+/* Routes every token of a layer without running its experts: the router logits, scores and
+ * selection (learned, table or softmax routing; not VL_ROUTE_GIVEN) of vl_moe_layer, with the routes
+ * left in the workspace for vl_moe_read_routes and refused tokens in its status word
+ * (vl_read_status). inputs->experts is not read (may be NULL); out is not written. The reference
+ * routes a layer before its provider acquires the selected experts (moe_forward's router-first
+ * batch, src/inference/deepseek_v4_graph.cpp:1971-2029): a caller whose experts live in host memory
+ * routes first, makes the selected experts resident, then runs vl_moe_layer with
+ * VL_ROUTE_GIVEN and these routes. */
+int vl_moe_route(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
+                 uint64_t workspace_bytes, void* stream);
+
 /* vl_moe_layer without a caller-owned workspace, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
  * counterpart in the reference. The workspace is a fixed 64 MiB array in the library's device

@@ -53,6 +53,7 @@ _SIGNATURES = {
     "vl_read_status": [_P, _P, C.POINTER(_U32)],
     "vl_moe_workspace": [_P, C.POINTER(_U64)],
     "vl_moe_layer": [_P, _P, _P, _U64, _P],
+    "vl_moe_route": [_P, _P, _P, _U64, _P],
     "vl_moe_layer_noalloc": [_P, _P, _P],
     "vl_moe_noalloc_status": [_P, _P],
     "vl_moe_read_routes": [_P, _P, _P, _P, _P],

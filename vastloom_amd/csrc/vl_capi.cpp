@@ -213,6 +213,28 @@ int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void*
     return e == hipSuccess ? VL_OK : hip_fail(e, "MoE launch");
 }
 
+int vl_moe_route(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
+                 uint64_t workspace_bytes, void* stream) {
+    vl::MoeShape s;
+    if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");
+    if (s.routing == vl::kRouteGiven) return fail(VL_INVALID_ARGUMENT, "given routes need no routing");
+    if (!inputs || !inputs->router || !inputs->x || !workspace)
+        return fail(VL_INVALID_ARGUMENT, "null input pointer");
+    if (s.routing == vl::kRouteTable && !inputs->table_ids)
+        return fail(VL_INVALID_ARGUMENT, "table routing needs table ids");
+    const uint32_t blocks = blocks_or_fail();
+    if (!blocks) return VL_UNSUPPORTED;
+    const vl::MoeWorkspace ws = vl::moe_workspace_layout(s, blocks, workspace);
+    if (workspace_bytes < ws.bytes)
+        return fail(VL_INVALID_ARGUMENT, "workspace of %llu bytes is below the %llu needed",
+                    (unsigned long long)workspace_bytes, (unsigned long long)ws.bytes);
+    // The experts are not read: the table pointer is only carried.
+    const vl::MoeInputs in{reinterpret_cast<const vl::MoeExpert*>(inputs->experts), inputs->router, inputs->bias,
+                           inputs->table_ids, nullptr, nullptr, inputs->x, inputs->out};
+    const hipError_t e = vl::launch_moe_route(s, in, ws, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? VL_OK : hip_fail(e, "MoE routing launch");
+}
+
 int vl_moe_layer_noalloc(const vl_moe_config* config, const vl_moe_inputs* inputs, void* stream) {
     vl::MoeShape s;
     if (!to_shape(config, &s)) return fail(VL_INVALID_ARGUMENT, "invalid MoE configuration");

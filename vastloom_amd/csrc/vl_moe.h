@@ -100,6 +100,11 @@ hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace
                       hipStream_t stream, hipEvent_t* events = nullptr,
                       hipEvent_t* kernel_events = nullptr);
 
+// Routes every token without running the experts: the router stage and the per-token routing of
+// the layer, leaving the routes (and the refusal bits of the status word) in the workspace. For
+// callers that must know the selected experts before their weights are on the device.
+hipError_t launch_moe_route(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& ws, hipStream_t stream);
+
 // Bytes of the per-device workspace that vl_moe_layer_noalloc uses instead of a caller's buffer.
 constexpr uint64_t kStaticWorkspaceBytes = 64ull << 20;
 

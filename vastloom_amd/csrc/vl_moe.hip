@@ -1958,6 +1958,32 @@ static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, con
     return hipSuccess;
 }
 
+hipError_t launch_moe_route(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w, hipStream_t st) {
+    if (!moe_shape_ok(s) || w.blocks == 0 || s.routing == kRouteGiven) return hipErrorInvalidValue;
+    hipError_t e;
+    if (w.grouped) {
+        // As the grouped layer: the router kernel zeroes the status and counters and forms the
+        // activation limbs; the logits come from the tiled product.
+        MoeShape sx = s;
+        sx.routing = kRouteGiven;
+        hipLaunchKernelGGL(k_moe_router, dim3(w.xblocks, (s.tokens + kMoeMaxTokens - 1u) / kMoeMaxTokens), dim3(256), 0,
+                           st, sx, in, w);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_moe_logits_part,
+                           dim3((s.experts + kLgE - 1u) / kLgE, (s.tokens + kLgT - 1u) / kLgT, w.lg_slices),
+                           dim3(256), 0, st, s, in, w);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        const uint64_t n = (uint64_t)s.tokens * s.experts;
+        hipLaunchKernelGGL(k_moe_logits_finish, dim3((uint32_t)((n + 255u) / 256u)), dim3(256), 0, st, s, in, w);
+    } else {
+        hipLaunchKernelGGL(k_moe_router, dim3(s.experts + w.xblocks), dim3(256), 0, st, s, in, w);
+    }
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_moe_route_many, dim3((s.tokens + kStreamWaves - 1u) / kStreamWaves), dim3(kStreamThreads),
+                       0, st, s, in, w);
+    return hipGetLastError();
+}
+
 hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
                       hipStream_t st, hipEvent_t* ev, hipEvent_t* kev) {
     if (!moe_shape_ok(s) || w.blocks == 0) return hipErrorInvalidValue;

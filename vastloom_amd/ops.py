@@ -183,6 +183,22 @@ class MoeLayer:
             raise_on_status(ws, s, "moe_layer")
         return out
 
+    def route(self, x: torch.Tensor, *, table_ids: torch.Tensor | None = None,
+              stream=None) -> tuple[np.ndarray, np.ndarray]:
+        """Routes the tokens without running the experts (vl_moe_route) and returns the routes:
+        expert ids and weights [tokens, top_k], synchronising the stream. Refused tokens raise."""
+        x2 = x.reshape(-1, self.width).contiguous()
+        tokens = x2.shape[0]
+        ws = self.workspace(tokens)
+        cfg = self.config(tokens)
+        p = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
+        inputs = _lib.MoeInputs(self.expert_table.data_ptr(), p(self.router), p(self.bias),
+                                p(table_ids), 0, 0, x2.data_ptr(), 0)
+        s = _stream(stream)
+        call("vl_moe_route", C.byref(cfg), C.byref(inputs), ws.data_ptr(), ws.numel(), s)
+        raise_on_status(ws, s, "moe_route")
+        return self.routes(tokens, stream)
+
     def routes(self, tokens: int, stream=None) -> tuple[np.ndarray, np.ndarray]:
         ids = np.zeros((tokens, self.top_k), np.uint32)
         w = np.zeros((tokens, self.top_k), np.float32)

@@ -27,6 +27,7 @@
 #include "vl_moe.h"
 #include "vl_moe_dev.h"
 #include "vl_moe_token.h"
+#include "vl_moe_wide.h"
 #include "vl_stream.h"
 
 namespace vl {
@@ -83,7 +84,9 @@ MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base
     MoeWorkspace w{};
     w.base = static_cast<uint8_t*>(base);
     w.grouped = s.tokens > kMoeMaxTokens ? 1u : 0u;
+    w.wide = w.grouped && wide_shape_ok(s) ? 1u : 0u;
     w.max_active = w.grouped ? (uint32_t)max_groups(s) : max_active(s);
+    w.max_items = w.wide ? w.max_active : 0u;
     w.slots = w.grouped ? kMoeMaxTokens : limb_slots(s.tokens);
     w.xslots = w.grouped ? s.tokens : w.slots;
     w.estride = w.grouped ? s.tokens : 8u;
@@ -99,7 +102,9 @@ MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base
     const uint64_t per_block = blocks ? (A * w.tiles_dn * UJ + blocks - 1u) / blocks : 1u;
     const uint64_t stage = (per_block > 0 ? per_block - 1u : 0u) / (w.tiles_dn * UJ) + 2u;
     w.stage = (uint32_t)(stage < A ? stage : A);
-    w.counters = (uint32_t)(A * w.tiles_gu + A * w.tiles_dn + w.tiles_dn + A * w.hblocks * 8u);
+    // The fp16 kernels use neither the hand-off counters and records nor the int8 limbs.
+    const uint64_t limbs = w.wide ? 0u : 1u;
+    w.counters = (uint32_t)(limbs * (A * w.tiles_gu + A * w.tiles_dn + w.tiles_dn + A * w.hblocks * 8u));
     uint64_t o = 0;
     w.off_header = o; o = align256(o + sizeof(MoeHeader));
     w.off_logits = o; o = align256(o + T * s.experts * 4u);
@@ -111,12 +116,18 @@ MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base
     w.off_combine = o; o = align256(o + T * (K + 1) * sizeof(CombineEntry));
     w.off_xexp = o; o = align256(o + (uint64_t)w.xblocks * w.estride * 4u);
     w.off_xflags = o; o = align256(o + (uint64_t)w.xblocks * w.estride * 4u);
-    w.off_xlimbs = o; o = align256(o + (uint64_t)(s.width / 32u) * w.xslots * 128u);
+    w.off_xlimbs = o; o = align256(o + limbs * (s.width / 32u) * w.xslots * 128u);
     w.off_counters = o; o = align256(o + (uint64_t)w.counters * 4u);
-    w.off_rec_gu = o; o = align256(o + (w.waves + A * w.tiles_gu) * 2u * NT * 64u * 4u);
-    w.off_rec_dn = o; o = align256(o + (w.waves + A * w.tiles_dn) * NT * 64u * 4u);
-    w.off_h = o; o = align256(o + A * NT * s.inter * 4u);
-    w.off_hslab = o; o = align256(o + (uint64_t)blocks * w.stage * down_expert_bytes(s.inter, w.slots));
+    w.off_rec_gu = o; o = align256(o + limbs * (w.waves + A * w.tiles_gu) * 2u * NT * 64u * 4u);
+    w.off_rec_dn = o; o = align256(o + limbs * (w.waves + A * w.tiles_dn) * NT * 64u * 4u);
+    w.off_h = o; o = align256(o + limbs * A * NT * s.inter * 4u);
+    w.off_hslab = o; o = align256(o + limbs * blocks * w.stage * down_expert_bytes(s.inter, w.slots));
+    const uint64_t wide = w.wide ? 1u : 0u;
+    w.off_x16 = o; o = align256(o + wide * T * s.width * 4u);
+    w.off_xsc = o; o = align256(o + wide * T * w.xblocks * 4u);
+    w.off_h16 = o; o = align256(o + wide * A * kMoeMaxTokens * s.inter * 4u);
+    w.off_hsc = o; o = align256(o + wide * A * kMoeMaxTokens * w.hblocks * 4u);
+    w.off_items = o; o = align256(o + wide * w.max_items * sizeof(WideItem));
     w.off_ypart = o; o = align256(o + A * NT * (uint64_t)s.width * 4u);
     w.off_gweights = o; o = align256(o + (w.grouped ? A * sizeof(MoeExpert) : 0u));
     // Grouped layers: f64 partial router logits of each column slice, [slice][token][expert].
@@ -1460,10 +1471,49 @@ __global__ void __launch_bounds__(kStreamThreads) k_moe_plan(const MoeShape s, c
             *gp(ce + 1) = __float_as_uint(1.0f);
         }
     }
+    // The fp16 kernels' items: each expert's entries in runs of up to 2 * kWideGroups, in entry
+    // order (an exclusive block scan of the run counts, as for the groups), then the shared
+    // expert's.
+    uint32_t nitems = 0;
+    if (w.wide) {
+        constexpr uint32_t RUN = 2u * kWideGroups;
+        const uint32_t g = tid < E ? (cnt[tid] + kMoeMaxTokens - 1u) / kMoeMaxTokens : 0u;
+        const uint32_t ni = (g + RUN - 1u) / RUN;
+        uint32_t inc = ni;
+#pragma unroll
+        for (uint32_t d = 1; d < 64u; d <<= 1) {
+            const uint32_t v = (uint32_t)__shfl_up((int)inc, d);
+            if (lane >= d) inc += v;
+        }
+        if (lane == 63u) flags[wave] = inc;
+        __syncthreads();
+        uint32_t before = 0, all = 0;
+        for (uint32_t v = 0; v < nw; ++v) {
+            const uint32_t f = flags[v];
+            before += v < wave ? f : 0u;
+            all += f;
+        }
+        before += inc - ni;
+        WideItem* items = ws_ptr<WideItem>(w, w.off_items);
+        for (uint32_t i = 0; i < ni; ++i) {
+            const uint32_t left = g - RUN * i;
+            items[before + i] = WideItem{base[tid] + RUN * i, left < RUN ? left : RUN, {0u, 0u}};
+        }
+        nitems = all;
+        if (s.has_shared) {
+            const uint32_t gs = (T + kMoeMaxTokens - 1u) / kMoeMaxTokens, ns = (gs + RUN - 1u) / RUN;
+            for (uint32_t i = tid; i < ns; i += nth) {
+                const uint32_t left = gs - RUN * i;
+                items[all + i] = WideItem{routed_groups + RUN * i, left < RUN ? left : RUN, {0u, 0u}};
+            }
+            nitems += ns;
+        }
+    }
     if (tid == 0) {
         const bool bad = (load_shared_u32(&hdr->status) & kStatusBadRoute) != 0;
         const uint32_t total = routed_groups + (s.has_shared ? (T + kMoeMaxTokens - 1u) / kMoeMaxTokens : 0u);
         *gp(&hdr->n_active) = bad ? 0u : total;
+        *gp(&hdr->reserved[0]) = bad ? 0u : nitems;
         if (any_nonfinite) or_bits(&hdr->status, kStatusNonFiniteInput);
     }
 }
@@ -1909,14 +1959,18 @@ static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, con
         if (kev && stage < kStageCount) (void)hipEventRecord(kev[2u * stage], st);  // start
     };
     mark(kStageRouter);
-    // The router kernel zeroes the counters and forms the activation limbs; the logits come
-    // from the tiled product.
+    // The router kernel zeroes the counters and forms the activation limbs (the fp16 kernels'
+    // activations come from k_wide_prep); the logits come from the tiled product.
     const uint32_t groups = (s.tokens + kMoeMaxTokens - 1u) / kMoeMaxTokens;
     MoeShape sx = s;
     sx.routing = kRouteGiven;
-    hipLaunchKernelGGL(k_moe_router, dim3(w.xblocks, groups), dim3(256), 0, st, sx, in, w);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e;
+    if (w.wide) {
+        if ((e = launch_wide_prep(s, in, w, st)) != hipSuccess) return e;
+    } else {
+        hipLaunchKernelGGL(k_moe_router, dim3(w.xblocks, groups), dim3(256), 0, st, sx, in, w);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     if (s.routing != kRouteGiven) {
         hipLaunchKernelGGL(k_moe_logits_part,
                            dim3((s.experts + kLgE - 1u) / kLgE, (s.tokens + kLgT - 1u) / kLgT, w.lg_slices),
@@ -1934,6 +1988,16 @@ static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, con
     hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(kStreamThreads), plan_shm, st, s, in, w);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     mark(kStageGateUp);
+    if (w.wide) {
+        if ((e = launch_wide_gateup(s, in, w, st)) != hipSuccess) return e;
+        mark(kStageDown);
+        if ((e = launch_wide_down(s, in, w, st)) != hipSuccess) return e;
+        const uint64_t outs = (uint64_t)s.tokens * s.width;
+        hipLaunchKernelGGL(k_moe_combine, dim3((uint32_t)((outs / 4u + 255u) / 256u)), dim3(256), 0, st, s, in, w);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        mark(kStageCount);
+        return hipSuccess;
+    }
     switch (s.gate_type) {
         case VL_TYPE_IQ2_XXS: e = launch_gateup_grouped<VL_TYPE_IQ2_XXS>(s, in, w, st); break;
         case VL_TYPE_IQ3_XXS: e = launch_gateup_grouped<VL_TYPE_IQ3_XXS>(s, in, w, st); break;
@@ -1966,9 +2030,13 @@ hipError_t launch_moe_route(const MoeShape& s, const MoeInputs& in, const MoeWor
         // activation limbs; the logits come from the tiled product.
         MoeShape sx = s;
         sx.routing = kRouteGiven;
-        hipLaunchKernelGGL(k_moe_router, dim3(w.xblocks, (s.tokens + kMoeMaxTokens - 1u) / kMoeMaxTokens), dim3(256), 0,
-                           st, sx, in, w);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (w.wide) {
+            if ((e = launch_wide_prep(s, in, w, st)) != hipSuccess) return e;
+        } else {
+            hipLaunchKernelGGL(k_moe_router, dim3(w.xblocks, (s.tokens + kMoeMaxTokens - 1u) / kMoeMaxTokens),
+                               dim3(256), 0, st, sx, in, w);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
         hipLaunchKernelGGL(k_moe_logits_part,
                            dim3((s.experts + kLgE - 1u) / kLgE, (s.tokens + kLgT - 1u) / kLgT, w.lg_slices),
                            dim3(256), 0, st, s, in, w);

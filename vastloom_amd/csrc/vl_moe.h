@@ -73,8 +73,8 @@ struct MoeWorkspace {
     uint64_t off_header, off_logits, off_scores, off_keys, off_route_idx, off_route_w, off_active, off_combine,
         off_xexp, off_xflags, off_xlimbs, off_counters, off_rec_gu, off_rec_dn, off_h,
         off_hslab, off_ypart, off_gweights, off_lgpart, off_trec;
-    // Grouped layers on the fp16 kernels: activations and h as hi/lo fp16 [row][2][cols] with
-    // one scale per row and 256-column block, and the item list.
+    // Grouped layers on the fp16 kernels: activations and h as hi/lo fp16 [row][2][cols], with one
+    // scale per token (x) and per row and 256-column block (h), and the item list.
     uint64_t off_x16, off_xsc, off_h16, off_hsc, off_items;
     uint32_t grouped;                                 // more than kMoeMaxTokens tokens
     uint32_t wide;                                    // grouped, on the fp16 kernels

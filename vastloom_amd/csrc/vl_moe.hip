@@ -124,7 +124,7 @@ MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base
     w.off_hslab = o; o = align256(o + limbs * blocks * w.stage * down_expert_bytes(s.inter, w.slots));
     const uint64_t wide = w.wide ? 1u : 0u;
     w.off_x16 = o; o = align256(o + wide * T * s.width * 4u);
-    w.off_xsc = o; o = align256(o + wide * T * w.xblocks * 4u);
+    w.off_xsc = o; o = align256(o + wide * T * 4u);
     w.off_h16 = o; o = align256(o + wide * A * kMoeMaxTokens * s.inter * 4u);
     w.off_hsc = o; o = align256(o + wide * A * kMoeMaxTokens * w.hblocks * 4u);
     w.off_items = o; o = align256(o + wide * w.max_items * sizeof(WideItem));

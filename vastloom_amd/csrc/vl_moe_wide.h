@@ -10,11 +10,12 @@
 
 namespace vl {
 
-// MFMA groups of sixteen tokens per item, waves per block (one 32-row tile each: 256 rows),
-// and output slabs of 256 rows per down block.
+// MFMA groups of sixteen tokens per item, waves per block (gate/up: one 32-row tile of each
+// matrix per wave, 256 rows; down: two tiles per wave, 512 rows), and output slabs of 512 rows
+// per down block.
 constexpr uint32_t kWideGroups = 2;
 constexpr uint32_t kWideWaves = 8;
-constexpr uint32_t kWideDownSlabs = 4;
+constexpr uint32_t kWideDownSlabs = 2;
 
 // One item of the group list: a run of up to 2 * kWideGroups consecutive entries of one expert.
 struct WideItem {

@@ -11,7 +11,7 @@
 //   k_wide_gateup  one block per (item, 256 rows of gate and up): the item's tokens (up to two
 //                  groups of sixteen) against every column, SwiGLU of the semantics, then h of
 //                  the block's 256 rows as hi/lo fp16 with one scale per token
-//   k_wide_down    one block per (item, run of 256-row slabs of the output): the item's h against
+//   k_wide_down    one block per (item, run of 512-row slabs of the output): the item's h against
 //                  the down rows, each (entry, slot)'s output rows into the partial-output array
 //                  that k_moe_combine adds in the reference's combine order
 //
@@ -495,7 +495,7 @@ __global__ void __launch_bounds__(kWideWaves * 64u) k_wide_down(const MoeShape s
     extern __shared__ __align__(16) uint8_t lds[];
     const MoeHeader* hdr = ws_ptr<const MoeHeader>(w, w.off_header);
     const uint32_t nitems = uni(*gp(&hdr->reserved[0]));
-    const uint32_t slabs = s.width / 256u, runs = (slabs + kWideDownSlabs - 1u) / kWideDownSlabs;
+    const uint32_t slabs = (s.width + 511u) / 512u, runs = (slabs + kWideDownSlabs - 1u) / kWideDownSlabs;
     const uint32_t item = blockIdx.x / runs, run = blockIdx.x - item * runs;
     if (item >= nitems) return;
     const WideItem it = ws_ptr<const WideItem>(w, w.off_items)[item];
@@ -522,25 +522,35 @@ __global__ void __launch_bounds__(kWideWaves * 64u) k_wide_down(const MoeShape s
     float* ypart = ws_ptr<float>(w, w.off_ypart);
     const uint32_t H = s.width;
     __syncthreads();  // the table
+    // Each wave takes two tiles of a 512-row slab (rows 32 (16 slab + wave) and 256 rows further),
+    // so that every A fragment read from LDS feeds two MFMAs. A slab past the last full 256 rows
+    // computes its first tile twice and stores it once.
+    const uint32_t tiles = L.tiles;
     for (uint32_t sl0 = run * kWideDownSlabs; sl0 < slabs && sl0 < (run + 1u) * kWideDownSlabs; ++sl0) {
-        const uint32_t tile = sl0 * kWideWaves + wave;
-        const uint8_t* const p0[1] = {d0 + (uint64_t)tile * L.superblocks * 2048u};
-        const uint8_t* const p1[1] = {d0 + L.plane1 + (uint64_t)tile * L.superblocks * 64u};
-        float acc[1][kWideGroups][8];
+        const uint32_t t0 = sl0 * 2u * kWideWaves + wave, t1r = t0 + kWideWaves;
+        const uint32_t t1 = t1r < tiles ? t1r : t0;
+        const uint8_t* const p0[2] = {d0 + (uint64_t)t0 * L.superblocks * 2048u, d0 + (uint64_t)t1 * L.superblocks * 2048u};
+        const uint8_t* const p1[2] = {d0 + L.plane1 + (uint64_t)t0 * L.superblocks * 64u,
+                                      d0 + L.plane1 + (uint64_t)t1 * L.superblocks * 64u};
+        float acc[2][kWideGroups][8];
 #pragma unroll
-        for (uint32_t g = 0; g < kWideGroups; ++g)
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int q = 0; q < 8; ++q) acc[0][g][q] = 0.0f;
-        wide_rows<1, true>(lds, st, L.superblocks, groups, p0, p1, acc);
-        const uint32_t row = tile * 32u + n;
+            for (uint32_t g = 0; g < kWideGroups; ++g)
+#pragma unroll
+                for (int q = 0; q < 8; ++q) acc[mt][g][q] = 0.0f;
+        wide_rows<2, true>(lds, st, L.superblocks, groups, p0, p1, acc);
 #pragma unroll
         for (uint32_t g = 0; g < kWideGroups; ++g) {
             if (g >= groups) break;
 #pragma unroll
             for (uint32_t q = 0; q < 8u; ++q) {
                 const uint32_t t = wide_pair_slot(q, hh), k = 2u * g + t / 8u, sl = t % 8u;
-                if (k < ne && sl < ntok[k])
-                    ypart[((uint64_t)(a0 + k) * kMoeMaxTokens + sl) * H + row] = acc[0][g][q];
+                if (k < ne && sl < ntok[k]) {
+                    float* y = ypart + ((uint64_t)(a0 + k) * kMoeMaxTokens + sl) * H;
+                    y[t0 * 32u + n] = acc[0][g][q];
+                    if (t1r < tiles) y[t1r * 32u + n] = acc[1][g][q];
+                }
             }
         }
     }
@@ -573,7 +583,7 @@ hipError_t launch_wide_gateup(const MoeShape& s, const MoeInputs& in, const MoeW
 hipError_t launch_wide_down(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w, hipStream_t st) {
     hipError_t e = ensure_dynamic_lds((const void*)k_wide_down, kWideLdsBytes);
     if (e != hipSuccess) return e;
-    const uint32_t runs = (s.width / 256u + kWideDownSlabs - 1u) / kWideDownSlabs;
+    const uint32_t runs = ((s.width + 511u) / 512u + kWideDownSlabs - 1u) / kWideDownSlabs;
     hipLaunchKernelGGL(k_wide_down, dim3(w.max_items * runs), dim3(kWideWaves * 64u), kWideLdsBytes, st, s, in, w);
     return hipGetLastError();
 }

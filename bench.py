@@ -86,12 +86,20 @@ def measured_traffic(kernel: str, workload: str) -> tuple[int | None, str | None
     return (int(m.group(1)), str(path.relative_to(ROOT))) if m else (None, None)
 
 
+def wide_path(wl) -> bool:
+    """Whether a grouped layer of this workload runs on the fp16 kernels (IQ2_XXS gate, up and
+    down; widths of whole 256-column blocks)."""
+    return (wl.tokens > 8 and wl.gate_type == 16 and wl.down_type == 16 and wl.width % 256 == 0
+            and wl.intermediate % 256 == 0)
+
+
 def gateup_kernel(wl) -> str:
     """The gate/up kernel a layer of this workload runs (single-token layers of the learned,
     softmax and given routings take the single-token kernels, except IQ3_XXS; 2-8 tokens the
-    token-slot stream kernels; more tokens the grouped path)."""
+    token-slot stream kernels; more tokens the grouped path: the fp16 kernels for IQ2_XXS, the
+    int8 ones otherwise)."""
     if wl.tokens > 8:
-        return "k_moe_gateup_grouped"
+        return "k_wide_gateup" if wide_path(wl) else "k_moe_gateup_grouped"
     if wl.tokens == 1 and wl.routing != "zipf_table" and 18 not in (wl.gate_type, wl.down_type):
         return "k_tok_gateup"
     return "k_moe_gateup"
@@ -430,7 +438,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": f"{TYPE(wl.gate_type).lower()}/{TYPE(wl.down_type).lower()} weights, "
-                 "i8xi8->i32 MFMA, f32 accumulate",
+                 + ("f16xf16->f32 MFMA (exact fp16 weights, hi/lo fp16 activations)" if wide_path(wl)
+                    else "i8xi8->i32 MFMA, f32 accumulate"),
         "data": f"synthetic (seeded PCG64; uniform random {TYPE(wl.gate_type)}/{TYPE(wl.down_type)} "
                 f"payload bytes, |N(0,1)|*{wl.scale_factor} fp16 scales, N(0,0.02) router, N(0,1) tokens)",
         "config": {"workload": f"{wl.name}: {wl.model} {wl.kind}, width {wl.width}, expert "

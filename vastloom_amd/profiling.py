@@ -87,8 +87,9 @@ def traffic(fetch: str, write: str, calib_fetch: str, calib_write: str, calib_by
 def counters(dirs: list[str], kernel: str, trace: str | None = None) -> list[str]:
     """Mean counter values per dispatch of each kernel matching `kernel`, and what follows from them:
     the share of wave cycles spent waiting on an instruction's operands (SQ_WAIT_INST_ANY, mostly
-    s_waitcnt) and issuing (SQ_ACTIVE_INST_ANY); int8 MFMA operations (SQ_INSTS_VALU_MFMA_MOPS_I8
-    counts units of 512) and, with the kernel's average duration from a trace, their rate."""
+    s_waitcnt) and issuing (SQ_ACTIVE_INST_ANY); int8 and f16 MFMA operations
+    (SQ_INSTS_VALU_MFMA_MOPS_I8 / _F16 count units of 512) and, with the kernel's average duration
+    from a trace, their rate against the dense peak."""
     means = pmc_means(dirs, kernel)
     durations = {r["name"]: r["avg_us"] for r in kernel_stats(trace)} if trace else {}
     out = []
@@ -104,12 +105,15 @@ def counters(dirs: list[str], kernel: str, trace: str | None = None) -> list[str
                 out.append(f"    {'-> issuing':34s} {100.0 * cs['SQ_ACTIVE_INST_ANY'] / wc:17.1f}% of wave cycles")
             if "SQ_WAIT_INST_LDS" in cs:
                 out.append(f"    {'-> waiting on LDS':34s} {100.0 * cs['SQ_WAIT_INST_LDS'] / wc:17.1f}% of wave cycles")
-        if "SQ_INSTS_VALU_MFMA_MOPS_I8" in cs:
-            ops = cs["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512.0
-            line = f"    {'-> int8 MFMA ops per dispatch':34s} {ops:18.4e}"
+        for counter, label, peak in (("SQ_INSTS_VALU_MFMA_MOPS_I8", "int8", "dense int8 peak 5000 TOPS"),
+                                     ("SQ_INSTS_VALU_MFMA_MOPS_F16", "f16", "dense f16 peak 2500 TFLOP/s")):
+            if counter not in cs:
+                continue
+            ops = cs[counter] * 512.0
+            line = f"    {'-> ' + label + ' MFMA ops per dispatch':34s} {ops:18.4e}"
             us = next((d for n, d in durations.items() if n == k), None)
             if us:
-                line += f"   at {us:.2f} us: {ops / (us * 1e-6) / 1e12:.1f} TOPS (dense int8 peak 5000)"
+                line += f"   at {us:.2f} us: {ops / (us * 1e-6) / 1e12:.1f} T/s ({peak})"
             out.append(line)
     return out
 

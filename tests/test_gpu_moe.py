@@ -233,6 +233,40 @@ def test_bad_table_route_is_refused(ops, lib, oracle):
             layer.forward(x, table_ids=torch.tensor(bad, dtype=torch.int32).cuda())
 
 
+@pytest.mark.parametrize("tokens", [1, 3, 20])
+@pytest.mark.parametrize("case", ["bias", "table_logit"])
+def test_nonfinite_routing_inputs_are_refused(ops, lib, oracle, tokens, case):
+    """A non-finite selection bias (learned routing), or a non-finite logit of an expert the table
+    does not select, refuses the layer, as the reference's require_finite of the bias and the
+    logits does (deepseek_v4_reference.cpp:235-238, :161): single-token, token-slot and grouped
+    paths."""
+    print(f"[moe refuse] {case} tokens={tokens}", flush=True)
+    rng = np.random.default_rng(7 + tokens)
+    from vastloom_amd.workloads import MoeWorkload
+    H, F, E, K = 256, 256, 6, 2
+    wl = MoeWorkload("refuse", 15, H, F, E, K, tokens, IQ2_XXS, IQ2_XXS, 0.01, "deepseek")
+    experts = [make_expert(rng, IQ2_XXS, IQ2_XXS, H, F) for _ in range(E)]
+    router = wl.router()
+    x = torch.from_numpy(rng.standard_normal((tokens, H)).astype(np.float32)).cuda()
+    if case == "bias":
+        bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+        ok = _device_layer(ops, lib, wl, experts, None, "deepseek", lib.ROUTE_LEARNED, router, bias)
+        assert torch.isfinite(ok.forward(x)).all()
+        bias[E - 1] = np.inf
+        bad = _device_layer(ops, lib, wl, experts, None, "deepseek", lib.ROUTE_LEARNED, router, bias)
+        with pytest.raises(ops.VlError):
+            bad.forward(x)
+    else:
+        table = torch.from_numpy(np.tile(np.array([[0, 1]], np.uint32), (tokens, 1))).cuda()
+        ok = _device_layer(ops, lib, wl, experts, None, "deepseek", lib.ROUTE_TABLE, router)
+        assert torch.isfinite(ok.forward(x, table_ids=table)).all()
+        router = router.copy()
+        router[E - 1, 0] = np.nan  # expert E-1's logit, which the table never selects
+        bad = _device_layer(ops, lib, wl, experts, None, "deepseek", lib.ROUTE_TABLE, router)
+        with pytest.raises(ops.VlError):
+            bad.forward(x, table_ids=table)
+
+
 def _workload_case(wl):
     experts = [wl.expert(e).triple() for e in range(wl.experts)]
     shared = wl.shared().triple() if wl.has_shared else None

@@ -395,7 +395,9 @@ __device__ bool route_topk(const float* lg, const float* scr, const uint32_t* ke
             key[i] = coherent ? load_shared_u32(keys + e) : *gp(keys + e);
             lv[i] = coherent ? load_shared(lg + e) : *gp(lg + e);
             sv[i] = coherent ? load_shared(scr + e) : *gp(scr + e);
-            bad |= !isfinite(lv[i]);
+            // A non-finite logit or selection bias refuses the token (require_finite of the
+            // logits and the bias, deepseek_v4_reference.cpp:235-238, :161).
+            bad |= !isfinite(lv[i]) || key[i] <= 1u;
         }
     }
     // key[] is sorted in place; hid[] follows it. Values are read from lv/sv by id.
@@ -531,20 +533,23 @@ __device__ __forceinline__ bool route_token(const MoeShape& s, const MoeInputs& 
         if (s.routing == kRouteGiven) {
             for (uint32_t k = lane; k < K; k += 64)
                 wt[k] = in.given_weights ? *gp(in.given_weights + t * K + k) : 1.0f;
-        } else if (lane == 0) {
+        } else {
+            // Every logit of the token must be finite, selected or not (activate_gate_logits,
+            // deepseek_v4_reference.cpp:161).
             const float* lg = ws_ptr<const float>(w, w.off_logits) + base;
-            const float* scr = ws_ptr<const float>(w, w.off_scores) + base;
-            double sum = 0.0;
-            float sc[kMoeMaxTopK];
-            for (uint32_t k = 0; k < K; ++k) {
-                const uint32_t e = idx[k];
-                bad |= !isfinite(coherent ? load_shared(lg + e) : *gp(lg + e));
-                sc[k] = coherent ? load_shared(scr + e) : *gp(scr + e);
-                sum += (double)sc[k];
+            for (uint32_t e = lane; e < E; e += 64u) bad |= !isfinite(coherent ? load_shared(lg + e) : *gp(lg + e));
+            if (lane == 0) {
+                const float* scr = ws_ptr<const float>(w, w.off_scores) + base;
+                double sum = 0.0;
+                float sc[kMoeMaxTopK];
+                for (uint32_t k = 0; k < K; ++k) {
+                    sc[k] = coherent ? load_shared(scr + idx[k]) : *gp(scr + idx[k]);
+                    sum += (double)sc[k];
+                }
+                if (!(sum > 0.0) || isinf(sum)) bad = true;
+                for (uint32_t k = 0; k < K; ++k)
+                    wt[k] = (float)((double)sc[k] / sum * (double)s.route_scale);
             }
-            if (!(sum > 0.0) || isinf(sum)) bad = true;
-            for (uint32_t k = 0; k < K; ++k)
-                wt[k] = (float)((double)sc[k] / sum * (double)s.route_scale);
         }
     } else {
         const float* lg = ws_ptr<const float>(w, w.off_logits) + base;

@@ -151,7 +151,13 @@ typedef struct vl_expert_weights {
  * VL_ROUTE_SOFTMAX: float64 softmax over the logits, top-k by probability, optional
  *   renormalisation (qwen38_moe_route, src/inference/qwen3_8_flash_next_reference.cpp:1186-1240).
  * VL_ROUTE_GIVEN: ids and weights supplied in given_ids / given_weights (null ids = expert 0,
- *   null weights = 1). */
+ *   null weights = 1).
+ * Refused (VL_STATUS_BAD_ROUTE): an expert id out of range; a non-finite logit or selection bias
+ * (require_finite, deepseek_v4_reference.cpp:161, :235-238); selected weights that cannot be
+ * normalised. Divergence: a token whose table or given ids repeat an expert is refused here,
+ * while the reference's route_from_indices accepts it and adds each slot's output
+ * (deepseek_v4_graph.cpp:2211-2228); every route the reference's own routers produce has
+ * distinct experts. */
 #define VL_ROUTE_LEARNED 0u
 #define VL_ROUTE_TABLE 1u
 #define VL_ROUTE_SOFTMAX 2u
@@ -198,10 +204,11 @@ int vl_moe_workspace(const vl_moe_config* config, uint64_t* bytes);
 /* One MoE layer: router logits (float64 accumulation), routing, the selected experts' SwiGLU
  * FFNs and the combine, all on the stream with no host synchronisation. Up to 8 tokens share
  * each expert's weight pass; more tokens take the grouped path, which splits each selected
- * expert's tokens, in ascending order, into groups of up to 8 and streams the expert's weights
- * once per group (moe_forward's per-expert token batches, deepseek_v4_graph.cpp:2211-2229). The status word of the
- * workspace (vl_read_status) reports non-finite values and invalid routes (an out-of-range or
- * repeated expert id); the output is then not meaningful, as the reference would have refused
+ * expert's tokens, in ascending order, into groups and streams the expert's weights once per run
+ * of up to 32 tokens for IQ2_XXS (up to 8 for the other types) (moe_forward's per-expert token
+ * batches, deepseek_v4_graph.cpp:2211-2229). The status word of the workspace (vl_read_status)
+ * reports non-finite values and refused routes (see Routing); the output is then not
+ * meaningful, as the reference would have refused
  * the layer. Replaces the per-matvec device calls of moe_forward / qwen38_moe_block. */
 int vl_moe_layer(const vl_moe_config* config, const vl_moe_inputs* inputs, void* workspace,
                  uint64_t workspace_bytes, void* stream);

@@ -46,6 +46,8 @@ def to_device_bytes(data, device="cuda") -> torch.Tensor:
     if isinstance(data, torch.Tensor):
         return data.to(device=device, dtype=torch.uint8).contiguous()
     arr = np.ascontiguousarray(data, dtype=np.uint8)
+    if not arr.flags.writeable:  # e.g. a view of a read-only expert pack mapping
+        arr = arr.copy()
     return torch.from_numpy(arr).to(device)
 
 

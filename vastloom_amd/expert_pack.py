@@ -124,7 +124,10 @@ def write_pack(root: Path, layer: int, experts: dict[int, dict[str, tuple[int, i
 
 
 class ExpertPack:
-    """A pack mapped read-only: experts by id, their matrices as views of the payload."""
+    """A pack mapped read-only: experts by id, their matrices as views of the payload. A pack that
+    fails its checks raises PackError and leaves nothing open."""
+
+    experts: dict[int, PackExpert]
 
     def __init__(self, root: Path, verify_hashes: bool = True):
         root = Path(root)
@@ -143,12 +146,21 @@ class ExpertPack:
         if size != int(payload["bytes"]) or size > MAX_PAYLOAD_BYTES:
             raise PackError("payload size does not match the manifest")
         self._file = path.open("rb")
-        self._map = mmap.mmap(self._file.fileno(), 0, access=mmap.ACCESS_READ) if size else None
+        self._map = None
+        try:
+            self._map = mmap.mmap(self._file.fileno(), 0, access=mmap.ACCESS_READ) if size else None
+            self._load(m, size, verify_hashes)
+        except BaseException:
+            self.experts = {}
+            self.close()
+            raise
+
+    def _load(self, m: dict, size: int, verify_hashes: bool) -> None:
         buf = np.frombuffer(self._map, np.uint8) if size else np.zeros(0, np.uint8)
         records = m.get("experts", [])
         if len(records) > MAX_RECORDS:
             raise PackError("too many expert records")
-        self.experts: dict[int, PackExpert] = {}
+        self.experts = {}
         end = 0
         for r in sorted(records, key=lambda r: int(r["offset"])):
             e, off, n = int(r["expert"]), int(r["offset"]), int(r["bytes"])
@@ -176,7 +188,7 @@ class ExpertPack:
 
     def close(self) -> None:
         """Drops the pack's records; the mapping closes once no matrix view handed out remains."""
-        self.experts.clear()
+        self.experts = {}
         if self._map is not None:
             try:
                 self._map.close()

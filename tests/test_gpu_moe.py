@@ -47,7 +47,7 @@ def device_expert(ops, triple, H, F):
 SEMS = {"deepseek": 0, "qwen": 1, "plain": 2}
 
 
-@pytest.mark.parametrize("gt,dt", [(IQ2_XXS, IQ2_XXS), (IQ1_S, IQ3_XXS), (Q8_0, Q8_0)])
+@pytest.mark.parametrize("gt,dt", [(IQ2_XXS, IQ2_XXS), (IQ1_S, IQ3_XXS), (IQ1_S, IQ1_S), (Q8_0, Q8_0)])
 @pytest.mark.parametrize("sem", ["deepseek", "qwen", "plain"])
 @pytest.mark.parametrize("tokens", [1, 3])
 def test_expert_ffn(ops, lib, oracle, gt, dt, sem, tokens):

@@ -208,39 +208,41 @@ __device__ __forceinline__ uint64_t ld_pinned(const uint64_t* p) {
     return *gp(p);
 }
 
-// Decode tables of FMT for the token kernels: one 8-byte source entry per thread, loaded
-// unconditionally (a clamped index; threads past the last entry store nothing), then replicated
-// into LDS. IQ2_XXS and IQ3_XXS: 128 sign entries (rows 0..127, upper halves) and 256 grid entries
-// (rows 0..255, lower halves), 16 copies each (vl_decode.h); IQ1_S: 2048 entries, one copy, two
-// per thread.
+// Decode tables of FMT for the token kernels, filled by nt threads (thread t of them): 8-byte
+// source entries loaded unconditionally (clamped indices; entries past the last are not stored),
+// then replicated into LDS. IQ2_XXS and IQ3_XXS: 128 sign entries (rows 0..127, upper halves) and
+// 256 grid entries (rows 0..255, lower halves), 16 copies each (vl_decode.h), one entry per thread
+// (nt >= 384); IQ1_S: 2048 entries, one copy, entries t, t + nt and t + 2 nt (nt >= 683).
 template <uint32_t FMT>
 struct TokTables {
     static constexpr bool kRepl = FMT == VL_TYPE_IQ2_XXS || FMT == VL_TYPE_IQ3_XXS;
     static constexpr uint32_t kEntries = kRepl ? 384u : FMT == VL_TYPE_IQ1_S ? 2048u : 0u;
-    uint64_t v0, v1;
-    __device__ __forceinline__ void load(uint32_t t) {
+    uint64_t v[3];
+    __device__ __forceinline__ void load(uint32_t t, uint32_t nt) {
         if (kRepl) {
             const uint32_t i = t < kEntries ? t : kEntries - 1u;
             const uint64_t* src = FMT == VL_TYPE_IQ2_XXS ? (i < 128u ? g_tables.sign_sel + i : g_tables.iq2_codes + (i - 128u))
                                                          : (i < 128u ? g_tables.iq3_sel + i : g_tables.iq3_pm + (i - 128u));
-            v0 = ld_pinned(src);
+            v[0] = ld_pinned(src);
         } else if (FMT == VL_TYPE_IQ1_S) {
-            v0 = ld_pinned(g_tables.iq1_codes + (t & 2047u));
-            v1 = ld_pinned(g_tables.iq1_codes + ((t + 1024u) & 2047u));
+#pragma unroll
+            for (uint32_t j = 0; j < 3u; ++j) {
+                const uint32_t i = t + j * nt;
+                v[j] = ld_pinned(g_tables.iq1_codes + (i < kEntries ? i : kEntries - 1u));
+            }
         }
     }
-    __device__ __forceinline__ void store(uint8_t* lds, uint32_t t) const {
+    __device__ __forceinline__ void store(uint8_t* lds, uint32_t t, uint32_t nt) const {
         if (kRepl) {
             if (t >= kEntries) return;
             const uint32_t row = t < 128u ? t * 256u + kTabB : (t - 128u) * 256u + kTabA;
-            const uint4 q = make_uint4(lo32(v0), hi32(v0), lo32(v0), hi32(v0));
+            const uint4 q = make_uint4(lo32(v[0]), hi32(v[0]), lo32(v[0]), hi32(v[0]));
 #pragma unroll
             for (uint32_t c = 0; c < kTabCopies / 2u; ++c) *reinterpret_cast<uint4*>(lds + row + 16u * c) = q;
         } else if (FMT == VL_TYPE_IQ1_S) {
-            if (t < 1024u) {
-                reinterpret_cast<uint64_t*>(lds)[t] = v0;
-                reinterpret_cast<uint64_t*>(lds)[t + 1024u] = v1;
-            }
+#pragma unroll
+            for (uint32_t j = 0; j < 3u; ++j)
+                if (t + j * nt < kEntries) reinterpret_cast<uint64_t*>(lds)[t + j * nt] = v[j];
         }
     }
 };
@@ -844,6 +846,81 @@ __device__ __forceinline__ void route_rank_block(uint32_t n, uint32_t K, uint32_
     }
 }
 
+// Learned and softmax routing of the token by wave 0 alone, for pools of up to kTokWaveRoute
+// experts: lane l holds the keys and scores of experts l, l + 64, l + 128 and l + 192. The same
+// threshold, candidates and ranks as the block version above; the candidate list is formed with a
+// ballot prefix instead of an LDS counter. Every LDS word it writes is read back by the same wave,
+// so no barrier is needed and the other waves fill LDS meanwhile. Leaves the top-k list in sel and
+// the non-finite-key flag in misc (the first key-flag word; the others zero) for route_weights.
+constexpr uint32_t kTokWaveRoute = 256;
+__device__ __forceinline__ void route_wave0(const MoeShape& s, const uint32_t (&key)[4], const float (&score)[4],
+                                            uint32_t val, uint32_t gmax, uint32_t cand, uint32_t sel,
+                                            uint32_t misc) {
+    const uint32_t lane = threadIdx.x & 63u, E = s.experts, K = s.top_k, G = tok_group(E, K);
+    uint32_t k[4];
+    float v[4];
+    bool bad = false;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t e = lane + 64u * j;
+        const bool live = e < E;
+        k[j] = live ? key[j] : 0u;
+        v[j] = s.routing == kRouteSoftmax ? (k[j] > 1u ? key_float(k[j]) : 0.0f) : score[j];
+        if (live) lds_st_f32(val + 4u * e, v[j]);
+        bad |= live && k[j] <= 1u;
+        if (G && 64u * j < E) {
+            const uint32_t m = group_max_u32(k[j], G);
+            if (live && e % G == 0u) lds_st_u32(gmax + 4u * (e / G), m);
+        }
+    }
+    const bool anybad = __any(bad);
+    if (lane < kTokWaves) lds_st_u32(misc + 4u * (kMiscKeyFlags + lane), lane == 0 && anybad ? 1u : 0u);
+    issue_fence();  // the stores above stay ahead of the reads below (one wave: LDS keeps its order)
+    uint32_t t0 = 0;
+    if (G) {
+        const uint32_t ng = (E + G - 1u) / G;  // 2K <= ng <= 64
+        const uint32_t gm = lane < ng ? lds_u32(gmax + 4u * lane) : 0u;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < ng; ++j) {
+            const uint32_t gj = (uint32_t)__builtin_amdgcn_readlane((int)gm, j);
+            rank += (gj > gm || (gj == gm && j < lane)) ? 1u : 0u;
+        }
+        const uint64_t hit = __ballot(lane < ng && rank == K - 1u);
+        t0 = (uint32_t)__builtin_amdgcn_readlane((int)gm, (uint32_t)__builtin_ctzll(hit));
+    }
+    uint32_t n = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t e = lane + 64u * j;
+        const bool c = e < E && k[j] >= t0;
+        const uint64_t mask = __ballot(c);
+        if (c) {
+            const uint32_t i = n + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+            VL_LDS TokCand* cc = lptr<TokCand>(cand + 16u * i);
+            cc->ck = route_key64(k[j], e);
+            cc->val = v[j];
+        }
+        n += (uint32_t)__builtin_popcountll(mask);
+    }
+    issue_fence();
+    if (n <= 64u) {
+        route_rank_wave(n, K, cand, sel);
+    } else {
+        for (uint32_t i = lane; i < n; i += 64u) {
+            const VL_LDS TokCand* e = lptr<TokCand>(cand + 16u * i);
+            const uint64_t c = e->ck;
+            uint32_t rank = 0;
+            for (uint32_t j = 0; j < n; ++j) rank += lptr<TokCand>(cand + 16u * j)->ck > c ? 1u : 0u;
+            if (rank < K) {
+                lds_st_u32(sel + 8u * rank, ~(uint32_t)c);
+                lds_st_f32(sel + 8u * rank + 4u, e->val);
+            }
+        }
+    }
+    issue_fence();
+}
+
 // Wave 0 once the top-k list is complete: lane k < K takes the expert of rank k and forms its
 // weight with the reference's float64 arithmetic. Learned: the selected scores over their sum in
 // rank order, times route_scale (route_from_indices, deepseek_v4_reference.cpp:80-121). Softmax:
@@ -1136,6 +1213,9 @@ __device__ __forceinline__ void fill_work(const TokPlan p, uint32_t b, const Tok
     }
 }
 
+static_assert((kTokWaves - 1u) * 64u >= 384u && 3u * (kTokWaves - 1u) * 64u >= 2048u,
+              "the tables are filled by the waves other than the routing wave");
+
 template <uint32_t FMT>
 __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s, const MoeInputs in,
                                                                 const MoeWorkspace w, const TokPlan p) {
@@ -1166,52 +1246,82 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
     //    flags. The first weight chunk is requested only after these have arrived and been stored:
     //    loads complete in order, and a chunk from HBM ahead of them would delay every wait of the
     //    prologue.
-    const uint32_t ek = tid < E ? tid : E - 1u;
-    const uint32_t key = *gp(ws_ptr<const uint32_t>(w, w.off_keys) + ek);
-    const float score = *gp(ws_ptr<const float>(w, w.off_scores) + ek);
+    //    Pools of up to kTokWaveRoute experts are routed by wave 0 alone, which requests the keys,
+    //    scores and gate/up pointers of four experts per lane; larger pools by the whole block.
+    const bool wave_route = E <= kTokWaveRoute;
+    uint32_t key = 0, rk[4] = {0, 0, 0, 0};
+    float score = 0.0f, rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    uint64_t pg = 0, pu = 0, rg[4] = {0, 0, 0, 0}, ru[4] = {0, 0, 0, 0};
     const uint32_t elast = s.has_shared ? E : E - 1u;
-    const MoeExpert* ex = in.experts + (tid < elast ? tid : elast);
-    const uint64_t pg = reinterpret_cast<uint64_t>(ex->gate), pu = reinterpret_cast<uint64_t>(ex->up);
+    if (!wave_route) {
+        const uint32_t ek = tid < E ? tid : E - 1u;
+        key = *gp(ws_ptr<const uint32_t>(w, w.off_keys) + ek);
+        score = *gp(ws_ptr<const float>(w, w.off_scores) + ek);
+        const MoeExpert* ex = in.experts + (tid < elast ? tid : elast);
+        pg = reinterpret_cast<uint64_t>(ex->gate);
+        pu = reinterpret_cast<uint64_t>(ex->up);
+    } else if (wave == 0) {
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t e = lane + 64u * j < E ? lane + 64u * j : E - 1u;
+            rk[j] = *gp(ws_ptr<const uint32_t>(w, w.off_keys) + e);
+            rs[j] = *gp(ws_ptr<const float>(w, w.off_scores) + e);
+            rg[j] = reinterpret_cast<uint64_t>(in.experts[e].gate);
+            ru[j] = reinterpret_cast<uint64_t>(in.experts[e].up);
+        }
+    }
     const MoeExpert* exs = in.experts + elast;
     const uint64_t shg = reinterpret_cast<uint64_t>(exs->gate), shu = reinterpret_cast<uint64_t>(exs->up);
+    // The LDS fill below is shared by the waves that do not route: all of them for a larger pool,
+    // waves 1.. when wave 0 routes (its thread index pt and count npt; wave 0 then fills nothing
+    // and routes as soon as its keys arrive).
+    const bool filler = !wave_route || wave != 0;
+    const uint32_t pt = wave_route ? tid - 64u : tid, npt = wave_route ? blockDim.x - 64u : blockDim.x;
     TokTables<FMT> tt;
-    tt.load(tid);
     const uint32_t xn = (s.width / 32u) * 128u / 16u;  // 16-byte words of the token's limbs
     const uint4* xsrc = ws_ptr<const uint4>(w, w.off_xlimbs);
     constexpr uint32_t XB = 2;
     uint4 xv[XB];
+    int ev = 0;
+    uint32_t fv = 0;
+    if (filler) {
+        tt.load(pt, npt);
 #pragma unroll
-    for (uint32_t j = 0; j < XB; ++j) {
-        const uint32_t i = tid + j * blockDim.x;
-        xv[j] = ld_u4(xsrc + (i < xn ? i : xn - 1u));
+        for (uint32_t j = 0; j < XB; ++j) {
+            const uint32_t i = pt + j * npt;
+            xv[j] = ld_u4(xsrc + (i < xn ? i : xn - 1u));
+        }
+        const uint32_t xb = pt < w.xblocks ? pt : w.xblocks - 1u;
+        ev = *gp(ws_ptr<const int>(w, w.off_xexp) + (uint64_t)w.estride * xb);
+        fv = *gp(ws_ptr<const uint32_t>(w, w.off_xflags) + (uint64_t)w.estride * xb);
     }
-    const uint32_t xb = tid < w.xblocks ? tid : w.xblocks - 1u;
-    const int ev = *gp(ws_ptr<const int>(w, w.off_xexp) + (uint64_t)w.estride * xb);
-    const uint32_t fv = *gp(ws_ptr<const uint32_t>(w, w.off_xflags) + (uint64_t)w.estride * xb);
     issue_fence();
 
     // 2. LDS stores: tables, limbs, 2^-e, pointers, counters and flags, the chunk table, the
     //    rare-path record, the routing keys and group maxima.
-    tt.store(lds_base(), tid);
     uint4* xdst = reinterpret_cast<uint4*>(lds_base() + lay.xstage);
+    if (filler) {
+        tt.store(lds_base(), pt, npt);
 #pragma unroll
-    for (uint32_t j = 0; j < XB; ++j)
-        if (tid + j * blockDim.x < xn) xdst[tid + j * blockDim.x] = xv[j];
-    for (uint32_t i = tid + XB * blockDim.x; i < xn; i += blockDim.x) xdst[i] = ld_u4(xsrc + i);
-    if (tid < w.xblocks) lds_st_f32(lay.xscale + 4u * tid, __builtin_amdgcn_ldexpf(1.0f, -ev));
-    if (ptab && tid <= E) {
+        for (uint32_t j = 0; j < XB; ++j)
+            if (pt + j * npt < xn) xdst[pt + j * npt] = xv[j];
+        for (uint32_t i = pt + XB * npt; i < xn; i += npt) xdst[i] = ld_u4(xsrc + i);
+        if (pt < w.xblocks) lds_st_f32(lay.xscale + 4u * pt, __builtin_amdgcn_ldexpf(1.0f, -ev));
+    }
+    if (!wave_route && ptab && tid <= E) {
         *lptr<uint64_t>(lay.ptab + 16u * tid) = pg;
         *lptr<uint64_t>(lay.ptab + 16u * tid + 8u) = pu;
     }
     // Counters start at zero (the chunk counter past the statically taken chunks); the flag words
-    // are written by their own waves.
-    if (tid < kMiscWaveFlags) lds_st_u32(lay.misc + 4u * tid, tid == kMiscGrab ? nstatic : 0u);
-    if (tid == kMiscWaveFlags) lds_st_u32(lay.misc + 4u * kMiscCand, 0u);
-    const bool xflag = __any(tid < w.xblocks && fv != 0u);
+    // are written by their own waves and the refusal flag by wave 0 alone. The counters and
+    // fill_work's segment counts are stored by one wave, in that order.
+    if (filler && pt < kMiscBad) lds_st_u32(lay.misc + 4u * pt, pt == kMiscGrab ? nstatic : 0u);
+    if (filler && pt == kMiscWaveFlags) lds_st_u32(lay.misc + 4u * kMiscCand, 0u);
+    const bool xflag = __any(filler && pt < w.xblocks && fv != 0u);
     if (lane == 0) lds_st_u32(lay.misc + 4u * (kMiscWaveFlags + wave), xflag ? 1u : 0u);
-    const float rv = ranked ? route_stage(s, key, score, lay.val, lay.gmax, lay.misc, G) : 0.0f;
-    fill_work<CU>(p, b, ps, pr, ctx.nchunks, lay.desc, lay.misc, true, tid, blockDim.x);
-    if (tid == 0) {
+    const float rv = ranked && !wave_route ? route_stage(s, key, score, lay.val, lay.gmax, lay.misc, G) : 0.0f;
+    if (filler) fill_work<CU>(p, b, ps, pr, ctx.nchunks, lay.desc, lay.misc, true, pt, npt);
+    if (filler && pt == 0) {
         TokRare r;
         r.p = p;
         r.ps = ps;
@@ -1233,9 +1343,40 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
         r.out = in.out;
         lds_put(lay.rare, r);
     }
-    // Listed routes (wave 0) and this wave's first chunk of the shared expert.
+    // Routes: wave 0 alone (pools of up to kTokWaveRoute experts: every route, the active list
+    // and the active experts' pointers, before the first barrier), or the listed routes of a larger
+    // pool (wave 0). Then this wave's first chunk of the shared expert.
     TokRoute rt{0, 0.0f, false};
-    if (!ranked && wave == 0) rt = route_listed(s, in, w);
+    if (wave == 0 && (wave_route || !ranked)) {
+        if (ranked) {
+            route_wave0(s, rk, rs, lay.val, lay.gmax, lay.cand, lay.sel, lay.misc);
+            rt = route_weights(s, lay.sel, lay.val, lay.misc);
+        } else {
+            rt = route_listed(s, in, w);
+        }
+    }
+    if (wave == 0 && wave_route) {
+        const bool bad = rt.bad;
+        const uint32_t a = tok_active(s, w, rt, lay.act, lay.comb, b == 0);
+        // Lane k < K: the pointers of its expert, from the lane that requested them.
+        const uint32_t src = rt.id & 63u, jj = rt.id >> 6;
+        uint64_t g = 0, u = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint64_t gj = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(rg[j] >> 32), (int)src) << 32) |
+                                (uint32_t)__shfl((int)(uint32_t)rg[j], (int)src);
+            const uint64_t uj = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(ru[j] >> 32), (int)src) << 32) |
+                                (uint32_t)__shfl((int)(uint32_t)ru[j], (int)src);
+            g = jj == j ? gj : g;
+            u = jj == j ? uj : u;
+        }
+        if (lane < K && !bad) {
+            *lptr<uint64_t>(lay.wptr + 16u * a) = g;
+            *lptr<uint64_t>(lay.wptr + 16u * a + 8u) = u;
+        }
+        if (lane < 2u && s.has_shared) *lptr<uint64_t>(lay.wptr + 16u * K + 8u * lane) = lane ? shu : shg;
+        if (lane == 0) lds_st_u32(lay.misc + 4u * kMiscBad, bad ? 1u : 0u);
+    }
     Chunk bufA[CU];
     TokWork ca{0, 0, 0, 0, 0, 2, 0};
     const uint32_t ka = wave;
@@ -1249,9 +1390,9 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
     }
     __syncthreads();
 
-    // 3. Routing: candidates, their ranks, then wave 0 forms the weights, the active list and the
-    //    active experts' pointers.
-    if (ranked) {
+    // 3. Routing of a larger pool: candidates, their ranks, then wave 0 forms the weights, the
+    //    active list and the active experts' pointers.
+    if (ranked && !wave_route) {
         route_candidates(s, key, rv, lay.gmax, lay.cand, lay.misc, G);
         __syncthreads();
         const uint32_t n = uni(lds_u32(lay.misc + 4u * kMiscCand));
@@ -1262,7 +1403,7 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
             __syncthreads();
         }
     }
-    if (wave == 0) {
+    if (wave == 0 && !wave_route) {
         if (ranked) {
             lds_settle();
             rt = route_weights(s, lay.sel, lay.val, lay.misc);
@@ -1284,7 +1425,7 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
         if (lane < 2u && s.has_shared) *lptr<uint64_t>(lay.wptr + 16u * K + 8u * lane) = lane ? shu : shg;
         if (lane == 0) lds_st_u32(lay.misc + 4u * kMiscBad, bad ? 1u : 0u);
     }
-    __syncthreads();
+    if (!wave_route) __syncthreads();
     if (b == 0 && tid == 0) {
         uint32_t xb = 0;
         for (uint32_t i = 0; i < nw; ++i) xb |= lds_u32(lay.misc + 4u * (kMiscWaveFlags + i));
@@ -1488,11 +1629,17 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     ctx.hb = HB;
     ctx.ebytes = (F / 32u) * 128u;
     const MoeHeader* hdr = ws_ptr<const MoeHeader>(w, w.off_header);
-    // 1. Requests, issued unconditionally (clamped indices) and together: the active count, the
-    //    active experts' ids, the combine entries, every expert's down pointer, the decode tables,
-    //    the active experts' h with the maxima of its 256-row blocks.
-    const uint32_t n_active_raw = *gp(&hdr->n_active);
+    // 1. Requests, issued unconditionally (clamped indices) and together. First the expert of this
+    //    wave's first chunk (as the chunk table will hold it), whose down pointer is requested as
+    //    soon as the id arrives; then the active count, the active experts' ids, the combine
+    //    entries, every expert's down pointer, the decode tables, the active experts' h with the
+    //    maxima of its 256-row blocks.
     const ActiveExpert* act = ws_ptr<const ActiveExpert>(w, w.off_active);
+    const uint32_t ka = wave;
+    const TokWork ca = ka < ctx.nchunks ? decode_work(encode_work(tok_chunk<CU>(p, b, ps, pr, ka), p.tiles, p.C, false))
+                                        : TokWork{0, 0, 0, 0, 0, 2, 0};
+    const uint32_t ea = uni(*gp(&act[ca.a < A ? ca.a : A - 1u].expert));
+    const uint32_t n_active_raw = *gp(&hdr->n_active);
     const uint32_t eid = *gp(&act[tid < A ? tid : A - 1u].expert);
     const uint32_t nc = 2u * (K + 1u);
     const uint32_t cw = *gp(ws_ptr<const uint32_t>(w, w.off_combine) + (tid < nc ? tid : nc - 1u));
@@ -1500,7 +1647,7 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     const uint32_t elast = s.has_shared ? E : E - 1u;
     const uint64_t pv = reinterpret_cast<uint64_t>(in.experts[tid < elast ? tid : elast].down);
     TokTables<FMT> tt;
-    tt.load(tid);
+    tt.load(tid, blockDim.x);
     const float* h = ws_ptr<const float>(w, w.off_h);
     const uint32_t* hmax = counters_of(w).hmax;
     const uint32_t quads = F / 4u, hq_total = A * quads;
@@ -1518,6 +1665,12 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     const uint32_t hb = A * HB;
     const uint32_t hm = *gp(hmax + (uint64_t)(tid < hb ? tid : hb - 1u) * 8u);
     issue_fence();
+    // The first chunk's matrix (a stale id of a refused layer still names a real expert).
+    const uint8_t* pa = uni_ptr(reinterpret_cast<const uint8_t*>(in.experts[ea < elast ? ea : elast].down));
+    issue_fence();
+
+    // 2. LDS stores: pointers, ids, combine entries, counters, the chunk table, the rare-path
+    //    record, the tables, and the active experts' h -> limbs with one exponent per 256 rows.
     if (tid <= elast && tid < pn) *lptr<uint64_t>(lay.ptab + 8u * tid) = pv;
     if (tid < A) lds_st_u32(lay.eid + 4u * tid, eid);
     if (tid < 2u * (K + 1u)) lds_st_u32(lay.comb + 4u * tid, cw);
@@ -1545,33 +1698,7 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
         r.out = in.out;
         lds_put(lay.rare, r);
     }
-    tt.store(lds_base(), tid);
-    __syncthreads();
-    const uint32_t n_active = uni(n_active_raw);
-    if (n_active == 0) {
-        // A refused route: the layer's output is zero (the status word says why).
-        for (uint32_t i = b * blockDim.x + tid; i < s.width; i += gridDim.x * blockDim.x) *gp(in.out + i) = 0.0f;
-        return;
-    }
-    // 2. The active experts' down pointers; this wave's first chunk is requested at once (its
-    //    pointer looked up through the LDS tables), before the h conversion whose latency it hides.
-    auto down_ptr = [&](uint32_t a) -> uint64_t {
-        const uint32_t e = lds_u32(lay.eid + 4u * a);
-        return pn ? *lptr<uint64_t>(lay.ptab + 8u * e) : reinterpret_cast<uint64_t>(in.experts[e].down);
-    };
-    if (tid < A) *lptr<uint64_t>(lay.dptr + 8u * tid) = down_ptr(tid);
-    Chunk bufA[CU];
-    const uint32_t ka = wave;
-    const TokWork ca = ctx.chunk(ka);
-    {
-        const TileRef tr = ca.count ? tile_ref<FMT>(ctx.L, uni_ptr(reinterpret_cast<const uint8_t*>(down_ptr(ca.a))), ca.t)
-                                    : idle_tile();
-#pragma unroll
-        for (uint32_t i = 0; i < CU; ++i)
-            tok_load<FMT>(i < ca.count ? tr : idle_tile(), i < ca.count ? ca.col + i : 0u, ctx.ng, bufA[i]);
-    }
-    // 3. The active experts' h -> limbs with one exponent per 256 rows, into LDS (the h requested
-    //    at entry; a layer with more than HQ quads per thread loads the rest here); tables.
+    tt.store(lds_base(), tid, blockDim.x);
     {
         auto convert = [&](uint32_t i, const float4& f4, uint32_t mx) {
             const uint32_t a = i / quads, col = 4u * (i - a * quads);
@@ -1599,11 +1726,32 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
             lds_st_f32(lay.hscale + 4u * i, __builtin_amdgcn_ldexpf(1.0f, -e));
         }
     }
+    // 3. This wave's first chunk, requested after every prologue load has been waited for.
+    Chunk bufA[CU];
+    {
+        const TileRef tr = ca.count ? tile_ref<FMT>(ctx.L, pa, ca.t) : idle_tile();
+#pragma unroll
+        for (uint32_t i = 0; i < CU; ++i)
+            tok_load<FMT>(i < ca.count ? tr : idle_tile(), i < ca.count ? ca.col + i : 0u, ctx.ng, bufA[i]);
+    }
     __syncthreads();
-    // 4. Stream.
+    const uint32_t n_active = uni(n_active_raw);
+    if (n_active == 0) {
+        // A refused route: the layer's output is zero (the status word says why).
+        for (uint32_t i = b * blockDim.x + tid; i < s.width; i += gridDim.x * blockDim.x) *gp(in.out + i) = 0.0f;
+        return;
+    }
+    // 4. The active experts' down pointers, for the chunks taken from the counter.
+    if (tid < A) {
+        const uint32_t e = lds_u32(lay.eid + 4u * tid);
+        *lptr<uint64_t>(lay.dptr + 8u * tid) =
+            pn ? *lptr<uint64_t>(lay.ptab + 8u * e) : reinterpret_cast<uint64_t>(in.experts[e].down);
+    }
+    __syncthreads();
+    // 5. Stream.
     tok_stream<FMT, CU>(ctx, ka, ca, bufA);
     __syncthreads();
-    // 5. Data-parallel tiles: each (tile, combine entry)'s expert sum over its chunks in order, a
+    // 6. Data-parallel tiles: each (tile, combine entry)'s expert sum over its chunks in order, a
     //    wave per pair (into the h limb area, no longer read), then a wave per tile combines.
     const TokRare r = lds_get<TokRare>(lay.rare);
     const uint32_t nd0 = r.ps.n + r.pr.n, cpe = r.p.C / CU, nent = r.K + (r.has_shared ? 1u : 0u);

@@ -1223,19 +1223,6 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
     const TokGuLds lay = tok_lds_gu(TB, s.width, p.max_chunks, s.experts);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nw = blockDim.x >> 6;
     const uint32_t b = blockIdx.x, K = s.top_k, E = s.experts;
-    const TokPiece ps = tok_piece(p.S, b, CU), pr = tok_piece(p.R, b, CU);
-    GuCtx<FMT> ctx;
-    ctx.part = lay.part;
-    ctx.desc = lay.desc;
-    ctx.misc = lay.misc;
-    ctx.rare = lay.rare;
-    vl_make_layout(FMT, s.inter, s.width, &ctx.L);
-    ctx.ng = ctx.L.groups;
-    ctx.nchunks = ps.n + pr.n + p.q * p.UJ / CU;
-    ctx.xstage = lay.xstage;
-    ctx.xscale = lay.xscale;
-    ctx.wptr = lay.wptr;
-    const uint32_t nS = ps.n, nstatic = nS < nw ? nS : nw;
     const bool ranked = s.routing == kRouteLearned || s.routing == kRouteSoftmax;
     const bool ptab = tok_has_ptab(E);
     const uint32_t G = tok_group(E, K);
@@ -1296,6 +1283,20 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_gateup(const MoeShape s
         fv = *gp(ws_ptr<const uint32_t>(w, w.off_xflags) + (uint64_t)w.estride * xb);
     }
     issue_fence();
+    // The block's pieces and the wave loop's view, formed while the requests are in flight.
+    const TokPiece ps = tok_piece(p.S, b, CU), pr = tok_piece(p.R, b, CU);
+    GuCtx<FMT> ctx;
+    ctx.part = lay.part;
+    ctx.desc = lay.desc;
+    ctx.misc = lay.misc;
+    ctx.rare = lay.rare;
+    vl_make_layout(FMT, s.inter, s.width, &ctx.L);
+    ctx.ng = ctx.L.groups;
+    ctx.nchunks = ps.n + pr.n + p.q * p.UJ / CU;
+    ctx.xstage = lay.xstage;
+    ctx.xscale = lay.xscale;
+    ctx.wptr = lay.wptr;
+    const uint32_t nS = ps.n, nstatic = nS < nw ? nS : nw;
 
     // 2. LDS stores: tables, limbs, 2^-e, pointers, counters and flags, the chunk table, the
     //    rare-path record, the routing keys and group maxima.
@@ -1614,33 +1615,15 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     const TokDnLds lay = tok_lds_dn(TB, A, F, p.max_chunks);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nw = blockDim.x >> 6;
     const uint32_t b = blockIdx.x;
-    const TokPiece ps = tok_piece(p.S, b, CU), pr = tok_piece(p.R, b, CU);
-    DnCtx<FMT> ctx;
-    ctx.part = lay.part;
-    ctx.desc = lay.desc;
-    ctx.misc = lay.misc;
-    ctx.rare = lay.rare;
-    vl_make_layout(FMT, s.width, s.inter, &ctx.L);
-    ctx.ng = ctx.L.groups;
-    ctx.nchunks = ps.n + pr.n + p.q * p.UJ / CU;
-    ctx.hstage = lay.hstage;
-    ctx.hscale = lay.hscale;
-    ctx.dptr = lay.dptr;
-    ctx.hb = HB;
-    ctx.ebytes = (F / 32u) * 128u;
     const MoeHeader* hdr = ws_ptr<const MoeHeader>(w, w.off_header);
-    // 1. Requests, issued unconditionally (clamped indices) and together. First the expert of this
-    //    wave's first chunk (as the chunk table will hold it), whose down pointer is requested as
-    //    soon as the id arrives; then the active count, the active experts' ids, the combine
-    //    entries, every expert's down pointer, the decode tables, the active experts' h with the
-    //    maxima of its 256-row blocks.
+    // 1. Requests, issued unconditionally (clamped indices) and together: the active experts' ids
+    //    (lane a of every wave: active expert a), the active count, the combine entries, every
+    //    expert's down pointer, the decode tables, the active experts' h with the maxima of its
+    //    256-row blocks. Then the down pointer of the expert of this wave's first chunk (as the
+    //    chunk table will hold it), picked from the ids once they arrive.
     const ActiveExpert* act = ws_ptr<const ActiveExpert>(w, w.off_active);
-    const uint32_t ka = wave;
-    const TokWork ca = ka < ctx.nchunks ? decode_work(encode_work(tok_chunk<CU>(p, b, ps, pr, ka), p.tiles, p.C, false))
-                                        : TokWork{0, 0, 0, 0, 0, 2, 0};
-    const uint32_t ea = uni(*gp(&act[ca.a < A ? ca.a : A - 1u].expert));
+    const uint32_t eid = *gp(&act[lane < A ? lane : A - 1u].expert);
     const uint32_t n_active_raw = *gp(&hdr->n_active);
-    const uint32_t eid = *gp(&act[tid < A ? tid : A - 1u].expert);
     const uint32_t nc = 2u * (K + 1u);
     const uint32_t cw = *gp(ws_ptr<const uint32_t>(w, w.off_combine) + (tid < nc ? tid : nc - 1u));
     const uint32_t pn = E + 1u <= kTokPtrTab + 1u ? E + 1u : 0u;
@@ -1665,8 +1648,28 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     const uint32_t hb = A * HB;
     const uint32_t hm = *gp(hmax + (uint64_t)(tid < hb ? tid : hb - 1u) * 8u);
     issue_fence();
-    // The first chunk's matrix (a stale id of a refused layer still names a real expert).
-    const uint8_t* pa = uni_ptr(reinterpret_cast<const uint8_t*>(in.experts[ea < elast ? ea : elast].down));
+    // The block's pieces and the wave loop's view, formed while the requests are in flight.
+    const TokPiece ps = tok_piece(p.S, b, CU), pr = tok_piece(p.R, b, CU);
+    DnCtx<FMT> ctx;
+    ctx.part = lay.part;
+    ctx.desc = lay.desc;
+    ctx.misc = lay.misc;
+    ctx.rare = lay.rare;
+    vl_make_layout(FMT, s.width, s.inter, &ctx.L);
+    ctx.ng = ctx.L.groups;
+    ctx.nchunks = ps.n + pr.n + p.q * p.UJ / CU;
+    ctx.hstage = lay.hstage;
+    ctx.hscale = lay.hscale;
+    ctx.dptr = lay.dptr;
+    ctx.hb = HB;
+    ctx.ebytes = (F / 32u) * 128u;
+    // The first chunk's matrix (a stale id of a refused layer still names a real expert): requested
+    // now, waited for only when the chunk is issued.
+    const uint32_t ka = wave;
+    const TokWork ca = ka < ctx.nchunks ? decode_work(encode_work(tok_chunk<CU>(p, b, ps, pr, ka), p.tiles, p.C, false))
+                                        : TokWork{0, 0, 0, 0, 0, 2, 0};
+    const uint32_t ea = (uint32_t)__builtin_amdgcn_readlane((int)eid, ca.a < A ? ca.a : 0u);
+    const uint64_t pa_raw = reinterpret_cast<uint64_t>(in.experts[ea < elast ? ea : elast].down);
     issue_fence();
 
     // 2. LDS stores: pointers, ids, combine entries, counters, the chunk table, the rare-path
@@ -1729,7 +1732,8 @@ __global__ void __launch_bounds__(kTokWaves * 64u) k_tok_down(const MoeShape s, 
     // 3. This wave's first chunk, requested after every prologue load has been waited for.
     Chunk bufA[CU];
     {
-        const TileRef tr = ca.count ? tile_ref<FMT>(ctx.L, pa, ca.t) : idle_tile();
+        const TileRef tr =
+            ca.count ? tile_ref<FMT>(ctx.L, uni_ptr(reinterpret_cast<const uint8_t*>(pa_raw)), ca.t) : idle_tile();
 #pragma unroll
         for (uint32_t i = 0; i < CU; ++i)
             tok_load<FMT>(i < ca.count ? tr : idle_tile(), i < ca.count ? ca.col + i : 0u, ctx.ng, bufA[i]);

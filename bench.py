@@ -11,6 +11,8 @@ cache between their uses.
 
     python bench.py [--steps K] [--warmup W] [--workload iq2_moe] [--no-cpu-baseline]
     python bench.py --copy-calibration BYTES     plain device copies of BYTES (counter scale)
+    python bench.py --matvec q4_k [--matvec-shape 2048x7168] [--matvec-tokens 1]
+                                                 device matvec of one storage type alone
 
 ms_per_step is the mean over the K bracketed steps; step_us gives the median and spread of
 per-step times from a second pass with an event between steps. roofline.traffic (HBM bytes per
@@ -59,6 +61,11 @@ def parse() -> argparse.Namespace:
     p.add_argument("--residency-mib", type=int, default=0, metavar="MIB",
                    help="only run the layer with its experts in host memory and at most MIB of "
                         "them resident (misses streamed through pinned staging); prints its own line")
+    p.add_argument("--matvec", default="", metavar="TYPE",
+                   help="only time the device matvec of one storage type (q4_k, q5_k, q6_k, mxfp4, "
+                        "bf16, f32, q8_0, iq2_xxs, iq3_xxs, iq1_s); prints its own line")
+    p.add_argument("--matvec-shape", default="2048x7168", metavar="ROWSxCOLS")
+    p.add_argument("--matvec-tokens", type=int, default=1)
     return p.parse_args()
 
 
@@ -325,6 +332,69 @@ def residency_run(args) -> int:
     return 0
 
 
+def matvec_run(args) -> int:
+    """The device matvec of one storage type alone: y = W x for one matrix of ROWS x COLS.
+
+    Matrix instances (copies of one random matrix at distinct addresses, more than 1 GiB in all)
+    rotate so that no weights stay in the 256 MiB last-level cache between uses. A spin kernel
+    holds the stream while all launches are queued, so the timed region is the launches back to
+    back: per launch, the status clear and the matvec kernel. GB/s = matrix bytes / time.
+    """
+    import ctypes as C
+
+    import torch
+
+    from vastloom_amd import ops
+    from vastloom_amd._lib import call
+    from vastloom_amd.workloads import TYPE_NAMES, random_matrix
+
+    by_name = {v: k for k, v in TYPE_NAMES.items()}
+    qtype = by_name[args.matvec]
+    rows, cols = (int(v) for v in args.matvec_shape.lower().split("x"))
+    tokens = args.matvec_tokens
+    enc = random_matrix(np.random.default_rng(12), qtype, rows, cols, 0.01)
+    src = torch.from_numpy(enc).cuda()
+    copies = max(2, min(512, (1 << 30) // enc.size + 1))
+    mats = [ops.DeviceMatrix(qtype, rows, cols, src) for _ in range(copies)]
+    x = torch.randn((tokens, cols), dtype=torch.float32, device="cuda")
+    ws_bytes = C.c_uint64()
+    call("vl_matvec_workspace", qtype, rows, cols, tokens, C.byref(ws_bytes))
+    ws = [torch.zeros(ws_bytes.value, dtype=torch.uint8, device="cuda") for _ in range(2)]
+    y = torch.empty((tokens, rows), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def launch(i):
+        call("vl_matvec", qtype, rows, cols, mats[i % copies].ptr(), x.data_ptr(), tokens,
+             y.data_ptr(), ws[i & 1].data_ptr(), ws_bytes.value, sp)
+
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(50_000_000)  # holds the stream while the launches below are queued
+    start.record(stream)
+    for i in range(args.steps):
+        launch(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / args.steps
+    bits = ops.read_status(ws[0], sp) | ops.read_status(ws[1], sp)
+    if bits:
+        raise RuntimeError(f"matvec raised status bits {bits:#x}")
+    gbs = enc.size / (us * 1e-6) / 1e9
+    print(json.dumps({
+        "metric": "matvec_hbm_gbs", "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "us_per_launch": round(us, 3),
+        "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"matvec {args.matvec} {rows}x{cols} tokens={tokens}",
+                   "matrix_bytes": int(enc.size), "instances": copies},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "note": "per launch including the status-clear kernel"}}))
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -335,6 +405,8 @@ def main() -> int:
         return copy_calibration(args.copy_calibration)
     if args.residency_mib:
         return residency_run(args)
+    if args.matvec:
+        return matvec_run(args)
     import torch
 
     from vastloom_amd import ops

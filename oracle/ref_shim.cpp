@@ -44,6 +44,11 @@ VLR_EXPORT int vlr_dequantize(std::uint32_t type, const std::uint8_t* enc, std::
         case vi::kGgmlTypeIq3Xxs:
             return status(vi::dequantize_iq3_xxs(bytes(enc, enc_bytes), o, limits));
         case vi::kGgmlTypeIq1S: return status(vi::dequantize_iq1_s(bytes(enc, enc_bytes), o, limits));
+        case vi::kGgmlTypeQ4K: return status(vi::dequantize_q4_k(bytes(enc, enc_bytes), o, limits));
+        case vi::kGgmlTypeQ5K: return status(vi::dequantize_q5_k(bytes(enc, enc_bytes), o, limits));
+        case vi::kGgmlTypeQ6K: return status(vi::dequantize_q6_k(bytes(enc, enc_bytes), o, limits));
+        case vi::kGgmlTypeMxfp4: return status(vi::dequantize_mxfp4(bytes(enc, enc_bytes), o, limits));
+        case vi::kGgmlTypeBf16: return status(vi::dequantize_bf16(bytes(enc, enc_bytes), o, limits));
         default: return 1 + static_cast<int>(vastloom::ErrorCode::unsupported);
     }
 }

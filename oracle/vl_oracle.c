@@ -153,15 +153,159 @@ static void decode_f32(const uint8_t* block, float* out) {
     memcpy(out, &bits, sizeof bits);
 }
 
-static int layout(uint32_t type, size_t* elements, size_t* bytes, block_decoder* decoder) {
+/* The 6-bit scale and minimum of sub-block j of a Q4_K/Q5_K superblock, packed into 12 bytes:
+ * bytes 0..3 hold scales 0..3 in their low six bits, bytes 4..7 minimums 0..3 likewise; for
+ * j >= 4 the low four bits come from byte j+4 (scale: low nibble, minimum: high nibble) and the
+ * top two from the spare high bits of bytes j-4 (scale) and j (minimum)
+ * (ggml_quantization.cpp:435-455). */
+static void k_scale_min(const uint8_t* s, unsigned j, unsigned* sc, unsigned* mn) {
+    if (j < 4u) {
+        *sc = s[j] & 63u;
+        *mn = s[j + 4u] & 63u;
+    } else {
+        *sc = (s[j + 4u] & 15u) | ((unsigned)(s[j - 4u] >> 6) << 4);
+        *mn = (unsigned)(s[j + 4u] >> 4) | ((unsigned)(s[j] >> 6) << 4);
+    }
+}
+
+/* Q4_K: 144 bytes -> 256 weights (ggml_quantization.cpp:457-493). fp16 d and dmin, 12 scale
+ * bytes, 128 quant bytes; sub-block j (32 weights) takes the low (even j) or high (odd j)
+ * nibbles of quant bytes 32*(j/2) .. +31, w = (d*sc) * q - (dmin*m). */
+static void decode_q4_k(const uint8_t* block, float* out) {
+    const float d = vlo_fp16_to_f32(le16(block)), dmin = vlo_fp16_to_f32(le16(block + 2));
+    for (unsigned j = 0; j < 8u; ++j) {
+        unsigned sc, mn;
+        k_scale_min(block + 4, j, &sc, &mn);
+        const float dj = d * (float)sc, mj = dmin * (float)mn;
+        const uint8_t* q = block + 16 + 32u * (j / 2u);
+        for (unsigned l = 0; l < 32u; ++l)
+            out[32u * j + l] = dj * (float)((q[l] >> (4u * (j & 1u))) & 15u) - mj;
+    }
+}
+
+/* Q5_K: 176 bytes -> 256 weights (ggml_quantization.cpp:495-539). As Q4_K with 32 high-bit
+ * bytes before the nibbles: bit j of high byte l adds 16 to weight l of sub-block j. */
+static void decode_q5_k(const uint8_t* block, float* out) {
+    const float d = vlo_fp16_to_f32(le16(block)), dmin = vlo_fp16_to_f32(le16(block + 2));
+    const uint8_t* high = block + 16;
+    for (unsigned j = 0; j < 8u; ++j) {
+        unsigned sc, mn;
+        k_scale_min(block + 4, j, &sc, &mn);
+        const float dj = d * (float)sc, mj = dmin * (float)mn;
+        const uint8_t* q = block + 48 + 32u * (j / 2u);
+        for (unsigned l = 0; l < 32u; ++l) {
+            const unsigned v = ((q[l] >> (4u * (j & 1u))) & 15u) + (((high[l] >> j) & 1u) << 4);
+            out[32u * j + l] = dj * (float)v - mj;
+        }
+    }
+}
+
+/* Q6_K: 210 bytes -> 256 weights (ggml_quantization.cpp:541-589). 128 low-nibble bytes, 64
+ * high-bit bytes (2 bits per weight), 16 int8 scales (one per 16 weights), fp16 d at byte 208.
+ * Half h (128 weights) reads low bytes 64h.., high bytes 128+32h.. and scales 192+8h..; its
+ * quarter k takes weight l's low bits from low byte l (k = 0, 2) or l+32 (k = 1, 3), low nibble
+ * for k < 2 and high nibble after, and bits 2k..2k+1 of high byte l on top;
+ * w = (d * scale) * (q - 32). */
+static void decode_q6_k(const uint8_t* block, float* out) {
+    const float d = vlo_fp16_to_f32(le16(block + 208));
+    for (unsigned h = 0; h < 2u; ++h) {
+        const uint8_t* low = block + 64u * h;
+        const uint8_t* high = block + 128u + 32u * h;
+        const int8_t* sc = (const int8_t*)(block + 192u + 8u * h);
+        for (unsigned k = 0; k < 4u; ++k) {
+            for (unsigned l = 0; l < 32u; ++l) {
+                const uint8_t lb = low[l + 32u * (k & 1u)];
+                const unsigned nib = k < 2u ? (lb & 15u) : (unsigned)(lb >> 4);
+                const int q = (int)(nib | (((unsigned)(high[l] >> (2u * k)) & 3u) << 4)) - 32;
+                out[128u * h + 32u * k + l] = d * (float)sc[l / 16u + 2u * k] * (float)q;
+            }
+        }
+    }
+}
+
+/* E8M0 block scale of MXFP4 with the one-half factor of the doubled value table folded in:
+ * byte v >= 2 is 2^(v-128) (exponent field v-1), bytes 0 and 1 the subnormals 2^-128 and
+ * 2^-127 (ggml_quantization.cpp:126-133). */
+static float e8m0_half(uint8_t v) {
+    const uint32_t bits = v < 2u ? 0x00200000u << v : (uint32_t)(v - 1u) << 23;
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+/* Twice the E2M1 values, indexed by the 4-bit code (ggml_quantization.cpp:44-47). */
+static const int8_t kE2m1Doubled[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+/* MXFP4: 17 bytes -> 32 weights (ggml_quantization.cpp:381-399). One E8M0 scale byte, then
+ * 16 bytes whose low nibbles are weights 0..15 and high nibbles weights 16..31. */
+static void decode_mxfp4(const uint8_t* block, float* out) {
+    const float s = e8m0_half(block[0]);
+    for (unsigned i = 0; i < 16u; ++i) {
+        out[i] = (float)kE2m1Doubled[block[1 + i] & 15u] * s;
+        out[i + 16u] = (float)kE2m1Doubled[block[1 + i] >> 4] * s;
+    }
+}
+
+/* BF16: the upper half of a binary32 (ggml_quantization.cpp:411-413). */
+static void decode_bf16(const uint8_t* block, float* out) {
+    const uint32_t bits = (uint32_t)le16(block) << 16;
+    memcpy(out, &bits, sizeof bits);
+}
+
+/* Whether a block passes the reference's pre-decode validation. */
+typedef int (*block_check)(const uint8_t* block);
+
+/* validate_block_scales (ggml_quantization.cpp:206-215): the fp16 scale leads the block. */
+static int check_lead_scale(const uint8_t* block) { return isfinite(vlo_fp16_to_f32(le16(block))); }
+/* Q4_K/Q5_K validators (:1140-1156, :1180-1196): d and dmin. */
+static int check_d_dmin(const uint8_t* block) {
+    return isfinite(vlo_fp16_to_f32(le16(block))) && isfinite(vlo_fp16_to_f32(le16(block + 2)));
+}
+/* Q6_K validator (:1220-1234): d at byte 208. */
+static int check_q6_k(const uint8_t* block) { return isfinite(vlo_fp16_to_f32(le16(block + 208))); }
+/* validate_mxfp4_blocks (:400-409): every decoded value. */
+static int check_mxfp4(const uint8_t* block) {
+    float v[32];
+    decode_mxfp4(block, v);
+    for (int i = 0; i < 32; ++i)
+        if (!isfinite(v[i])) return 0;
+    return 1;
+}
+/* validate_dense_values (:856-871): every element of a dense matrix. */
+static int check_f32(const uint8_t* block) {
+    float v;
+    decode_f32(block, &v);
+    return isfinite(v);
+}
+static int check_bf16(const uint8_t* block) {
+    float v;
+    decode_bf16(block, &v);
+    return isfinite(v);
+}
+
+/* Block shape, decoder and validator of each storage type (ggml_storage_bytes,
+ * ggml_quantization.cpp:1052-1113, and the per-type entry points at :1115-1500). */
+static int layout_checked(uint32_t type, size_t* elements, size_t* bytes, block_decoder* decoder,
+                          block_check* check) {
+    *check = check_lead_scale;
     switch (type) {
-        case VLO_F32: *elements = 1; *bytes = 4; *decoder = decode_f32; return VLO_OK;
+        case VLO_F32: *elements = 1; *bytes = 4; *decoder = decode_f32; *check = check_f32; return VLO_OK;
         case VLO_Q8_0: *elements = 32; *bytes = 34; *decoder = decode_q8_0; return VLO_OK;
+        case VLO_Q4_K: *elements = 256; *bytes = 144; *decoder = decode_q4_k; *check = check_d_dmin; return VLO_OK;
+        case VLO_Q5_K: *elements = 256; *bytes = 176; *decoder = decode_q5_k; *check = check_d_dmin; return VLO_OK;
+        case VLO_Q6_K: *elements = 256; *bytes = 210; *decoder = decode_q6_k; *check = check_q6_k; return VLO_OK;
         case VLO_IQ2_XXS: *elements = 256; *bytes = 66; *decoder = decode_iq2_xxs; return VLO_OK;
         case VLO_IQ3_XXS: *elements = 256; *bytes = 98; *decoder = decode_iq3_xxs; return VLO_OK;
         case VLO_IQ1_S: *elements = 256; *bytes = 50; *decoder = decode_iq1_s; return VLO_OK;
+        case VLO_BF16: *elements = 1; *bytes = 2; *decoder = decode_bf16; *check = check_bf16; return VLO_OK;
+        case VLO_MXFP4: *elements = 32; *bytes = 17; *decoder = decode_mxfp4; *check = check_mxfp4; return VLO_OK;
         default: return VLO_E_UNSUPPORTED;
     }
+}
+
+static int layout(uint32_t type, size_t* elements, size_t* bytes, block_decoder* decoder) {
+    block_check c;
+    return layout_checked(type, elements, bytes, decoder, &c);
 }
 
 int vlo_block_layout(uint32_t type, size_t* block_elements, size_t* block_bytes) {
@@ -187,18 +331,14 @@ int vlo_storage_bytes(uint32_t type, size_t rows, size_t cols, size_t max_elemen
     return checked_bytes(rows, cols, be, bb, max_elements, bytes);
 }
 
-/* validate_block_scales (ggml_quantization.cpp:206-215): the fp16 scale leads every block. */
-static int scales_finite(const uint8_t* encoded, size_t bytes, size_t block_bytes) {
-    if (block_bytes == 4) { /* F32: every value must be finite (validate_dense_values, :670-685) */
-        for (size_t off = 0; off < bytes; off += 4) {
-            float v;
-            decode_f32(encoded + off, &v);
-            if (!isfinite(v)) return 0;
-        }
-        return 1;
-    }
-    for (size_t off = 0; off < bytes; off += block_bytes)
-        if (!isfinite(vlo_fp16_to_f32(le16(encoded + off)))) return 0;
+/* The type's pre-decode validation over every block of an encoded span. */
+static int blocks_valid(uint32_t type, const uint8_t* encoded, size_t bytes) {
+    size_t be, bb;
+    block_decoder d;
+    block_check check;
+    if (layout_checked(type, &be, &bb, &d, &check)) return 0;
+    for (size_t off = 0; off < bytes; off += bb)
+        if (!check(encoded + off)) return 0;
     return 1;
 }
 
@@ -213,7 +353,7 @@ int vlo_dequantize(uint32_t type, const uint8_t* encoded, size_t encoded_bytes, 
     if (out_elements == 0 || out_elements % be != 0 || out_elements > max_elements)
         return VLO_E_INVALID_ARGUMENT;
     if (encoded_bytes != out_elements / be * bb) return VLO_E_INVALID_FORMAT;
-    if (!scales_finite(encoded, encoded_bytes, bb)) return VLO_E_INVALID_FORMAT;
+    if (!blocks_valid(type, encoded, encoded_bytes)) return VLO_E_INVALID_FORMAT;
     for (size_t b = 0; b < out_elements / be; ++b) decode(encoded + b * bb, out + b * be);
     return VLO_OK;
 }
@@ -279,7 +419,7 @@ int vlo_matvec(uint32_t type, const uint8_t* encoded, size_t encoded_bytes, size
     if (encoded_bytes != need || x_len != cols || y_len != rows) return VLO_E_INVALID_ARGUMENT;
     for (size_t i = 0; i < cols; ++i)
         if (!isfinite(x[i])) return VLO_E_INVALID_ARGUMENT;
-    if (!scales_finite(encoded, encoded_bytes, bb)) return VLO_E_INVALID_FORMAT;
+    if (!blocks_valid(type, encoded, encoded_bytes)) return VLO_E_INVALID_FORMAT;
 
     /* Computed into scratch and published on success, as matvec_ggml_f32_transactional
      * (ggml_quantization.cpp:1585-1676) does for every graph call. */

@@ -12,8 +12,8 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.oracle import IQ1_S, IQ2_XXS, IQ3_XXS, Q8_0
-from tests.kat_blocks import KAT, fnv_f32, kat_input
+from oracle.oracle import BF16, F32, IQ1_S, IQ2_XXS, IQ3_XXS, MXFP4, Q4_K, Q5_K, Q6_K, Q8_0
+from tests.kat_blocks import KAT, fnv_f32, kat_count, kat_poisoned, kat_rows, kat_x
 from vastloom_amd.workloads import random_matrix
 
 pytestmark = pytest.mark.gpu
@@ -40,14 +40,18 @@ def row_bound(w: np.ndarray, x: np.ndarray) -> np.ndarray:
 def test_kat_blocks_decode_bit_exact(ops, oracle, name):
     k = KAT[name]
     enc = k["blocks"]()
-    rows, cols = 3, k["cols"]
+    rows, cols = kat_rows(k), k["cols"]
+    assert rows * cols == kat_count(k)
     print(f"[decode KAT] {name} {rows}x{cols}", flush=True)
     m = ops.DeviceMatrix(k["qtype"], rows, cols, enc)
     got = m.dequantize().cpu().numpy().reshape(-1)
     want = oracle.dequantize(k["qtype"], enc, rows * cols)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
-    assert fnv_f32(got) == k["fnv"]
-    y = m.matvec(torch.from_numpy(kat_input(cols)).cuda()).cpu().numpy()
+    if k["fnv"] is not None:
+        assert fnv_f32(got) == k["fnv"]
+    for index, value in k["values"].items():
+        assert got[index] == np.float32(value), (name, index)
+    y = m.matvec(torch.from_numpy(kat_x(k)).cuda()).cpu().numpy()
     for got_v, (want_v, tol) in zip(y, k["outputs"]):
         assert abs(float(got_v) - want_v) <= max(tol, 1e-5 * abs(want_v) + 1e-6)
 
@@ -57,6 +61,13 @@ SHAPES = [
     (IQ2_XXS, 3, 512), (IQ2_XXS, 100, 1024), (IQ2_XXS, 2048, 7168), (IQ2_XXS, 7168, 2048),
     (IQ3_XXS, 33, 512), (IQ3_XXS, 7168, 2048),
     (IQ1_S, 31, 768), (IQ1_S, 2048, 7168),
+    # GGUF-layout types: ragged row counts, the expert gate/up and down shapes.
+    (Q4_K, 3, 512), (Q4_K, 130, 2048), (Q4_K, 2048, 7168), (Q4_K, 7168, 2048),
+    (Q5_K, 65, 2048), (Q5_K, 2048, 7168),
+    (Q6_K, 3, 512), (Q6_K, 67, 1792), (Q6_K, 2048, 7168), (Q6_K, 7168, 2048),
+    (MXFP4, 3, 64), (MXFP4, 45, 2880), (MXFP4, 2880, 2880),
+    (BF16, 2, 4), (BF16, 33, 100), (BF16, 1024, 2048),
+    (F32, 5, 33), (F32, 512, 2048),
 ]
 
 
@@ -75,13 +86,16 @@ def test_extreme_scales_decode_bit_exact(ops, oracle):
     rng = np.random.default_rng(3)
     special = np.array([0x0001, 0x03FF, 0x0400, 0x7BFF, 0x8001, 0xFBFF, 0x0000], np.uint16)
     for qtype, rows, cols in ((Q8_0, 40, 256), (IQ2_XXS, 40, 512), (IQ3_XXS, 40, 512),
-                              (IQ1_S, 40, 512)):
+                              (IQ1_S, 40, 512), (Q4_K, 40, 512), (Q5_K, 40, 512), (Q6_K, 40, 512)):
         print(f"[decode extreme] type={qtype}", flush=True)
         enc = random_matrix(rng, qtype, rows, cols, 0.01)
         be = 32 if qtype == Q8_0 else 256
         blocks = enc.reshape(rows * cols // be, -1)
-        s = special[np.arange(blocks.shape[0]) % special.size]
-        blocks[:, 0], blocks[:, 1] = s & 0xFF, s >> 8
+        # The fp16 scale fields: d (and dmin) of the K-quants, Q6_K's d at byte 208.
+        offsets = (208,) if qtype == Q6_K else (0, 2) if qtype in (Q4_K, Q5_K) else (0,)
+        for i, off in enumerate(offsets):
+            s = special[(np.arange(blocks.shape[0]) + 3 * i) % special.size]
+            blocks[:, off], blocks[:, off + 1] = s & 0xFF, s >> 8
         m = ops.DeviceMatrix(qtype, rows, cols, enc)
         got = m.dequantize().cpu().numpy().reshape(-1)
         want = oracle.dequantize(qtype, enc, rows * cols)
@@ -174,3 +188,41 @@ def test_matvec_refuses_non_finite(ops):
     with pytest.raises(ops.VlError) as err:
         m2.matvec(torch.from_numpy(np.ones(cols, np.float32)).cuda())
     assert err.value.name == "invalid_format"
+
+
+def test_mxfp4_every_scale_byte_decodes_bit_exact(ops, oracle):
+    # Every E8M0 byte that decodes to finite values (0 and 1 are the subnormal scales), against
+    # every code byte.
+    codes = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    scales = [e for e in range(256) if e < 247]  # 2^(e-128) * 12 stays finite up to e = 246
+    enc = np.zeros((len(scales), 16, 17), np.uint8)
+    enc[:, :, 0] = np.array(scales, np.uint8)[:, None]
+    enc[:, :, 1:] = codes[None]
+    rows, cols = len(scales), 512
+    print(f"[decode mxfp4 scales] {rows}x{cols}", flush=True)
+    m = ops.DeviceMatrix(MXFP4, rows, cols, enc.reshape(-1))
+    got = m.dequantize().cpu().numpy().reshape(-1)
+    want = oracle.dequantize(MXFP4, enc.reshape(-1), rows * cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["q4_k", "q6_k", "mxfp4_ggml", "bf16"])
+def test_gguf_types_refuse_non_finite(ops, oracle, name):
+    # A block the reference refuses (non-finite dmin, d, decoded value or element) makes the
+    # device matvec report invalid_format, and a NaN activation invalid_argument.
+    k = KAT[name]
+    rows, cols = kat_rows(k), k["cols"]
+    print(f"[refuse] {name}", flush=True)
+    bad = kat_poisoned(k)
+    with pytest.raises(Exception):
+        oracle.matvec(k["qtype"], bad, rows, cols, kat_x(k))
+    m = ops.DeviceMatrix(k["qtype"], rows, cols, bad)
+    with pytest.raises(ops.VlError) as err:
+        m.matvec(torch.from_numpy(kat_x(k)).cuda())
+    assert err.value.name == "invalid_format"
+    good = ops.DeviceMatrix(k["qtype"], rows, cols, k["blocks"]())
+    xn = kat_x(k).copy()
+    xn[1] = np.nan
+    with pytest.raises(ops.VlError) as err:
+        good.matvec(torch.from_numpy(xn).cuda())
+    assert err.value.name == "invalid_argument"

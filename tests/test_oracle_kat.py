@@ -1,9 +1,10 @@
 """The oracle against the reference's committed known-answer vectors (no GPU).
 
 Mirrors test_trunk_storage_reference_kernels, test_iq1_s_reference_kernel,
-test_iq2_xxs_reference_kernel, test_iq3_xxs_reference_kernel,
+test_iq2_xxs_reference_kernel, test_q4k_mxfp4_reference_parity, test_iq3_xxs_reference_kernel,
 test_quantized_routed_expert_contract and test_qwen38_moe_router
-(reference tests/test_main.cpp:863-973, :1295-1460, :1832-1907, :2006-2051, :3966-3990).
+(reference tests/test_main.cpp:863-1112, :1295-1460, :1663-1723, :1832-1907, :2006-2051,
+:3966-3990).
 """
 
 from __future__ import annotations
@@ -12,7 +13,7 @@ import numpy as np
 import pytest
 
 from oracle.oracle import IQ1_S, IQ2_XXS, IQ3_XXS, Q8_0, OracleError
-from tests.kat_blocks import KAT, fnv_f32, kat_input
+from tests.kat_blocks import KAT, fnv_f32, kat_count, kat_poisoned, kat_rows, kat_x
 
 
 def test_codebook_fingerprints(oracle):
@@ -40,11 +41,13 @@ def test_fp16_decode_exhaustive(oracle):
 def test_decode_fingerprint_and_values(oracle, name):
     k = KAT[name]
     enc = k["blocks"]()
-    n = 6 * k["block_elements"]
-    out = oracle.dequantize(k["qtype"], enc, n)
-    assert fnv_f32(out) == k["fnv"]
+    out = oracle.dequantize(k["qtype"], enc, kat_count(k))
+    if k["fnv"] is not None:
+        assert fnv_f32(out) == k["fnv"]
     for index, value in k["values"].items():
         assert out[index] == np.float32(value), (name, index)
+    for index, (value, tol) in k.get("approx", {}).items():
+        assert abs(float(out[index]) - value) <= tol, (name, index)
 
 
 @pytest.mark.parametrize("name", sorted(KAT))
@@ -52,7 +55,7 @@ def test_decode_fingerprint_and_values(oracle, name):
 def test_matvec_known_outputs(oracle, name, threads):
     k = KAT[name]
     cols = k["cols"]
-    y = oracle.matvec(k["qtype"], k["blocks"](), 3, cols, kat_input(cols), threads=threads)
+    y = oracle.matvec(k["qtype"], k["blocks"](), kat_rows(k), cols, kat_x(k), threads=threads)
     for got, (want, tol) in zip(y, k["outputs"]):
         if tol == 0.0:
             assert got == np.float32(want)
@@ -74,9 +77,9 @@ def test_malformed_inputs_fail_closed(oracle, name):
     k = KAT[name]
     qtype, be = k["qtype"], k["block_elements"]
     enc = k["blocks"]()
-    cols = k["cols"]
-    x = kat_input(cols)
-    n = 6 * be
+    cols, rows = k["cols"], kat_rows(k)
+    x = kat_x(k)
+    n = kat_count(k)
     sentinel = np.full(n, 17.0, np.float32)
     # Truncated payload, empty output, a ceiling below the matrix, an unaligned column count.
     with pytest.raises(OracleError):
@@ -86,27 +89,25 @@ def test_malformed_inputs_fail_closed(oracle, name):
     with pytest.raises(OracleError):
         oracle.dequantize(qtype, enc, n, max_elements=be)
     with pytest.raises(OracleError):
-        oracle.matvec(qtype, enc, 3, cols - 1, x[:-1])
+        oracle.matvec(qtype, enc, rows, cols - 1, x[:-1])
     with pytest.raises(OracleError):
-        oracle.matvec(qtype, enc[:-1], 3, cols, x)
+        oracle.matvec(qtype, enc[:-1], rows, cols, x)
     assert np.all(sentinel == 17.0)
-    # A non-finite block scale is refused and the destination is left untouched.
-    bad = enc.copy()
-    block_bytes = enc.size // 6
-    bad[4 * block_bytes], bad[4 * block_bytes + 1] = 0x00, 0x7C
+    # A non-finite block scale (or value) is refused and the destination is left untouched.
+    bad = kat_poisoned(k)
     with pytest.raises(OracleError) as err:
         oracle.dequantize(qtype, bad, n, out=sentinel)
     assert err.value.name == "invalid_format"
     assert np.all(sentinel == 17.0)
-    ys = np.full(3, 17.0, np.float32)
+    ys = np.full(rows, 17.0, np.float32)
     with pytest.raises(OracleError):
-        oracle.matvec(qtype, bad, 3, cols, x, out=ys)
+        oracle.matvec(qtype, bad, rows, cols, x, out=ys)
     assert np.all(ys == 17.0)
     # A NaN input is refused.
     xn = x.copy()
     xn[0] = np.nan
     with pytest.raises(OracleError) as err:
-        oracle.matvec(qtype, enc, 3, cols, xn, out=ys)
+        oracle.matvec(qtype, enc, rows, cols, xn, out=ys)
     assert err.value.name == "invalid_argument"
     assert np.all(ys == 17.0)
 

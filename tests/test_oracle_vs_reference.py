@@ -11,7 +11,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from oracle.oracle import IQ1_S, IQ2_XXS, IQ3_XXS, Q8_0, SCORE_SQRT_SOFTPLUS
+from oracle.oracle import (BF16, IQ1_S, IQ2_XXS, IQ3_XXS, MXFP4, Q4_K, Q5_K, Q6_K, Q8_0,
+                           SCORE_SQRT_SOFTPLUS, OracleError)
 from vastloom_amd.workloads import random_matrix, workload
 
 SHAPES = {
@@ -19,6 +20,11 @@ SHAPES = {
     IQ2_XXS: [(3, 512), (130, 1024), (2048, 7168), (7168, 2048)],
     IQ3_XXS: [(3, 512), (65, 2048), (512, 2048)],
     IQ1_S: [(3, 512), (64, 1792), (256, 7168)],
+    Q4_K: [(3, 512), (130, 2048), (2048, 7168)],
+    Q5_K: [(3, 512), (65, 2048), (512, 7168)],
+    Q6_K: [(3, 512), (64, 1792), (1024, 2048)],
+    MXFP4: [(3, 64), (45, 2880), (512, 2048)],
+    BF16: [(2, 4), (33, 100), (512, 2048)],
 }
 
 
@@ -120,3 +126,83 @@ def test_clamped_expert_against_reference_float_oracle(oracle, reference):
                                    (0, d.view(np.uint8)), H, F, x, routing=route, limit=limit)
         b = reference.expert_swiglu_f32(x, g, d, u, route, H, F, limit)
         assert np.allclose(a, b, atol=1e-6 * np.abs(b).max(), rtol=0)
+
+
+def _outcome(fn):
+    try:
+        return fn()
+    except OracleError as e:  # both wrappers raise it with the reference's error code
+        return e.name
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K])
+def test_k_quant_special_scales_bit_identical(oracle, reference, qtype):
+    # fp16 subnormal, smallest normal, largest finite, negative and zero d / dmin, then an
+    # infinite and a NaN one, which both sides must refuse alike.
+    rng = np.random.default_rng(qtype)
+    rows, cols = 7, 512
+    special = np.array([0x0001, 0x03FF, 0x0400, 0x7BFF, 0x8001, 0xFBFF, 0x0000], np.uint16)
+    offsets = (208,) if qtype == Q6_K else (0, 2)
+    enc = random_matrix(rng, qtype, rows, cols, 0.01)
+    blocks = enc.reshape(rows * cols // 256, -1)
+    for i, off in enumerate(offsets):
+        s = special[(np.arange(blocks.shape[0]) + 3 * i) % special.size]
+        blocks[:, off], blocks[:, off + 1] = s & 0xFF, s >> 8
+    n = rows * cols
+    x = rng.standard_normal(cols).astype(np.float32)
+    assert np.array_equal(oracle.dequantize(qtype, enc, n).view(np.uint32),
+                          reference.dequantize(qtype, enc, n).view(np.uint32))
+    assert np.array_equal(oracle.matvec(qtype, enc, rows, cols, x).view(np.uint32),
+                          reference.matvec(qtype, enc, rows, cols, x).view(np.uint32))
+    for bad_bits in (0x7C00, 0xFE00):
+        for off in offsets:
+            bad = enc.copy().reshape(blocks.shape)
+            bad[5, off], bad[5, off + 1] = bad_bits & 0xFF, bad_bits >> 8
+            bad = bad.reshape(-1)
+            a = _outcome(lambda: oracle.dequantize(qtype, bad, n))
+            b = _outcome(lambda: reference.dequantize(qtype, bad, n))
+            assert a == b == "invalid_format"
+            a = _outcome(lambda: oracle.matvec(qtype, bad, rows, cols, x))
+            b = _outcome(lambda: reference.matvec(qtype, bad, rows, cols, x))
+            assert a == b == "invalid_format"
+
+
+def test_mxfp4_every_scale_byte(oracle, reference):
+    # All 256 E8M0 scale bytes against all 256 code bytes: the subnormal scales 0 and 1, the
+    # normal range, and the top bytes whose large codes overflow to infinity (refused by both).
+    codes = np.arange(256, dtype=np.uint8)
+    for e in range(256):
+        enc = np.zeros((16, 17), np.uint8)
+        enc[:, 0] = e
+        enc[:, 1:] = codes.reshape(16, 16)
+        enc = enc.reshape(-1)
+        a = _outcome(lambda: oracle.dequantize(MXFP4, enc, 512))
+        b = _outcome(lambda: reference.dequantize(MXFP4, enc, 512))
+        if isinstance(a, str) or isinstance(b, str):
+            assert a == b == "invalid_format", e
+        else:
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), e
+            assert np.all(np.isfinite(a))
+    x = np.linspace(-1, 1, 64).astype(np.float32)
+    enc = random_matrix(np.random.default_rng(39), MXFP4, 16, 64, 0.01)
+    enc.reshape(-1, 17)[:, 0] = np.arange(32) % 2  # the two subnormal scales
+    assert np.array_equal(oracle.matvec(MXFP4, enc, 16, 64, x).view(np.uint32),
+                          reference.matvec(MXFP4, enc, 16, 64, x).view(np.uint32))
+
+
+def test_bf16_special_values(oracle, reference):
+    # Every finite bf16 bit pattern decodes alike; an infinity or NaN anywhere is refused alike.
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = np.isfinite((codes.astype(np.uint32) << 16).view(np.float32))
+    enc = codes[finite].view(np.uint8)
+    n = int(finite.sum())
+    a = oracle.dequantize(BF16, enc, n)
+    assert np.array_equal(a.view(np.uint32), reference.dequantize(BF16, enc, n).view(np.uint32))
+    assert np.array_equal(a.view(np.uint32), codes[finite].astype(np.uint32) << 16)
+    for bad_code in (0x7F80, 0xFF80, 0x7FC1):
+        bad = np.array([0x3F80, bad_code, 0x4000, 0x3F00], np.uint16).view(np.uint8)
+        x = np.ones(2, np.float32)
+        assert _outcome(lambda: oracle.dequantize(BF16, bad, 4)) == "invalid_format"
+        assert _outcome(lambda: reference.dequantize(BF16, bad, 4)) == "invalid_format"
+        assert _outcome(lambda: oracle.matvec(BF16, bad, 2, 2, x)) == \
+            _outcome(lambda: reference.matvec(BF16, bad, 2, 2, x))

@@ -22,7 +22,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libvastloom_hip.so"
 
-SOURCES = ["vl_kernels.hip", "vl_moe.hip", "vl_moe_token.hip", "vl_moe_wide.hip", "vl_capi.cpp", "vl_host.cpp"]
+SOURCES = ["vl_kernels.hip", "vl_gguf.hip", "vl_moe.hip", "vl_moe_token.hip", "vl_moe_wide.hip", "vl_capi.cpp", "vl_host.cpp"]
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall",

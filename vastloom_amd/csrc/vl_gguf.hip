@@ -1,0 +1,375 @@
+// HIP kernels for the storage types that stay in their GGUF bytes on the device: Q4_K, Q5_K,
+// Q6_K, MXFP4, BF16 and F32 (vl_type_tiled() is false for them).
+//
+//   k_gguf_dequant   GGUF matrix -> float32 rows, bit-identical to the reference decoders
+//   k_gguf_matvec    y[token][row] = W x[token] for up to eight tokens, one block per row
+//
+// These matrices are read as they are stored, row-major with each row's blocks contiguous, so
+// making one resident is a device copy. A "piece" is eight consecutive weights of a row; a block
+// holds a whole number of pieces (32 for the 256-weight K-quants, 4 for MXFP4), so a piece never
+// crosses a block. A 256-thread block takes one row: thread i decodes the pieces i, i + 256, ...
+// of the row, four at a time with all four pieces' loads issued before the first is decoded,
+// and accumulates w * x in float per token; the block then adds its 256 partial sums per token
+// in a fixed order.
+// The weights themselves are formed exactly as the reference forms them (each product and
+// difference rounded once, in the reference's order, fp contraction off), so the dequantize
+// kernel is bit-exact and the matvec differs from the reference's float64 accumulation only by
+// float rounding of the partial sums.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vl_kernels.h"
+#include "vl_layout.h"
+#include "vl_stream.h"
+
+namespace vl {
+
+namespace {
+
+__device__ __forceinline__ uint32_t ld_u8(const uint8_t* p) { return *gp(p); }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {  // p 2-byte aligned
+    return *gp(reinterpret_cast<const uint16_t*>(p));
+}
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {  // p 4-byte aligned
+    return *gp(reinterpret_cast<const uint32_t*>(p));
+}
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint2 ld_u64(const uint8_t* p) {  // p 8-byte aligned
+    const u32x2 v = *gp(reinterpret_cast<const u32x2*>(p));
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ u32x4 ld_u128(const uint8_t* p) {  // p 16-byte aligned
+    return *gp(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ uint32_t byte_of(uint2 v, int i) {
+    return ((i < 4 ? v.x : v.y) >> (8 * (i & 3))) & 0xffu;
+}
+__device__ __forceinline__ float bits_float(uint32_t b) { return __uint_as_float(b); }
+
+// Byte i (0..11) of a Q4_K/Q5_K scale field held as three little-endian words.
+__device__ __forceinline__ uint32_t scale_byte(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t i) {
+    const uint32_t w = i < 4u ? s0 : i < 8u ? s1 : s2;
+    return (w >> (8u * (i & 3u))) & 0xffu;
+}
+
+// The raw bytes one piece needs, loaded before any of them is used.
+struct RawPiece {
+    uint32_t a, b, c, d;  // format-specific words
+    uint2 q, h;           // quant bytes and high bits
+};
+
+// Weights per block and bytes per block of each format (the K-quants' 256-weight superblocks,
+// MXFP4's 32-weight blocks; BF16 is handled per element).
+template <uint32_t FMT> struct Fmt;
+template <> struct Fmt<VL_TYPE_Q4_K> { static constexpr uint32_t be = 256, bb = 144; };
+template <> struct Fmt<VL_TYPE_Q5_K> { static constexpr uint32_t be = 256, bb = 176; };
+template <> struct Fmt<VL_TYPE_Q6_K> { static constexpr uint32_t be = 256, bb = 210; };
+template <> struct Fmt<VL_TYPE_MXFP4> { static constexpr uint32_t be = 32, bb = 17; };
+template <> struct Fmt<VL_TYPE_BF16> { static constexpr uint32_t be = 1, bb = 2; };
+template <> struct Fmt<VL_TYPE_F32> { static constexpr uint32_t be = 1, bb = 4; };
+
+// Loads piece p of a row (row = the row's first byte). A BF16 or F32 piece past the row's last
+// column reads nothing for the missing columns.
+template <uint32_t FMT>
+__device__ __forceinline__ void load_piece(const uint8_t* row, uint32_t p, uint32_t cols, RawPiece& r) {
+    if constexpr (FMT == VL_TYPE_F32) {
+        const uint8_t* e = row + 32ull * p;
+        if ((cols & 7u) == 0u) {  // row bytes % 32 == 0: two 16-byte loads
+            const u32x4 v0 = ld_u128(e), v1 = ld_u128(e + 16);
+            r.a = v0.x; r.b = v0.y; r.c = v0.z; r.d = v0.w;
+            r.q = make_uint2(v1.x, v1.y);
+            r.h = make_uint2(v1.z, v1.w);
+        } else {
+            uint32_t w[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (8u * p + i < cols) w[i] = ld_u32(e + 4 * i);
+            r.a = w[0]; r.b = w[1]; r.c = w[2]; r.d = w[3];
+            r.q = make_uint2(w[4], w[5]);
+            r.h = make_uint2(w[6], w[7]);
+        }
+    } else if constexpr (FMT == VL_TYPE_BF16) {
+        const uint8_t* e = row + 16ull * p;
+        if ((cols & 7u) == 0u) {  // rows of whole pieces: one 16-byte load (row bytes % 16 == 0)
+            const u32x4 v = ld_u128(e);
+            r.a = v.x; r.b = v.y; r.c = v.z; r.d = v.w;
+        } else {
+            uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (8u * p + i < cols) w[i >> 1] |= ld_u16(e + 2 * i) << (16 * (i & 1));
+            r.a = w[0]; r.b = w[1]; r.c = w[2]; r.d = w[3];
+        }
+    } else if constexpr (FMT == VL_TYPE_MXFP4) {
+        // Piece q of a block: low nibbles (q < 2) or high nibbles (q >= 2) of code bytes
+        // 1 + 8 (q & 1) .. +7. Blocks are 17 bytes, so every byte is loaded on its own.
+        const uint32_t q = p & 3u;
+        const uint8_t* blk = row + 17ull * (p >> 2);
+        const uint8_t* c = blk + 1u + 8u * (q & 1u);
+        r.a = ld_u8(blk);
+        r.q.x = ld_u8(c) | ld_u8(c + 1) << 8 | ld_u8(c + 2) << 16 | ld_u8(c + 3) << 24;
+        r.q.y = ld_u8(c + 4) | ld_u8(c + 5) << 8 | ld_u8(c + 6) << 16 | ld_u8(c + 7) << 24;
+    } else if constexpr (FMT == VL_TYPE_Q6_K) {
+        // Blocks are 210 bytes: 2-byte aligned loads only. Piece q = 16h + 4k + l0/8.
+        const uint32_t q = p & 31u, h = q >> 4, k = (q >> 2) & 3u, l0 = (q & 3u) * 8u;
+        const uint8_t* blk = row + 210ull * (p >> 5);
+        const uint8_t* lo = blk + 64u * h + 32u * (k & 1u) + l0;
+        const uint8_t* hi = blk + 128u + 32u * h + l0;
+        r.q.x = ld_u16(lo) | ld_u16(lo + 2) << 16;
+        r.q.y = ld_u16(lo + 4) | ld_u16(lo + 6) << 16;
+        r.h.x = ld_u16(hi) | ld_u16(hi + 2) << 16;
+        r.h.y = ld_u16(hi + 4) | ld_u16(hi + 6) << 16;
+        r.a = ld_u16(blk + 208u);
+        r.b = ld_u8(blk + 192u + 8u * h + (l0 >> 4) + 2u * k);
+    } else {  // Q4_K, Q5_K: 144- and 176-byte blocks keep 16-byte alignment
+        const uint32_t q = p & 31u, j = q >> 2, l0 = (q & 3u) * 8u;
+        const uint8_t* blk = row + (uint64_t)Fmt<FMT>::bb * (p >> 5);
+        r.a = ld_u32(blk);
+        r.b = ld_u32(blk + 4);
+        r.c = ld_u32(blk + 8);
+        r.d = ld_u32(blk + 12);
+        if constexpr (FMT == VL_TYPE_Q5_K) {
+            r.h = ld_u64(blk + 16u + l0);
+            r.q = ld_u64(blk + 48u + 32u * (j >> 1) + l0);
+        } else {
+            r.q = ld_u64(blk + 16u + 32u * (j >> 1) + l0);
+        }
+    }
+}
+
+// The eight weights of piece p, exactly as the reference decoders produce them
+// (ggml_quantization.cpp:381-413, :435-589).
+template <uint32_t FMT>
+__device__ __forceinline__ void decode_piece(const RawPiece& r, uint32_t p, float w[8]) {
+#pragma clang fp contract(off)
+    if constexpr (FMT == VL_TYPE_F32) {
+        const uint32_t v[8] = {r.a, r.b, r.c, r.d, r.q.x, r.q.y, r.h.x, r.h.y};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = bits_float(v[i]);
+    } else if constexpr (FMT == VL_TYPE_BF16) {
+        const uint32_t v[4] = {r.a, r.b, r.c, r.d};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = bits_float((i & 1) ? (v[i >> 1] & 0xffff0000u) : (v[i >> 1] << 16));
+    } else if constexpr (FMT == VL_TYPE_MXFP4) {
+        // Scale: E8M0 with the half of the doubled code table folded in; codes: twice E2M1.
+        const uint32_t e = r.a;
+        const float s = bits_float(e < 2u ? 0x00200000u << e : (e - 1u) << 23);
+        const uint32_t shift = 4u * ((p & 3u) >> 1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c = (byte_of(r.q, i) >> shift) & 15u, m = c & 7u;
+            const int mag = m < 4u ? (int)m : (int)((m & 1u ? 6u : 4u) << ((m - 4u) >> 1));
+            w[i] = (float)(c & 8u ? -mag : mag) * s;
+        }
+    } else if constexpr (FMT == VL_TYPE_Q6_K) {
+        const uint32_t q = p & 31u, k = (q >> 2) & 3u;
+        const float d = half_bits_to_float(r.a);
+        const float ds = d * (float)(int)(int8_t)(uint8_t)r.b;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lb = byte_of(r.q, i);
+            const uint32_t nib = k < 2u ? (lb & 15u) : (lb >> 4);
+            const int v = (int)(nib | ((byte_of(r.h, i) >> (2u * k)) & 3u) << 4) - 32;
+            w[i] = ds * (float)v;
+        }
+    } else {  // Q4_K, Q5_K
+        const uint32_t j = (p & 31u) >> 2;
+        const float d = half_bits_to_float(r.a), dmin = half_bits_to_float(r.a >> 16);
+        // Sub-block j's 6-bit scale and minimum from the 12 packed bytes (words b, c, d).
+        uint32_t sc, mn;
+        if (j < 4u) {
+            sc = scale_byte(r.b, r.c, r.d, j) & 63u;
+            mn = scale_byte(r.b, r.c, r.d, j + 4u) & 63u;
+        } else {
+            const uint32_t x = scale_byte(r.b, r.c, r.d, j + 4u);
+            sc = (x & 15u) | (scale_byte(r.b, r.c, r.d, j - 4u) >> 6) << 4;
+            mn = (x >> 4) | (scale_byte(r.b, r.c, r.d, j) >> 6) << 4;
+        }
+        const float dj = d * (float)sc, mj = dmin * (float)mn;
+        const uint32_t shift = 4u * (j & 1u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t v = (byte_of(r.q, i) >> shift) & 15u;
+            if constexpr (FMT == VL_TYPE_Q5_K) v += ((byte_of(r.h, i) >> j) & 1u) << 4;
+            w[i] = dj * (float)v - mj;
+        }
+    }
+}
+
+template <uint32_t FMT>
+__device__ __forceinline__ uint64_t row_bytes(uint32_t cols) {
+    return (uint64_t)(cols / Fmt<FMT>::be) * Fmt<FMT>::bb;
+}
+
+// One thread per piece of the matrix.
+template <uint32_t FMT>
+__global__ void __launch_bounds__(256) k_gguf_dequant(vl_tiled_layout L, const uint8_t* __restrict__ w,
+                                                      float* __restrict__ out) {
+    const uint32_t ppr = (L.cols + 7u) / 8u;
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i >= (uint64_t)L.rows * ppr) return;
+    const uint32_t row = (uint32_t)(i / ppr), p = (uint32_t)(i % ppr);
+    RawPiece r;
+    load_piece<FMT>(w + (uint64_t)row * row_bytes<FMT>(L.cols), p, L.cols, r);
+    float v[8];
+    decode_piece<FMT>(r, p, v);
+    float* dst = out + (uint64_t)row * L.cols + 8u * p;
+    if (8u * p + 8u <= L.cols) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) dst[k] = v[k];
+    } else {
+        for (uint32_t k = 0; 8u * p + k < L.cols; ++k) dst[k] = v[k];
+    }
+}
+
+__global__ void k_gguf_clear_status(uint32_t* status) {
+    if (threadIdx.x == 0) *status = 0u;
+}
+
+constexpr int kPiecesInFlight = 4;
+
+// One row per 256-thread block; thread i takes pieces i, i + 256, ... of the row, all of a
+// thread's loads (up to kPiecesInFlight pieces) issued before the first piece is decoded.
+// NT = token slots (tokens <= NT).
+template <uint32_t FMT, int NT>
+__global__ void __launch_bounds__(256) k_gguf_matvec(vl_tiled_layout L, const uint8_t* __restrict__ W,
+                                                     const float* __restrict__ x, uint32_t tokens,
+                                                     float* __restrict__ y, uint32_t* status) {
+    __shared__ float part[4][NT];
+    __shared__ uint32_t bad[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t row = blockIdx.x;  // grid = rows
+    const uint32_t cols = L.cols, ppr = (cols + 7u) / 8u;
+    const bool whole = (cols & 7u) == 0u;
+    const uint8_t* rp = W + (uint64_t)row * row_bytes<FMT>(cols);
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    bool bad_x = false;
+    for (uint32_t base = tid; base < ppr; base += 256u * kPiecesInFlight) {
+        RawPiece r[kPiecesInFlight];
+#pragma unroll
+        for (int u = 0; u < kPiecesInFlight; ++u) {
+            const uint32_t p = base + 256u * u;
+            if (p < ppr) load_piece<FMT>(rp, p, cols, r[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kPiecesInFlight; ++u) {
+            const uint32_t p = base + 256u * u;
+            if (p >= ppr) break;
+            float wv[8];
+            decode_piece<FMT>(r[u], p, wv);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (t >= (int)tokens) break;
+                const float* xp = x + (uint64_t)t * cols + 8u * p;
+                float xv[8];
+                if (whole) {
+                    const f32x4 a = *gp(reinterpret_cast<const f32x4*>(xp));
+                    const f32x4 b = *gp(reinterpret_cast<const f32x4*>(xp + 4));
+                    xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+                    xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) xv[i] = 8u * p + i < cols ? xp[i] : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    bad_x |= !__builtin_isfinite(xv[i]);
+                    acc[t] = fmaf(wv[i], xv[i], acc[t]);
+                }
+            }
+        }
+    }
+    // Each wave adds its lanes, then thread 0 adds the four waves' sums in wave order.
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc[t] += __shfl_xor(acc[t], off, 64);
+    }
+    const bool wave_bad = __ballot(bad_x) != 0ull;
+    if (lane == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) part[wave][t] = acc[t];
+        bad[wave] = wave_bad ? 1u : 0u;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t bits = (bad[0] | bad[1] | bad[2] | bad[3]) ? kStatusNonFiniteInput : 0u;
+        for (uint32_t t = 0; t < tokens && t < (uint32_t)NT; ++t) {
+            const float v = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
+            y[(uint64_t)t * L.rows + row] = v;
+            if (!__builtin_isfinite(v)) bits |= kStatusNonFiniteOutput;
+        }
+        if (bits) or_bits(status, bits);
+    }
+}
+
+template <uint32_t FMT>
+hipError_t dequant_fmt(const vl_tiled_layout& L, const uint8_t* w, float* out, hipStream_t st) {
+    const uint64_t n = (uint64_t)L.rows * ((L.cols + 7u) / 8u);
+    hipLaunchKernelGGL(k_gguf_dequant<FMT>, dim3((uint32_t)((n + 255u) / 256u)), dim3(256), 0, st, L, w, out);
+    return hipGetLastError();
+}
+
+template <uint32_t FMT, int NT>
+hipError_t matvec_nt(const vl_tiled_layout& L, const uint8_t* w, const float* x, uint32_t tokens,
+                     float* y, uint32_t* status, hipStream_t st) {
+    hipLaunchKernelGGL((k_gguf_matvec<FMT, NT>), dim3(L.rows), dim3(256), 0, st, L, w, x,
+                       tokens, y, status);
+    return hipGetLastError();
+}
+
+template <uint32_t FMT>
+hipError_t matvec_fmt(const vl_tiled_layout& L, const uint8_t* w, const float* x, uint32_t tokens,
+                      float* y, uint32_t* status, hipStream_t st) {
+    switch (limb_slots(tokens)) {
+        case 1: return matvec_nt<FMT, 1>(L, w, x, tokens, y, status, st);
+        case 2: return matvec_nt<FMT, 2>(L, w, x, tokens, y, status, st);
+        case 4: return matvec_nt<FMT, 4>(L, w, x, tokens, y, status, st);
+        default: return matvec_nt<FMT, 8>(L, w, x, tokens, y, status, st);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gguf_copy_rows(const vl_tiled_layout& L, const uint8_t* gguf_row0, uint8_t* dst,
+                                 uint32_t row0, uint32_t row1, hipStream_t stream) {
+    if (row0 >= row1 || row1 > L.rows) return hipErrorInvalidValue;
+    const uint64_t rb = L.gguf_bytes / L.rows;
+    return hipMemcpyAsync(dst + (uint64_t)row0 * rb, gguf_row0, (uint64_t)(row1 - row0) * rb,
+                          hipMemcpyDeviceToDevice, stream);
+}
+
+hipError_t launch_gguf_dequant(const vl_tiled_layout& L, const uint8_t* w, float* out, hipStream_t stream) {
+    switch (L.type) {
+        case VL_TYPE_Q4_K: return dequant_fmt<VL_TYPE_Q4_K>(L, w, out, stream);
+        case VL_TYPE_Q5_K: return dequant_fmt<VL_TYPE_Q5_K>(L, w, out, stream);
+        case VL_TYPE_Q6_K: return dequant_fmt<VL_TYPE_Q6_K>(L, w, out, stream);
+        case VL_TYPE_MXFP4: return dequant_fmt<VL_TYPE_MXFP4>(L, w, out, stream);
+        case VL_TYPE_BF16: return dequant_fmt<VL_TYPE_BF16>(L, w, out, stream);
+        case VL_TYPE_F32: return dequant_fmt<VL_TYPE_F32>(L, w, out, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gguf_matvec(const vl_tiled_layout& L, const uint8_t* w, const float* x, uint32_t tokens,
+                              float* y, uint8_t* workspace, hipStream_t stream) {
+    if (tokens == 0 || tokens > 8) return hipErrorInvalidValue;
+    uint32_t* status = reinterpret_cast<uint32_t*>(workspace);
+    hipLaunchKernelGGL(k_gguf_clear_status, dim3(1), dim3(64), 0, stream, status);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (L.type) {
+        case VL_TYPE_Q4_K: return matvec_fmt<VL_TYPE_Q4_K>(L, w, x, tokens, y, status, stream);
+        case VL_TYPE_Q5_K: return matvec_fmt<VL_TYPE_Q5_K>(L, w, x, tokens, y, status, stream);
+        case VL_TYPE_Q6_K: return matvec_fmt<VL_TYPE_Q6_K>(L, w, x, tokens, y, status, stream);
+        case VL_TYPE_MXFP4: return matvec_fmt<VL_TYPE_MXFP4>(L, w, x, tokens, y, status, stream);
+        case VL_TYPE_BF16: return matvec_fmt<VL_TYPE_BF16>(L, w, x, tokens, y, status, stream);
+        case VL_TYPE_F32: return matvec_fmt<VL_TYPE_F32>(L, w, x, tokens, y, status, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace vl

@@ -646,9 +646,12 @@ struct vl_accel {
 
 namespace {
 
+// Every type with a device layout: the four tiled types and the GGUF-layout ones (Q4_K, Q5_K,
+// Q6_K, MXFP4, BF16, F32), the storage types the reference's accelerator takes
+// (src/cuda/cuda_matvec_accelerator.cpp:46-58).
 bool has_kernel(uint32_t type) {
-    return type == VL_GGML_Q8_0 || type == VL_GGML_IQ2_XXS || type == VL_GGML_IQ3_XXS ||
-           type == VL_GGML_IQ1_S;
+    uint32_t elems = 0, bytes = 0;
+    return vl_block_shape(type, &elems, &bytes) != 0;
 }
 
 // Counts a declined storage type in the first free or matching slot; types beyond the slots go

@@ -50,6 +50,15 @@ hipError_t launch_matvec(const vl_tiled_layout& L, const uint8_t* w, const float
                          uint32_t tokens, float* y, uint8_t* workspace, uint32_t blocks,
                          hipStream_t stream);
 
+// The GGUF-layout types (vl_type_tiled() false), in vl_gguf.hip; launch_pack_rows,
+// launch_dequant and launch_matvec hand these types on to them.
+hipError_t launch_gguf_copy_rows(const vl_tiled_layout& L, const uint8_t* gguf_row0, uint8_t* dst,
+                                 uint32_t row0, uint32_t row1, hipStream_t stream);
+hipError_t launch_gguf_dequant(const vl_tiled_layout& L, const uint8_t* w, float* out,
+                               hipStream_t stream);
+hipError_t launch_gguf_matvec(const vl_tiled_layout& L, const uint8_t* w, const float* x,
+                              uint32_t tokens, float* y, uint8_t* workspace, hipStream_t stream);
+
 }  // namespace vl
 
 #endif  // VL_KERNELS_H

@@ -8,6 +8,9 @@
 //               the matrix's (tile, superblock) units; the last wave of each tile adds the
 //               tile's partials in a fixed order and writes the rows
 //
+// Q4_K, Q5_K, Q6_K, MXFP4, BF16 and F32 matrices stay in their GGUF bytes and are handed on to the
+// kernels of vl_gguf.hip by the launchers below.
+//
 // Numerics of k_matvec: every product w*x is formed exactly in integers (weights are exact small
 // integers times a per-group float factor, activations are 30-bit fixed point per 256-column
 // block); each group's int32 MFMA result is scaled by the group's integer scale, summed exactly
@@ -134,6 +137,7 @@ __global__ void k_pack(vl_tiled_layout L, const uint8_t* __restrict__ gguf,
 
 hipError_t launch_pack_rows(const vl_tiled_layout& L, const uint8_t* gguf_row0, uint8_t* tiled,
                             uint32_t row0, uint32_t row1, hipStream_t stream) {
+    if (!vl_type_tiled(L.type)) return launch_gguf_copy_rows(L, gguf_row0, tiled, row0, row1, stream);
     if (row0 >= row1 || row1 > L.rows_padded) return hipErrorInvalidValue;
     const uint64_t units = (uint64_t)(row1 - row0) * (L.type == VL_TYPE_Q8_0 ? L.groups : L.superblocks);
     const uint32_t block = 256;
@@ -215,6 +219,7 @@ static hipError_t launch_dequant_fmt(const vl_tiled_layout& L, const uint8_t* ti
 
 hipError_t launch_dequant(const vl_tiled_layout& L, const uint8_t* tiled, float* out,
                           hipStream_t stream) {
+    if (!vl_type_tiled(L.type)) return launch_gguf_dequant(L, tiled, out, stream);
     switch (L.type) {
         case VL_TYPE_IQ2_XXS: return launch_dequant_fmt<VL_TYPE_IQ2_XXS>(L, tiled, out, stream);
         case VL_TYPE_IQ3_XXS: return launch_dequant_fmt<VL_TYPE_IQ3_XXS>(L, tiled, out, stream);
@@ -251,8 +256,9 @@ static MatvecWs matvec_ws(uint32_t rows, uint32_t cols, uint32_t tokens, uint32_
     return m;
 }
 
-uint64_t matvec_workspace_bytes(uint32_t, uint32_t rows, uint32_t cols, uint32_t tokens,
+uint64_t matvec_workspace_bytes(uint32_t type, uint32_t rows, uint32_t cols, uint32_t tokens,
                                 uint32_t blocks) {
+    if (!vl_type_tiled(type)) return 256u;  // the status word alone
     return matvec_ws(rows, cols, tokens, blocks).bytes;
 }
 
@@ -426,6 +432,7 @@ static hipError_t launch_matvec_fmt(const vl_tiled_layout& L, const uint8_t* w, 
 hipError_t launch_matvec(const vl_tiled_layout& L, const uint8_t* w, const float* x,
                          uint32_t tokens, float* y, uint8_t* workspace, uint32_t blocks,
                          hipStream_t stream) {
+    if (!vl_type_tiled(L.type)) return launch_gguf_matvec(L, w, x, tokens, y, workspace, stream);
     if (tokens == 0 || tokens > 8 || L.cols % 32u != 0 || blocks == 0) return hipErrorInvalidValue;
     const MatvecWs m = matvec_ws(L.rows, L.cols, tokens, blocks);
     hipLaunchKernelGGL(k_prep_x, dim3(m.xblocks), dim3(256), 0, stream, x, L.cols, tokens,

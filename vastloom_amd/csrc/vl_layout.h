@@ -1,5 +1,8 @@
 // Device-resident ("tiled") layout of a quantized expert matrix, shared by host and device code.
 //
+// Q4_K, Q5_K, Q6_K, MXFP4, BF16 and F32 matrices are not rearranged: they stay in their GGUF bytes
+// (vl_type_tiled); everything below describes the four tiled types.
+//
 // The GGUF block bytes of a matrix are rearranged once, when the matrix becomes resident, into
 // planes that the matvec kernels read with aligned 16-byte loads. The rearrangement moves whole
 // bit fields and never changes a value: the tiled matrix holds exactly the GGUF bytes (66, 98,
@@ -39,6 +42,11 @@
 #define VL_TYPE_IQ2_XXS 16u
 #define VL_TYPE_IQ3_XXS 18u
 #define VL_TYPE_IQ1_S 19u
+#define VL_TYPE_Q4_K 12u
+#define VL_TYPE_Q5_K 13u
+#define VL_TYPE_Q6_K 14u
+#define VL_TYPE_BF16 30u
+#define VL_TYPE_MXFP4 39u
 
 #define VL_TILE_ROWS 32u
 
@@ -64,8 +72,22 @@ static inline VL_HD int vl_block_shape(uint32_t type, uint32_t* elements, uint32
         case VL_TYPE_IQ2_XXS: *elements = 256u; *bytes = 66u; return 1;
         case VL_TYPE_IQ3_XXS: *elements = 256u; *bytes = 98u; return 1;
         case VL_TYPE_IQ1_S: *elements = 256u; *bytes = 50u; return 1;
+        case VL_TYPE_Q4_K: *elements = 256u; *bytes = 144u; return 1;
+        case VL_TYPE_Q5_K: *elements = 256u; *bytes = 176u; return 1;
+        case VL_TYPE_Q6_K: *elements = 256u; *bytes = 210u; return 1;
+        case VL_TYPE_MXFP4: *elements = 32u; *bytes = 17u; return 1;
+        case VL_TYPE_BF16: *elements = 1u; *bytes = 2u; return 1;
+        case VL_TYPE_F32: *elements = 1u; *bytes = 4u; return 1;
         default: return 0;
     }
+}
+
+// Whether a type is rearranged into the tiled planes above (the types the MFMA matvec and the
+// MoE layer kernels read). The other types keep their GGUF bytes unchanged on the device: the
+// layout's "tiled" matrix is then the GGUF matrix itself (rows_padded = rows, one plane).
+static inline VL_HD int vl_type_tiled(uint32_t type) {
+    return type == VL_TYPE_Q8_0 || type == VL_TYPE_IQ2_XXS || type == VL_TYPE_IQ3_XXS ||
+           type == VL_TYPE_IQ1_S;
 }
 
 // Fills *out; returns 0 for an unsupported type or a column count that is not a whole number
@@ -77,7 +99,8 @@ static inline VL_HD int vl_make_layout(uint32_t type, uint32_t rows, uint32_t co
     vl_tiled_layout L;
     L.type = type;
     L.rows = rows;
-    L.rows_padded = (rows + VL_TILE_ROWS - 1u) / VL_TILE_ROWS * VL_TILE_ROWS;
+    L.rows_padded = vl_type_tiled(type) ? (rows + VL_TILE_ROWS - 1u) / VL_TILE_ROWS * VL_TILE_ROWS
+                                        : rows;
     L.tiles = L.rows_padded / VL_TILE_ROWS;
     L.cols = cols;
     L.block_elements = be;
@@ -86,6 +109,12 @@ static inline VL_HD int vl_make_layout(uint32_t type, uint32_t rows, uint32_t co
     L.superblocks = cols / 256u;
     const uint64_t rp = L.rows_padded;
     L.gguf_bytes = (uint64_t)rows * (cols / be) * bb;
+    if (!vl_type_tiled(type)) {
+        L.plane0 = L.plane1 = L.plane2 = 0;
+        L.bytes = L.gguf_bytes;
+        *out = L;
+        return 1;
+    }
     switch (type) {
         case VL_TYPE_IQ2_XXS:
             L.plane0 = 0;

@@ -50,6 +50,7 @@ bool moe_shape_ok(const MoeShape& s) {
     if (s.tokens > kMoeMaxTokens &&
         ((uint64_t)s.tokens * s.top_k > kMoeMaxGroupAssign || max_groups(s) > kMoeMaxGroups))
         return false;
+    if (!vl_type_tiled(s.gate_type) || !vl_type_tiled(s.down_type)) return false;
     if (!vl_block_shape(s.gate_type, &be, &bb) || s.width % be || s.width % 256u) return false;
     if (!vl_block_shape(s.down_type, &be, &bb) || s.inter % be || s.inter % 32u) return false;
     if (s.semantics > kSemPlain || s.routing > kRouteGiven || s.score_fn > kScoreSigmoid) return false;

@@ -13,7 +13,9 @@ role, index])))``, so any one expert or matrix can be regenerated without the ot
 Block scales are binary16, rounded to nearest-even from the float32 draw. Payload bytes are
 uniform: for Q8_0 the int8 quants are uniform on [-127, 127]; for IQ2_XXS, IQ3_XXS and IQ1_S every
 byte is uniform on [0, 255], which always decodes (every grid index, sign field and scale field
-is valid). Matrices are in GGUF block layout, row-major: row r's blocks are contiguous.
+is valid); Q4_K/Q5_K/Q6_K draw their fp16 d (and dmin) scaled down by the 6-bit sub-block
+scales' range, MXFP4 an E8M0 scale in [2^-10, 2^-4], BF16 truncated normal values. Matrices are
+in GGUF block layout, row-major: row r's blocks are contiguous.
 
 Workload shapes (the model shapes they mimic are OLMoE-1B-7B experts and DeepSeek-class
 routed experts):
@@ -33,10 +35,13 @@ from dataclasses import dataclass, field
 import numpy as np
 
 F32, Q8_0, IQ2_XXS, IQ3_XXS, IQ1_S = 0, 8, 16, 18, 19
+Q4_K, Q5_K, Q6_K, BF16, MXFP4 = 12, 13, 14, 30, 39
 
 # (block elements, block bytes) of each GGUF storage type (ggml_quantization.hpp:13-28).
-BLOCK = {F32: (1, 4), Q8_0: (32, 34), IQ2_XXS: (256, 66), IQ3_XXS: (256, 98), IQ1_S: (256, 50)}
-TYPE_NAMES = {F32: "f32", Q8_0: "q8_0", IQ2_XXS: "iq2_xxs", IQ3_XXS: "iq3_xxs", IQ1_S: "iq1_s"}
+BLOCK = {F32: (1, 4), Q8_0: (32, 34), IQ2_XXS: (256, 66), IQ3_XXS: (256, 98), IQ1_S: (256, 50),
+         Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), BF16: (1, 2), MXFP4: (32, 17)}
+TYPE_NAMES = {F32: "f32", Q8_0: "q8_0", IQ2_XXS: "iq2_xxs", IQ3_XXS: "iq3_xxs", IQ1_S: "iq1_s",
+              Q4_K: "q4_k", Q5_K: "q5_k", Q6_K: "q6_k", BF16: "bf16", MXFP4: "mxfp4"}
 
 
 def storage_bytes(qtype: int, rows: int, cols: int) -> int:
@@ -61,7 +66,26 @@ def random_matrix(rng: np.random.Generator, qtype: int, rows: int, cols: int,
     be, bb = BLOCK[qtype]
     if qtype == F32:
         return rng.standard_normal(rows * cols).astype(np.float32).view(np.uint8)
+    if qtype == BF16:  # N(0, scale_factor) truncated to its upper 16 bits
+        v = (rng.standard_normal(rows * cols) * scale_factor).astype(np.float32)
+        return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
     blocks = rows * (cols // be)
+    if qtype == MXFP4:  # E8M0 scales 2^-10 .. 2^-4, uniform code bytes
+        out = rng.integers(0, 256, size=(blocks, bb), dtype=np.uint8)
+        out[:, 0] = rng.integers(118, 125, size=blocks, dtype=np.uint8)
+        return out.reshape(-1)
+    if qtype == Q6_K:  # fp16 d at byte 208; quants and int8 sub-block scales uniform
+        scales = _fp16_scales(rng, blocks, scale_factor / 32.0)
+        out = rng.integers(0, 256, size=(blocks, bb), dtype=np.uint8)
+        out[:, 208] = scales & 0xFF
+        out[:, 209] = scales >> 8
+        return out.reshape(-1)
+    if qtype in (Q4_K, Q5_K):  # fp16 d and dmin, then uniform scale and quant bytes
+        scales = _fp16_scales(rng, 2 * blocks, scale_factor / 16.0).reshape(blocks, 2)
+        out = rng.integers(0, 256, size=(blocks, bb), dtype=np.uint8)
+        out[:, 0], out[:, 1] = scales[:, 0] & 0xFF, scales[:, 0] >> 8
+        out[:, 2], out[:, 3] = scales[:, 1] & 0xFF, scales[:, 1] >> 8
+        return out.reshape(-1)
     scales = _fp16_scales(rng, blocks, scale_factor)
     out = np.empty((blocks, bb), np.uint8)
     out[:, 0] = scales & 0xFF

@@ -2,19 +2,21 @@
 // Q6_K, MXFP4, BF16 and F32 (vl_type_tiled() is false for them).
 //
 //   k_gguf_dequant   GGUF matrix -> float32 rows, bit-identical to the reference decoders
-//   k_gguf_matvec    y[token][row] = W x[token] for up to eight tokens, one block per row
+//   k_gguf_matvec    y[token][row] = W x[token] for up to eight tokens, four rows per block
 //
 // These matrices are read as they are stored, row-major with each row's blocks contiguous, so
 // making one resident is a device copy. A "piece" is eight consecutive weights of a row; a block
 // holds a whole number of pieces (32 for the 256-weight K-quants, 4 for MXFP4), so a piece never
-// crosses a block. A 256-thread block takes one row: thread i decodes the pieces i, i + 256, ...
-// of the row, four at a time with all four pieces' loads issued before the first is decoded,
-// and accumulates w * x in float per token; the block then adds its 256 partial sums per token
-// in a fixed order.
-// The weights themselves are formed exactly as the reference forms them (each product and
-// difference rounded once, in the reference's order, fp contraction off), so the dequantize
-// kernel is bit-exact and the matvec differs from the reference's float64 accumulation only by
-// float rounding of the partial sums.
+// crosses a block. A 256-thread block takes four rows: thread i decodes the pieces i, i + 256,
+// ... of each, two pieces per row at a time with all their loads issued before the first is
+// decoded, and accumulates w * x in float per row and token (the activations of a piece are
+// loaded once for the four rows; block and sub-block factors multiply the piece's sum of
+// integer code times x rather than each weight); the block then adds its 256 partial sums per
+// row and token in a fixed order.
+// The dequantize kernel forms each weight exactly as the reference does (each product and
+// difference rounded once, in the reference's order, fp contraction off) and is bit-exact; the
+// matvec differs from the reference's float64 accumulation only by float rounding of its
+// partial sums.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -125,10 +127,8 @@ __device__ __forceinline__ void load_piece(const uint8_t* row, uint32_t p, uint3
     } else {  // Q4_K, Q5_K: 144- and 176-byte blocks keep 16-byte alignment
         const uint32_t q = p & 31u, j = q >> 2, l0 = (q & 3u) * 8u;
         const uint8_t* blk = row + (uint64_t)Fmt<FMT>::bb * (p >> 5);
-        r.a = ld_u32(blk);
-        r.b = ld_u32(blk + 4);
-        r.c = ld_u32(blk + 8);
-        r.d = ld_u32(blk + 12);
+        const u32x4 head = ld_u128(blk);  // d, dmin and the 12 scale bytes
+        r.a = head.x; r.b = head.y; r.c = head.z; r.d = head.w;
         if constexpr (FMT == VL_TYPE_Q5_K) {
             r.h = ld_u64(blk + 16u + l0);
             r.q = ld_u64(blk + 48u + 32u * (j >> 1) + l0);
@@ -223,85 +223,191 @@ __global__ void __launch_bounds__(256) k_gguf_dequant(vl_tiled_layout L, const u
     }
 }
 
+// Four unsigned bytes of a word as floats (v_cvt_f32_ubyte0..3).
+__device__ __forceinline__ void bytes_float(uint32_t v, float* f) {
+    f[0] = (float)(v & 0xffu);
+    f[1] = (float)((v >> 8) & 0xffu);
+    f[2] = (float)((v >> 16) & 0xffu);
+    f[3] = (float)(v >> 24);
+}
+
+// acc[t] += sum_i w_i x[t][i] over piece p, for the matvec. The block and sub-block factors are
+// taken out of the sum: K-quant pieces are d_j * sum q_i x_i - m_j * sum x_i (Q6_K:
+// d_s * (sum q_i x_i - 32 sum x_i)), MXFP4 pieces s * sum v_i x_i, with the small integer codes
+// converted straight from their bytes; sx[t] = sum_i x[t][i] is shared by the block's rows.
+// Only the rounding of these partial sums differs from forming each weight first.
+template <uint32_t FMT, int NT>
+__device__ __forceinline__ void piece_dot(const RawPiece& r, uint32_t p, const float (&xv)[NT][8],
+                                          const float (&sx)[NT], float (&acc)[NT]) {
+    if constexpr (FMT == VL_TYPE_F32 || FMT == VL_TYPE_BF16) {
+        float w[8];
+        decode_piece<FMT>(r, p, w);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[t] = fmaf(w[i], xv[t][i], acc[t]);
+    } else if constexpr (FMT == VL_TYPE_MXFP4) {
+        const uint32_t e = r.a;
+        const float s = bits_float(e < 2u ? 0x00200000u << e : (e - 1u) << 23);
+        const uint32_t shift = 4u * ((p & 3u) >> 1);
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c = (byte_of(r.q, i) >> shift) & 15u, m = c & 7u;
+            const int mag = m < 4u ? (int)m : (int)((m & 1u ? 6u : 4u) << ((m - 4u) >> 1));
+            v[i] = (float)(c & 8u ? -mag : mag);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) d = fmaf(v[i], xv[t][i], d);
+            acc[t] = fmaf(s, d, acc[t]);
+        }
+    } else {
+        float q[8];
+        float scale, offset;  // acc += scale * (sum q x) - offset * (sum x)
+        if constexpr (FMT == VL_TYPE_Q6_K) {
+            const uint32_t k = ((p & 31u) >> 2) & 3u;
+            const uint32_t sh = k < 2u ? 0u : 4u;
+            const uint32_t lo = (r.q.x >> sh) & 0x0f0f0f0fu, hi = (r.q.y >> sh) & 0x0f0f0f0fu;
+            bytes_float(lo | ((r.h.x >> (2u * k)) & 0x03030303u) << 4, q);
+            bytes_float(hi | ((r.h.y >> (2u * k)) & 0x03030303u) << 4, q + 4);
+            scale = half_bits_to_float(r.a) * (float)(int)(int8_t)(uint8_t)r.b;
+            offset = 32.0f * scale;
+        } else {  // Q4_K, Q5_K
+            const uint32_t j = (p & 31u) >> 2;
+            const float d = half_bits_to_float(r.a), dmin = half_bits_to_float(r.a >> 16);
+            uint32_t sc, mn;
+            if (j < 4u) {
+                sc = scale_byte(r.b, r.c, r.d, j) & 63u;
+                mn = scale_byte(r.b, r.c, r.d, j + 4u) & 63u;
+            } else {
+                const uint32_t x = scale_byte(r.b, r.c, r.d, j + 4u);
+                sc = (x & 15u) | (scale_byte(r.b, r.c, r.d, j - 4u) >> 6) << 4;
+                mn = (x >> 4) | (scale_byte(r.b, r.c, r.d, j) >> 6) << 4;
+            }
+            const uint32_t sh = 4u * (j & 1u);
+            uint32_t lo = (r.q.x >> sh) & 0x0f0f0f0fu, hi = (r.q.y >> sh) & 0x0f0f0f0fu;
+            if constexpr (FMT == VL_TYPE_Q5_K) {
+                lo |= ((r.h.x >> j) & 0x01010101u) << 4;
+                hi |= ((r.h.y >> j) & 0x01010101u) << 4;
+            }
+            bytes_float(lo, q);
+            bytes_float(hi, q + 4);
+            scale = d * (float)sc;
+            offset = dmin * (float)mn;
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) d = fmaf(q[i], xv[t][i], d);
+            acc[t] = fmaf(scale, d, fmaf(-offset, sx[t], acc[t]));
+        }
+    }
+}
+
 __global__ void k_gguf_clear_status(uint32_t* status) {
     if (threadIdx.x == 0) *status = 0u;
 }
 
-constexpr int kPiecesInFlight = 4;
+constexpr int kPiecesInFlight = 2;
 
-// One row per 256-thread block; thread i takes pieces i, i + 256, ... of the row, all of a
-// thread's loads (up to kPiecesInFlight pieces) issued before the first piece is decoded.
+constexpr uint32_t kRowsPerBlock = 4;
+
+// kRowsPerBlock rows per 256-thread block; thread i takes pieces i, i + 256, ... of each of the
+// block's rows, so that the activations it loads for a piece serve all of them, and issues the
+// loads of kPiecesInFlight pieces of every row before it decodes the first.
 // NT = token slots (tokens <= NT).
 template <uint32_t FMT, int NT>
 __global__ void __launch_bounds__(256) k_gguf_matvec(vl_tiled_layout L, const uint8_t* __restrict__ W,
                                                      const float* __restrict__ x, uint32_t tokens,
                                                      float* __restrict__ y, uint32_t* status) {
-    __shared__ float part[4][NT];
+    constexpr uint32_t R = kRowsPerBlock;
+    __shared__ float part[4][R][NT];
     __shared__ uint32_t bad[4];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t row = blockIdx.x;  // grid = rows
+    const uint32_t row0 = blockIdx.x * R;  // grid = ceil(rows / R)
+    const uint32_t nrows = L.rows - row0 < R ? L.rows - row0 : R;
     const uint32_t cols = L.cols, ppr = (cols + 7u) / 8u;
     const bool whole = (cols & 7u) == 0u;
-    const uint8_t* rp = W + (uint64_t)row * row_bytes<FMT>(cols);
-    float acc[NT];
+    const uint64_t rb = row_bytes<FMT>(cols);
+    const uint8_t* rp = W + (uint64_t)row0 * rb;
+    float acc[R][NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    for (uint32_t rr = 0; rr < R; ++rr)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[rr][t] = 0.0f;
     bool bad_x = false;
     for (uint32_t base = tid; base < ppr; base += 256u * kPiecesInFlight) {
-        RawPiece r[kPiecesInFlight];
+        RawPiece r[kPiecesInFlight][R];
 #pragma unroll
         for (int u = 0; u < kPiecesInFlight; ++u) {
             const uint32_t p = base + 256u * u;
-            if (p < ppr) load_piece<FMT>(rp, p, cols, r[u]);
+#pragma unroll
+            for (uint32_t rr = 0; rr < R; ++rr)
+                if (p < ppr && rr < nrows) load_piece<FMT>(rp + rr * rb, p, cols, r[u][rr]);
         }
 #pragma unroll
         for (int u = 0; u < kPiecesInFlight; ++u) {
             const uint32_t p = base + 256u * u;
             if (p >= ppr) break;
-            float wv[8];
-            decode_piece<FMT>(r[u], p, wv);
+            float xv[NT][8];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                if (t >= (int)tokens) break;
                 const float* xp = x + (uint64_t)t * cols + 8u * p;
-                float xv[8];
-                if (whole) {
+                if (t >= (int)tokens) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) xv[t][i] = 0.0f;
+                } else if (whole) {
                     const f32x4 a = *gp(reinterpret_cast<const f32x4*>(xp));
                     const f32x4 b = *gp(reinterpret_cast<const f32x4*>(xp + 4));
-                    xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-                    xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+                    xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
+                    xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) xv[i] = 8u * p + i < cols ? xp[i] : 0.0f;
+                    for (int i = 0; i < 8; ++i) xv[t][i] = 8u * p + i < cols ? xp[i] : 0.0f;
                 }
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    bad_x |= !__builtin_isfinite(xv[i]);
-                    acc[t] = fmaf(wv[i], xv[i], acc[t]);
-                }
+                for (int i = 0; i < 8; ++i) bad_x |= !__builtin_isfinite(xv[t][i]);
+            }
+            float sx[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                sx[t] = ((xv[t][0] + xv[t][1]) + (xv[t][2] + xv[t][3])) +
+                        ((xv[t][4] + xv[t][5]) + (xv[t][6] + xv[t][7]));
+#pragma unroll
+            for (uint32_t rr = 0; rr < R; ++rr) {
+                if (rr >= nrows) break;
+                piece_dot<FMT, NT>(r[u][rr], p, xv, sx, acc[rr]);
             }
         }
     }
     // Each wave adds its lanes, then thread 0 adds the four waves' sums in wave order.
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
+    for (uint32_t rr = 0; rr < R; ++rr)
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) acc[t] += __shfl_xor(acc[t], off, 64);
-    }
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) acc[rr][t] += __shfl_xor(acc[rr][t], off, 64);
     const bool wave_bad = __ballot(bad_x) != 0ull;
     if (lane == 0) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) part[wave][t] = acc[t];
+        for (uint32_t rr = 0; rr < R; ++rr)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) part[wave][rr][t] = acc[rr][t];
         bad[wave] = wave_bad ? 1u : 0u;
     }
     __syncthreads();
     if (tid == 0) {
         uint32_t bits = (bad[0] | bad[1] | bad[2] | bad[3]) ? kStatusNonFiniteInput : 0u;
-        for (uint32_t t = 0; t < tokens && t < (uint32_t)NT; ++t) {
-            const float v = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
-            y[(uint64_t)t * L.rows + row] = v;
-            if (!__builtin_isfinite(v)) bits |= kStatusNonFiniteOutput;
-        }
+        for (uint32_t rr = 0; rr < nrows; ++rr)
+            for (uint32_t t = 0; t < tokens && t < (uint32_t)NT; ++t) {
+                const float v = ((part[0][rr][t] + part[1][rr][t]) + part[2][rr][t]) + part[3][rr][t];
+                y[(uint64_t)t * L.rows + row0 + rr] = v;
+                if (!__builtin_isfinite(v)) bits |= kStatusNonFiniteOutput;
+            }
         if (bits) or_bits(status, bits);
     }
 }
@@ -316,7 +422,7 @@ hipError_t dequant_fmt(const vl_tiled_layout& L, const uint8_t* w, float* out, h
 template <uint32_t FMT, int NT>
 hipError_t matvec_nt(const vl_tiled_layout& L, const uint8_t* w, const float* x, uint32_t tokens,
                      float* y, uint32_t* status, hipStream_t st) {
-    hipLaunchKernelGGL((k_gguf_matvec<FMT, NT>), dim3(L.rows), dim3(256), 0, st, L, w, x,
+    hipLaunchKernelGGL((k_gguf_matvec<FMT, NT>), dim3((L.rows + kRowsPerBlock - 1u) / kRowsPerBlock), dim3(256), 0, st, L, w, x,
                        tokens, y, status);
     return hipGetLastError();
 }

@@ -33,6 +33,9 @@ def _csvs(d: str, suffix: str) -> list[Path]:
 
 
 def _short(name: str) -> str:
+    """A kernel's name without its parameter list, return type or anonymous-namespace part."""
+    name = name.replace("(anonymous namespace)::", "")
+    name = re.sub(r"^void ", "", name)
     return re.sub(r"\(.*", "", name).strip()
 
 

@@ -41,8 +41,8 @@ typedef enum vl_status {
 
 /* GGUF storage type ids (include/vastloom/inference/ggml_quantization.hpp:34-45). Q8_0 and the
  * three IQ types are rearranged ("tiled") when they become resident and are the types the MoE
- * layer entry points take; Q4_K, Q5_K, Q6_K, MXFP4, BF16 and F32 stay in their GGUF bytes and
- * have device dequantize and matvec through the same matrix entry points. */
+ * layer entry points take; Q4_K, Q5_K, Q6_K, IQ2_S, MXFP4, BF16 and F32 stay in their GGUF bytes
+ * and have device dequantize and matvec through the same matrix entry points. */
 #define VL_GGML_F32 0u
 #define VL_GGML_Q8_0 8u
 #define VL_GGML_Q4_K 12u
@@ -51,6 +51,7 @@ typedef enum vl_status {
 #define VL_GGML_IQ2_XXS 16u
 #define VL_GGML_IQ3_XXS 18u
 #define VL_GGML_IQ1_S 19u
+#define VL_GGML_IQ2_S 22u
 #define VL_GGML_BF16 30u
 #define VL_GGML_MXFP4 39u
 
@@ -104,7 +105,7 @@ int vl_pack_matrix(uint32_t ggml_type, uint64_t rows, uint64_t cols, const void*
                    void* tiled_device, void* stream);
 
 /* Decode a tiled matrix to float32 rows [rows][cols], bit-identical to the reference decoders
- * (dequantize_q8_0 / _q4_k / _q5_k / _q6_k / _iq2_xxs / _iq3_xxs / _iq1_s / _mxfp4 / _bf16 /
+ * (dequantize_q8_0 / _q4_k / _q5_k / _q6_k / _iq2_xxs / _iq2_s / _iq3_xxs / _iq1_s / _mxfp4 / _bf16 /
  * _f32_le, ggml_quantization.hpp:99-266). */
 int vl_dequantize(uint32_t ggml_type, uint64_t rows, uint64_t cols, const void* tiled_device,
                   float* out_device, void* stream);
@@ -117,7 +118,7 @@ int vl_matvec_workspace(uint32_t ggml_type, uint64_t rows, uint64_t cols, uint32
 /* y[t][r] = sum_c W[r][c] * x[t][c] for t < tokens (1..8); x is [tokens][cols] float32, y is
  * [tokens][rows] float32, both on the device. The device-resident counterpart of the reference
  * matvecs (matvec_q8_0_f32 / _iq2_xxs_f32 / _iq3_xxs_f32 / _iq1_s_f32 and, for the GGUF-layout
- * types, matvec_q4_k_f32 / _q5_k / _q6_k / _mxfp4 / _bf16 / _f32_le_f32,
+ * types, matvec_q4_k_f32 / _q5_k / _q6_k / _iq2_s / _mxfp4 / _bf16 / _f32_le_f32,
  * ggml_quantization.hpp:99-266) and of the CudaDriver *_with_transfer launches
  * (src/cuda/cuda_driver.cpp:2083-2180) without their per-call transfers. Asynchronous on the
  * stream; the workspace's status word (vl_read_status) reports non-finite inputs or outputs,

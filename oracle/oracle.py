@@ -20,7 +20,7 @@ ORACLE_SO = HERE / "_build" / "liboracle.so"
 REF_SO = HERE / "_ref" / "libvlref.so"
 
 F32, Q8_0, IQ2_XXS, IQ3_XXS, IQ1_S = 0, 8, 16, 18, 19
-Q4_K, Q5_K, Q6_K, BF16, MXFP4 = 12, 13, 14, 30, 39
+Q4_K, Q5_K, Q6_K, IQ2_S, BF16, MXFP4 = 12, 13, 14, 22, 30, 39
 SCORE_SQRT_SOFTPLUS, SCORE_SIGMOID = 0, 1
 DEFAULT_MAX_ELEMENTS = 64_000_000
 

@@ -49,6 +49,7 @@ VLR_EXPORT int vlr_dequantize(std::uint32_t type, const std::uint8_t* enc, std::
         case vi::kGgmlTypeQ6K: return status(vi::dequantize_q6_k(bytes(enc, enc_bytes), o, limits));
         case vi::kGgmlTypeMxfp4: return status(vi::dequantize_mxfp4(bytes(enc, enc_bytes), o, limits));
         case vi::kGgmlTypeBf16: return status(vi::dequantize_bf16(bytes(enc, enc_bytes), o, limits));
+        case vi::kGgmlTypeIq2S: return status(vi::dequantize_iq2_s(bytes(enc, enc_bytes), o, limits));
         default: return 1 + static_cast<int>(vastloom::ErrorCode::unsupported);
     }
 }

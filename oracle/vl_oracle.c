@@ -153,6 +153,32 @@ static void decode_f32(const uint8_t* block, float* out) {
     memcpy(out, &bits, sizeof bits);
 }
 
+/* IQ2_S: 82 bytes -> 256 weights (ggml_quantization.cpp:285-334). fp16 d, 32 low index bytes,
+ * 32 explicit sign bytes, 8 high-bit bytes (two index bits per sub-block) and 8 scale bytes
+ * (low nibble for sub-blocks 0-1 of a group, high nibble for 2-3):
+ * w = ((d * (0.5 + nibble)) * 0.25) * grid magnitude * sign. */
+static void decode_iq2_s(const uint8_t* block, float* out) {
+    const float d = vlo_fp16_to_f32(le16(block));
+    const uint8_t* qs = block + 2;
+    const uint8_t* signs = block + 34;
+    const uint8_t* high = block + 66;
+    const uint8_t* scales = block + 74;
+    for (unsigned g = 0; g < 8u; ++g) {
+        const float ls_low = d * (0.5f + (float)(scales[g] & 15u)) * 0.25f;
+        const float ls_high = d * (0.5f + (float)(scales[g] >> 4)) * 0.25f;
+        for (unsigned s = 0; s < 4u; ++s) {
+            const unsigned index = qs[4u * g + s] | (((unsigned)high[g] >> (2u * s)) & 3u) << 8;
+            const uint64_t grid = g_books.iq2s[index];
+            const unsigned sg = signs[4u * g + s];
+            const float ls = s < 2u ? ls_low : ls_high;
+            for (unsigned l = 0; l < 8u; ++l) {
+                const float mag = (float)((grid >> (8u * l)) & 0xffu);
+                out[32u * g + 8u * s + l] = ls * mag * ((sg >> l) & 1u ? -1.0f : 1.0f);
+            }
+        }
+    }
+}
+
 /* The 6-bit scale and minimum of sub-block j of a Q4_K/Q5_K superblock, packed into 12 bytes:
  * bytes 0..3 hold scales 0..3 in their low six bits, bytes 4..7 minimums 0..3 likewise; for
  * j >= 4 the low four bits come from byte j+4 (scale: low nibble, minimum: high nibble) and the
@@ -297,6 +323,7 @@ static int layout_checked(uint32_t type, size_t* elements, size_t* bytes, block_
         case VLO_IQ2_XXS: *elements = 256; *bytes = 66; *decoder = decode_iq2_xxs; return VLO_OK;
         case VLO_IQ3_XXS: *elements = 256; *bytes = 98; *decoder = decode_iq3_xxs; return VLO_OK;
         case VLO_IQ1_S: *elements = 256; *bytes = 50; *decoder = decode_iq1_s; return VLO_OK;
+        case VLO_IQ2_S: *elements = 256; *bytes = 82; *decoder = decode_iq2_s; return VLO_OK;
         case VLO_BF16: *elements = 1; *bytes = 2; *decoder = decode_bf16; *check = check_bf16; return VLO_OK;
         case VLO_MXFP4: *elements = 32; *bytes = 17; *decoder = decode_mxfp4; *check = check_mxfp4; return VLO_OK;
         default: return VLO_E_UNSUPPORTED;

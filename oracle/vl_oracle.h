@@ -37,7 +37,7 @@ enum {
 /* GGML storage type ids (include/vastloom/inference/ggml_quantization.hpp:34-45). */
 enum {
     VLO_F32 = 0, VLO_Q8_0 = 8, VLO_Q4_K = 12, VLO_Q5_K = 13, VLO_Q6_K = 14, VLO_IQ2_XXS = 16,
-    VLO_IQ3_XXS = 18, VLO_IQ1_S = 19, VLO_BF16 = 30, VLO_MXFP4 = 39
+    VLO_IQ3_XXS = 18, VLO_IQ1_S = 19, VLO_IQ2_S = 22, VLO_BF16 = 30, VLO_MXFP4 = 39
 };
 
 enum { VLO_SCORE_SQRT_SOFTPLUS = 0, VLO_SCORE_SIGMOID = 1 };

@@ -261,8 +261,8 @@ int run(bool fake_device) {
         auto y3 = sentinel(rows);
         auto r3 = acc->matvec(anon, x, y3);
         check(r3.ok() && !r3.value() && untouched(y3), "no identity declined, output untouched");
-        std::vector<std::byte> iq2s(rows * (cols / 256) * 82);  // IQ2_S has no device kernel
-        auto q4 = matrix(inference::kGgmlTypeIq2S, rows, cols, iq2s, 0x52);
+        std::vector<std::byte> i32(rows * cols * 4);  // I32 storage has no device kernel
+        auto q4 = matrix(inference::kGgmlTypeI32, rows, cols, i32, 0x52);
         auto y4 = sentinel(rows);
         auto r4 = acc->matvec(q4, x, y4);
         check(r4.ok() && !r4.value() && untouched(y4), "type without a kernel declined, output untouched");

@@ -3,7 +3,8 @@
 The byte patterns, scales, inputs and expected outputs below are the reference's test data
 (tests/test_main.cpp:863-973 for Q8_0, :975-1054 Q4_K and Q5_K, :1056-1089 Q6_K, :1091-1112
 BF16, :1295-1365 IQ1_S, :1367-1460 IQ2_XXS, :1663-1723 the Q4_K and MXFP4 blocks the reference
-checked against ggml's own dequantize_row_q4_K / dequantize_row_mxfp4, :1832-1907 IQ3_XXS),
+checked against ggml's own dequantize_row_q4_K / dequantize_row_mxfp4, :1725-1790 IQ2_S,
+:1832-1907 IQ3_XXS),
 regenerated here from the same formulas so that the oracle and the HIP decoders can be held to
 the reference's pinned fingerprints and values.
 
@@ -132,6 +133,17 @@ def mxfp4_ggml_blocks() -> np.ndarray:
     return out.reshape(-1)
 
 
+def iq2_s_blocks() -> np.ndarray:
+    out = np.zeros((len(SCALES), 82), np.uint8)
+    for b, s in enumerate(SCALES):
+        out[b, 0], out[b, 1] = s & 0xFF, s >> 8
+        out[b, 2:34] = [(b * 733 + i * 977 + 0x1234) & 0xFF for i in range(32)]
+        out[b, 34:66] = [(b * 251 + i * 131 + 0x5AA5) & 0xFF for i in range(32)]
+        out[b, 66:74] = [(b * 97 + i * 43 + 0x3C) & 0xFF for i in range(8)]
+        out[b, 74:82] = [(b * 61 + i * 29 + 0x17) & 0xFF for i in range(8)]
+    return out.reshape(-1)
+
+
 def bf16_values() -> np.ndarray:
     return np.array([0x3F80, 0xC000, 0x3F00, 0x4080, 0xBF80, 0x4040, 0xBE80, 0x4000],
                     np.uint16).view(np.uint8)
@@ -192,6 +204,11 @@ KAT = {
         values={0: -0.0078125, 1: 0.00390625, 2: 0.0, 3: -0.046875, 4: 0.03125},
         cols=64, outputs=[],
         poison={0: 0xFF, 1: 0x77}),  # scale 2^127 times a code of 12
+    "iq2_s": dict(
+        qtype=22, block_elements=256, blocks=iq2_s_blocks, fnv=0x785968D455DE0695,
+        values={0: -15.0, 7: -15.0, 8: 15.0, 31: 3.0, 32: -9.0, 63: 21.875, 127: 40.625,
+                255: -29.0, 256: -4.5, 511: -8.0625},
+        cols=512, outputs=[(209.540527, 0.0), (274.050537, 0.0), (0.0192997903, 1e-9)]),
     "bf16": dict(
         qtype=30, block_elements=1, blocks=bf16_values, fnv=None, count=8,
         values={0: 1.0, 1: -2.0, 2: 0.5, 3: 4.0, 4: -1.0, 5: 3.0, 6: -0.25, 7: 2.0},

@@ -9,7 +9,8 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.oracle import BF16, F32, IQ1_S, IQ2_XXS, IQ3_XXS, MXFP4, Q4_K, Q5_K, Q6_K, Q8_0
+from oracle.oracle import (BF16, F32, IQ1_S, IQ2_S, IQ2_XXS, IQ3_XXS, MXFP4, Q4_K, Q5_K, Q6_K,
+                           Q8_0)
 from vastloom_amd import _lib
 from vastloom_amd.accel import (KIND_STAGING, KIND_VRAM, Accelerator, Buffer, Governor,
                                 PackedMatrix, VlError, default_limits)
@@ -36,7 +37,7 @@ CASES = [(Q8_0, 100, 512), (IQ2_XXS, 100, 1024), (IQ3_XXS, 33, 512), (IQ1_S, 31,
          (IQ2_XXS, 2048, 7168),
          # GGUF-layout types: resident as their GGUF bytes, uploaded in row ranges as the others.
          (Q4_K, 2048, 7168), (Q5_K, 100, 1024), (Q6_K, 77, 2048), (MXFP4, 45, 2880),
-         (BF16, 33, 100), (F32, 64, 512)]
+         (IQ2_S, 65, 2048), (BF16, 33, 100), (F32, 64, 512)]
 
 
 @pytest.mark.parametrize("qtype,rows,cols", CASES)

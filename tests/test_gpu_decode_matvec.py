@@ -12,7 +12,8 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.oracle import BF16, F32, IQ1_S, IQ2_XXS, IQ3_XXS, MXFP4, Q4_K, Q5_K, Q6_K, Q8_0
+from oracle.oracle import (BF16, F32, IQ1_S, IQ2_S, IQ2_XXS, IQ3_XXS, MXFP4, Q4_K, Q5_K, Q6_K,
+                           Q8_0)
 from tests.kat_blocks import KAT, fnv_f32, kat_count, kat_poisoned, kat_rows, kat_x
 from vastloom_amd.workloads import random_matrix
 
@@ -66,6 +67,7 @@ SHAPES = [
     (Q5_K, 65, 2048), (Q5_K, 2048, 7168),
     (Q6_K, 3, 512), (Q6_K, 67, 1792), (Q6_K, 2048, 7168), (Q6_K, 7168, 2048),
     (MXFP4, 3, 64), (MXFP4, 45, 2880), (MXFP4, 2880, 2880),
+    (IQ2_S, 3, 512), (IQ2_S, 65, 2048), (IQ2_S, 2048, 7168),
     (BF16, 2, 4), (BF16, 33, 100), (BF16, 1024, 2048),
     (F32, 5, 33), (F32, 512, 2048),
 ]
@@ -86,7 +88,8 @@ def test_extreme_scales_decode_bit_exact(ops, oracle):
     rng = np.random.default_rng(3)
     special = np.array([0x0001, 0x03FF, 0x0400, 0x7BFF, 0x8001, 0xFBFF, 0x0000], np.uint16)
     for qtype, rows, cols in ((Q8_0, 40, 256), (IQ2_XXS, 40, 512), (IQ3_XXS, 40, 512),
-                              (IQ1_S, 40, 512), (Q4_K, 40, 512), (Q5_K, 40, 512), (Q6_K, 40, 512)):
+                              (IQ1_S, 40, 512), (Q4_K, 40, 512), (Q5_K, 40, 512), (Q6_K, 40, 512),
+                              (IQ2_S, 40, 512)):
         print(f"[decode extreme] type={qtype}", flush=True)
         enc = random_matrix(rng, qtype, rows, cols, 0.01)
         be = 32 if qtype == Q8_0 else 256

@@ -11,7 +11,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from oracle.oracle import (BF16, IQ1_S, IQ2_XXS, IQ3_XXS, MXFP4, Q4_K, Q5_K, Q6_K, Q8_0,
+from oracle.oracle import (BF16, IQ1_S, IQ2_S, IQ2_XXS, IQ3_XXS, MXFP4, Q4_K, Q5_K, Q6_K, Q8_0,
                            SCORE_SQRT_SOFTPLUS, OracleError)
 from vastloom_amd.workloads import random_matrix, workload
 
@@ -24,6 +24,7 @@ SHAPES = {
     Q5_K: [(3, 512), (65, 2048), (512, 7168)],
     Q6_K: [(3, 512), (64, 1792), (1024, 2048)],
     MXFP4: [(3, 64), (45, 2880), (512, 2048)],
+    IQ2_S: [(3, 512), (65, 2048), (512, 7168)],
     BF16: [(2, 4), (33, 100), (512, 2048)],
 }
 
@@ -48,7 +49,7 @@ def test_subnormal_and_extreme_scales_bit_identical(oracle, reference):
     # fp16 subnormal, smallest normal and largest finite scales in every format.
     rng = np.random.default_rng(3)
     for qtype, (rows, cols) in ((Q8_0, (8, 256)), (IQ2_XXS, (8, 512)), (IQ3_XXS, (8, 512)),
-                                (IQ1_S, (8, 512))):
+                                (IQ1_S, (8, 512)), (IQ2_S, (8, 512))):
         enc = random_matrix(rng, qtype, rows, cols, 0.01)
         bb = enc.size // (rows * cols // (32 if qtype == Q8_0 else 256))
         blocks = enc.reshape(-1, bb)

@@ -17,6 +17,7 @@ typedef struct vl_expanded_codebooks {
     uint64_t iq2xxs[256];  /* eight unsigned magnitudes in {8, 25, 43} */
     uint32_t iq3xxs[256];  /* four unsigned magnitudes in {4, ..., 62} */
     uint64_t iq1s[2048];   /* eight int8 lanes in {-1, 0, +1} */
+    uint64_t iq2s[1024];   /* eight unsigned magnitudes in {8, 25, 43} */
 } vl_expanded_codebooks;
 
 static inline uint64_t vl_fnv1a_lanes(const void* table, unsigned entries, unsigned lane_bytes) {
@@ -35,6 +36,7 @@ static inline void vl_codebooks_expand(vl_expanded_codebooks* out) {
     static const uint16_t c2[256] = VL_IQ2XXS_CODES;
     static const uint16_t c3[256] = VL_IQ3XXS_CODES;
     static const uint16_t c1[2048] = VL_IQ1S_CODES;
+    static const uint16_t c2s[1024] = VL_IQ2S_CODES;
     static const uint8_t v2[4] = {8, 25, 43, 0};
     static const uint8_t v1[4] = {0x00, 0x01, 0xff, 0x00};
     for (unsigned e = 0; e < 256; ++e) {
@@ -53,12 +55,18 @@ static inline void vl_codebooks_expand(vl_expanded_codebooks* out) {
         for (unsigned l = 0; l < 8; ++l) g |= (uint64_t)v1[(c1[e] >> (2u * l)) & 3u] << (8u * l);
         out->iq1s[e] = g;
     }
+    for (unsigned e = 0; e < 1024; ++e) {
+        uint64_t g = 0;
+        for (unsigned l = 0; l < 8; ++l) g |= (uint64_t)v2[(c2s[e] >> (2u * l)) & 3u] << (8u * l);
+        out->iq2s[e] = g;
+    }
 }
 
 static inline int vl_codebooks_fingerprints_ok(const vl_expanded_codebooks* t) {
     return vl_fnv1a_lanes(t->iq2xxs, 256, 8) == VL_IQ2XXS_GRID_FNV &&
            vl_fnv1a_lanes(t->iq3xxs, 256, 4) == VL_IQ3XXS_GRID_FNV &&
-           vl_fnv1a_lanes(t->iq1s, 2048, 8) == VL_IQ1S_GRID_FNV;
+           vl_fnv1a_lanes(t->iq1s, 2048, 8) == VL_IQ1S_GRID_FNV &&
+           vl_fnv1a_lanes(t->iq2s, 1024, 8) == VL_IQ2S_GRID_FNV;
 }
 
 #endif /* VL_CODEBOOKS_EXPAND_H */

@@ -1,5 +1,5 @@
 // HIP kernels for the storage types that stay in their GGUF bytes on the device: Q4_K, Q5_K,
-// Q6_K, MXFP4, BF16 and F32 (vl_type_tiled() is false for them).
+// Q6_K, IQ2_S, MXFP4, BF16 and F32 (vl_type_tiled() is false for them).
 //
 //   k_gguf_dequant   GGUF matrix -> float32 rows, bit-identical to the reference decoders
 //   k_gguf_matvec    y[token][row] = W x[token] for up to eight tokens, four rows per block
@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "iq_codebooks.h"
 #include "vl_kernels.h"
 #include "vl_layout.h"
 #include "vl_stream.h"
@@ -27,6 +28,25 @@
 namespace vl {
 
 namespace {
+
+// The IQ2_S grid (1024 entries of eight magnitudes in {8, 25, 43}, lane l in bits 8l..8l+7),
+// expanded at compile time from the compact codes; identical to the reference's table, whose
+// fingerprint the host-side expansion checks.
+struct Iq2sGrid {
+    uint64_t g[1024];
+};
+constexpr Iq2sGrid make_iq2s_grid() {
+    Iq2sGrid t{};
+    constexpr uint16_t codes[1024] = VL_IQ2S_CODES;
+    constexpr uint8_t v[4] = {8, 25, 43, 0};
+    for (unsigned e = 0; e < 1024; ++e) {
+        uint64_t g = 0;
+        for (unsigned l = 0; l < 8; ++l) g |= (uint64_t)v[(codes[e] >> (2 * l)) & 3u] << (8 * l);
+        t.g[e] = g;
+    }
+    return t;
+}
+__device__ const Iq2sGrid kIq2sGrid = make_iq2s_grid();
 
 __device__ __forceinline__ uint32_t ld_u8(const uint8_t* p) { return *gp(p); }
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {  // p 2-byte aligned
@@ -67,6 +87,7 @@ template <uint32_t FMT> struct Fmt;
 template <> struct Fmt<VL_TYPE_Q4_K> { static constexpr uint32_t be = 256, bb = 144; };
 template <> struct Fmt<VL_TYPE_Q5_K> { static constexpr uint32_t be = 256, bb = 176; };
 template <> struct Fmt<VL_TYPE_Q6_K> { static constexpr uint32_t be = 256, bb = 210; };
+template <> struct Fmt<VL_TYPE_IQ2_S> { static constexpr uint32_t be = 256, bb = 82; };
 template <> struct Fmt<VL_TYPE_MXFP4> { static constexpr uint32_t be = 32, bb = 17; };
 template <> struct Fmt<VL_TYPE_BF16> { static constexpr uint32_t be = 1, bb = 2; };
 template <> struct Fmt<VL_TYPE_F32> { static constexpr uint32_t be = 1, bb = 4; };
@@ -112,6 +133,16 @@ __device__ __forceinline__ void load_piece(const uint8_t* row, uint32_t p, uint3
         r.a = ld_u8(blk);
         r.q.x = ld_u8(c) | ld_u8(c + 1) << 8 | ld_u8(c + 2) << 16 | ld_u8(c + 3) << 24;
         r.q.y = ld_u8(c + 4) | ld_u8(c + 5) << 8 | ld_u8(c + 6) << 16 | ld_u8(c + 7) << 24;
+    } else if constexpr (FMT == VL_TYPE_IQ2_S) {
+        // Piece q of a block is sub-block s = q & 3 of group g = q >> 2: its grid index byte,
+        // sign byte, the group's high-index byte and scale byte, and the block's d (82-byte
+        // blocks: d is 2-byte aligned, the rest are single bytes).
+        const uint32_t q = p & 31u, g = q >> 2, sb = q & 3u;
+        const uint8_t* blk = row + 82ull * (p >> 5);
+        r.a = ld_u16(blk);
+        r.b = ld_u8(blk + 2u + 4u * g + sb);
+        r.c = ld_u8(blk + 34u + 4u * g + sb);
+        r.d = ld_u8(blk + 66u + g) | ld_u8(blk + 74u + g) << 8;
     } else if constexpr (FMT == VL_TYPE_Q6_K) {
         // Blocks are 210 bytes: 2-byte aligned loads only. Piece q = 16h + 4k + l0/8.
         const uint32_t q = p & 31u, h = q >> 4, k = (q >> 2) & 3u, l0 = (q & 3u) * 8u;
@@ -139,7 +170,7 @@ __device__ __forceinline__ void load_piece(const uint8_t* row, uint32_t p, uint3
 }
 
 // The eight weights of piece p, exactly as the reference decoders produce them
-// (ggml_quantization.cpp:381-413, :435-589).
+// (ggml_quantization.cpp:285-334, :381-413, :435-589).
 template <uint32_t FMT>
 __device__ __forceinline__ void decode_piece(const RawPiece& r, uint32_t p, float w[8]) {
 #pragma clang fp contract(off)
@@ -161,6 +192,17 @@ __device__ __forceinline__ void decode_piece(const RawPiece& r, uint32_t p, floa
             const uint32_t c = (byte_of(r.q, i) >> shift) & 15u, m = c & 7u;
             const int mag = m < 4u ? (int)m : (int)((m & 1u ? 6u : 4u) << ((m - 4u) >> 1));
             w[i] = (float)(c & 8u ? -mag : mag) * s;
+        }
+    } else if constexpr (FMT == VL_TYPE_IQ2_S) {
+        const uint32_t sb = p & 3u;
+        const uint32_t index = r.b | ((r.d >> (2u * sb)) & 3u) << 8;
+        const uint64_t grid = *gp(&kIq2sGrid.g[index]);
+        const uint32_t nib = sb < 2u ? (r.d >> 8) & 15u : (r.d >> 12) & 15u;
+        const float ls = half_bits_to_float(r.a) * (0.5f + (float)nib) * 0.25f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float mag = (float)((uint32_t)(grid >> (8 * i)) & 0xffu);
+            w[i] = ls * mag * ((r.c >> i) & 1u ? -1.0f : 1.0f);
         }
     } else if constexpr (FMT == VL_TYPE_Q6_K) {
         const uint32_t q = p & 31u, k = (q >> 2) & 3u;
@@ -234,7 +276,8 @@ __device__ __forceinline__ void bytes_float(uint32_t v, float* f) {
 // acc[t] += sum_i w_i x[t][i] over piece p, for the matvec. The block and sub-block factors are
 // taken out of the sum: K-quant pieces are d_j * sum q_i x_i - m_j * sum x_i (Q6_K:
 // d_s * (sum q_i x_i - 32 sum x_i)), MXFP4 pieces s * sum v_i x_i, with the small integer codes
-// converted straight from their bytes; sx[t] = sum_i x[t][i] is shared by the block's rows.
+// converted straight from their bytes (IQ2_S pieces: ls * sum (+/-grid magnitude) x_i);
+// sx[t] = sum_i x[t][i] is shared by the block's rows.
 // Only the rounding of these partial sums differs from forming each weight first.
 template <uint32_t FMT, int NT>
 __device__ __forceinline__ void piece_dot(const RawPiece& r, uint32_t p, const float (&xv)[NT][8],
@@ -246,6 +289,24 @@ __device__ __forceinline__ void piece_dot(const RawPiece& r, uint32_t p, const f
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[t] = fmaf(w[i], xv[t][i], acc[t]);
+    } else if constexpr (FMT == VL_TYPE_IQ2_S) {
+        const uint32_t sb = p & 3u;
+        const uint32_t index = r.b | ((r.d >> (2u * sb)) & 3u) << 8;
+        const uint64_t grid = *gp(&kIq2sGrid.g[index]);
+        const uint32_t nib = sb < 2u ? (r.d >> 8) & 15u : (r.d >> 12) & 15u;
+        const float ls = half_bits_to_float(r.a) * (0.5f + (float)nib) * 0.25f;
+        float v[8];
+        bytes_float((uint32_t)grid, v);
+        bytes_float((uint32_t)(grid >> 32), v + 4);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (r.c >> i) & 1u ? -v[i] : v[i];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) d = fmaf(v[i], xv[t][i], d);
+            acc[t] = fmaf(ls, d, acc[t]);
+        }
     } else if constexpr (FMT == VL_TYPE_MXFP4) {
         const uint32_t e = r.a;
         const float s = bits_float(e < 2u ? 0x00200000u << e : (e - 1u) << 23);
@@ -453,6 +514,7 @@ hipError_t launch_gguf_dequant(const vl_tiled_layout& L, const uint8_t* w, float
         case VL_TYPE_Q4_K: return dequant_fmt<VL_TYPE_Q4_K>(L, w, out, stream);
         case VL_TYPE_Q5_K: return dequant_fmt<VL_TYPE_Q5_K>(L, w, out, stream);
         case VL_TYPE_Q6_K: return dequant_fmt<VL_TYPE_Q6_K>(L, w, out, stream);
+        case VL_TYPE_IQ2_S: return dequant_fmt<VL_TYPE_IQ2_S>(L, w, out, stream);
         case VL_TYPE_MXFP4: return dequant_fmt<VL_TYPE_MXFP4>(L, w, out, stream);
         case VL_TYPE_BF16: return dequant_fmt<VL_TYPE_BF16>(L, w, out, stream);
         case VL_TYPE_F32: return dequant_fmt<VL_TYPE_F32>(L, w, out, stream);
@@ -471,6 +533,7 @@ hipError_t launch_gguf_matvec(const vl_tiled_layout& L, const uint8_t* w, const 
         case VL_TYPE_Q4_K: return matvec_fmt<VL_TYPE_Q4_K>(L, w, x, tokens, y, status, stream);
         case VL_TYPE_Q5_K: return matvec_fmt<VL_TYPE_Q5_K>(L, w, x, tokens, y, status, stream);
         case VL_TYPE_Q6_K: return matvec_fmt<VL_TYPE_Q6_K>(L, w, x, tokens, y, status, stream);
+        case VL_TYPE_IQ2_S: return matvec_fmt<VL_TYPE_IQ2_S>(L, w, x, tokens, y, status, stream);
         case VL_TYPE_MXFP4: return matvec_fmt<VL_TYPE_MXFP4>(L, w, x, tokens, y, status, stream);
         case VL_TYPE_BF16: return matvec_fmt<VL_TYPE_BF16>(L, w, x, tokens, y, status, stream);
         case VL_TYPE_F32: return matvec_fmt<VL_TYPE_F32>(L, w, x, tokens, y, status, stream);

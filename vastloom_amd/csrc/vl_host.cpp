@@ -647,8 +647,8 @@ struct vl_accel {
 namespace {
 
 // Every type with a device layout: the four tiled types and the GGUF-layout ones (Q4_K, Q5_K,
-// Q6_K, MXFP4, BF16, F32), the storage types the reference's accelerator takes
-// (src/cuda/cuda_matvec_accelerator.cpp:46-58).
+// Q6_K, IQ2_S, MXFP4, BF16, F32): the storage types the reference's accelerator takes
+// (src/cuda/cuda_matvec_accelerator.cpp:46-58), and IQ2_S.
 bool has_kernel(uint32_t type) {
     uint32_t elems = 0, bytes = 0;
     return vl_block_shape(type, &elems, &bytes) != 0;

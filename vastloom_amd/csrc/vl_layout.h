@@ -1,6 +1,6 @@
 // Device-resident ("tiled") layout of a quantized expert matrix, shared by host and device code.
 //
-// Q4_K, Q5_K, Q6_K, MXFP4, BF16 and F32 matrices are not rearranged: they stay in their GGUF bytes
+// Q4_K, Q5_K, Q6_K, IQ2_S, MXFP4, BF16 and F32 matrices are not rearranged: they stay in their GGUF bytes
 // (vl_type_tiled); everything below describes the four tiled types.
 //
 // The GGUF block bytes of a matrix are rearranged once, when the matrix becomes resident, into
@@ -45,6 +45,7 @@
 #define VL_TYPE_Q4_K 12u
 #define VL_TYPE_Q5_K 13u
 #define VL_TYPE_Q6_K 14u
+#define VL_TYPE_IQ2_S 22u
 #define VL_TYPE_BF16 30u
 #define VL_TYPE_MXFP4 39u
 
@@ -75,6 +76,7 @@ static inline VL_HD int vl_block_shape(uint32_t type, uint32_t* elements, uint32
         case VL_TYPE_Q4_K: *elements = 256u; *bytes = 144u; return 1;
         case VL_TYPE_Q5_K: *elements = 256u; *bytes = 176u; return 1;
         case VL_TYPE_Q6_K: *elements = 256u; *bytes = 210u; return 1;
+        case VL_TYPE_IQ2_S: *elements = 256u; *bytes = 82u; return 1;
         case VL_TYPE_MXFP4: *elements = 32u; *bytes = 17u; return 1;
         case VL_TYPE_BF16: *elements = 1u; *bytes = 2u; return 1;
         case VL_TYPE_F32: *elements = 1u; *bytes = 4u; return 1;

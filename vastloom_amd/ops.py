@@ -18,7 +18,7 @@ from . import _lib
 from ._lib import VlError, call, lib
 
 F32, Q8_0, IQ2_XXS, IQ3_XXS, IQ1_S = 0, 8, 16, 18, 19
-Q4_K, Q5_K, Q6_K, BF16, MXFP4 = 12, 13, 14, 30, 39
+Q4_K, Q5_K, Q6_K, IQ2_S, BF16, MXFP4 = 12, 13, 14, 22, 30, 39
 QUANT_TYPES = (Q8_0, IQ2_XXS, IQ3_XXS, IQ1_S)
 
 

@@ -11,11 +11,11 @@ role, index])))``, so any one expert or matrix can be regenerated without the ot
   role 3  routing table draws (Zipf workload)
 
 Block scales are binary16, rounded to nearest-even from the float32 draw. Payload bytes are
-uniform: for Q8_0 the int8 quants are uniform on [-127, 127]; for IQ2_XXS, IQ3_XXS and IQ1_S every
-byte is uniform on [0, 255], which always decodes (every grid index, sign field and scale field
-is valid); Q4_K/Q5_K/Q6_K draw their fp16 d (and dmin) scaled down by the 6-bit sub-block
-scales' range, MXFP4 an E8M0 scale in [2^-10, 2^-4], BF16 truncated normal values. Matrices are
-in GGUF block layout, row-major: row r's blocks are contiguous.
+uniform: for Q8_0 the int8 quants are uniform on [-127, 127]; for IQ2_XXS, IQ3_XXS, IQ1_S and
+IQ2_S every byte is uniform on [0, 255], which always decodes (every grid index, sign field and
+scale field is valid); Q4_K/Q5_K/Q6_K draw their fp16 d (and dmin) scaled down by the 6-bit
+sub-block scales' range, MXFP4 an E8M0 scale in [2^-10, 2^-4], BF16 truncated normal values.
+Matrices are in GGUF block layout, row-major: row r's blocks are contiguous.
 
 Workload shapes (the model shapes they mimic are OLMoE-1B-7B experts and DeepSeek-class
 routed experts):
@@ -35,13 +35,15 @@ from dataclasses import dataclass, field
 import numpy as np
 
 F32, Q8_0, IQ2_XXS, IQ3_XXS, IQ1_S = 0, 8, 16, 18, 19
-Q4_K, Q5_K, Q6_K, BF16, MXFP4 = 12, 13, 14, 30, 39
+Q4_K, Q5_K, Q6_K, IQ2_S, BF16, MXFP4 = 12, 13, 14, 22, 30, 39
 
 # (block elements, block bytes) of each GGUF storage type (ggml_quantization.hpp:13-28).
 BLOCK = {F32: (1, 4), Q8_0: (32, 34), IQ2_XXS: (256, 66), IQ3_XXS: (256, 98), IQ1_S: (256, 50),
-         Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), BF16: (1, 2), MXFP4: (32, 17)}
+         Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), IQ2_S: (256, 82), BF16: (1, 2),
+         MXFP4: (32, 17)}
 TYPE_NAMES = {F32: "f32", Q8_0: "q8_0", IQ2_XXS: "iq2_xxs", IQ3_XXS: "iq3_xxs", IQ1_S: "iq1_s",
-              Q4_K: "q4_k", Q5_K: "q5_k", Q6_K: "q6_k", BF16: "bf16", MXFP4: "mxfp4"}
+              Q4_K: "q4_k", Q5_K: "q5_k", Q6_K: "q6_k", IQ2_S: "iq2_s", BF16: "bf16",
+              MXFP4: "mxfp4"}
 
 
 def storage_bytes(qtype: int, rows: int, cols: int) -> int:

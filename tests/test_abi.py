@@ -94,3 +94,23 @@ def test_route_scale_must_be_finite_and_positive():
     cfg.route_scale = 0.0
     rc = lib.vl_moe_workspace(C.byref(cfg), C.byref(n))
     assert rc != 1 or b"configuration" not in lib.vl_last_error()
+
+
+def test_layer_storage_type_combinations():
+    """The layer takes every storage type with a device layout on either side, except a
+    GGUF-layout gate/up with a tiled down (the tiled down stage reads h magnitudes that only the
+    tiled gate/up stage forms): that configuration is refused before any device is touched."""
+    lib = _lib.lib()
+    n = C.c_uint64()
+
+    def refused(gate_type, down_type):
+        cfg = _lib.MoeConfig(1, 1024, 512, 8, 2, gate_type, down_type, 0, _lib.ROUTE_GIVEN, 0, 0, 1,
+                             1.0, 0.0, 0.0)
+        rc = lib.vl_moe_workspace(C.byref(cfg), C.byref(n))
+        return rc == 1 and b"invalid MoE configuration" in lib.vl_last_error()
+
+    q4_k, q6_k, iq2_xxs, iq1_s, iq2_s, mxfp4, i32 = 12, 14, 16, 19, 22, 39, 26
+    assert refused(q4_k, iq2_xxs)
+    assert refused(i32, i32)
+    for gate_type, down_type in ((q4_k, q6_k), (iq2_xxs, mxfp4), (iq2_s, q4_k), (iq1_s, q6_k)):
+        assert not refused(gate_type, down_type)

@@ -12,7 +12,8 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.oracle import IQ1_S, IQ2_XXS, IQ3_XXS, Q8_0, SCORE_SIGMOID, SCORE_SQRT_SOFTPLUS
+from oracle.oracle import (BF16, IQ1_S, IQ2_S, IQ2_XXS, IQ3_XXS, MXFP4, Q4_K, Q5_K, Q6_K, Q8_0,
+                           SCORE_SIGMOID, SCORE_SQRT_SOFTPLUS)
 from tests.moe_cases import TOL, down_row_norms, expert_h, layer_bound, oracle_routes
 from vastloom_amd.workloads import random_matrix, workload
 
@@ -47,7 +48,10 @@ def device_expert(ops, triple, H, F):
 SEMS = {"deepseek": 0, "qwen": 1, "plain": 2}
 
 
-@pytest.mark.parametrize("gt,dt", [(IQ2_XXS, IQ2_XXS), (IQ1_S, IQ3_XXS), (IQ1_S, IQ1_S), (Q8_0, Q8_0)])
+@pytest.mark.parametrize("gt,dt", [(IQ2_XXS, IQ2_XXS), (IQ1_S, IQ3_XXS), (IQ1_S, IQ1_S), (Q8_0, Q8_0),
+                                   # GGUF-layout types, alone and under tiled gate/up matrices
+                                   (Q4_K, Q6_K), (Q5_K, Q4_K), (IQ2_S, IQ2_S), (BF16, MXFP4),
+                                   (IQ2_XXS, MXFP4), (IQ1_S, Q6_K)])
 @pytest.mark.parametrize("sem", ["deepseek", "qwen", "plain"])
 @pytest.mark.parametrize("tokens", [1, 3])
 def test_expert_ffn(ops, lib, oracle, gt, dt, sem, tokens):
@@ -356,3 +360,29 @@ def test_workload_grouped_moe(ops, lib, oracle):
     sample = np.union1d(np.random.default_rng(4).choice(512, 64, replace=False), [0, 1, 255, 256, 511])
     _check_layer(ops, lib, oracle, wl, experts, shared, "deepseek", "table", lib.ROUTE_TABLE,
                  wl.x(), SCORE_SIGMOID, table=wl.zipf_table(), sample=sample)
+
+
+@pytest.mark.parametrize("routing_name,tokens,gt,dt", [
+    ("learned", 1, Q4_K, Q6_K), ("learned", 5, IQ2_XXS, MXFP4), ("table", 20, Q5_K, Q5_K),
+    ("softmax", 3, MXFP4, MXFP4), ("learned", 2, IQ2_S, Q4_K)])
+def test_gguf_layout_layers(ops, lib, oracle, routing_name, tokens, gt, dt):
+    # Layers whose experts (shared expert included) are K-quant, IQ2_S or MXFP4 matrices run on
+    # the grouped plan at every token count; routes and outputs as for the other layers.
+    print(f"[moe gguf] {routing_name} tokens={tokens} {gt}/{dt}", flush=True)
+    rng = np.random.default_rng(700 + tokens + gt + dt)
+    from vastloom_amd.workloads import MoeWorkload
+    sem = "qwen" if routing_name == "softmax" else "deepseek"
+    H, F, E, K = 1024, 512, 16, 4
+    wl = MoeWorkload("gguf", 13, H, F, E, K, tokens, gt, dt, 0.01, sem)
+    experts = [make_expert(rng, gt, dt, H, F) for _ in range(E)]
+    shared = make_expert(rng, gt, dt, H, F)
+    x = rng.standard_normal((tokens, H)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32) if routing_name == "learned" else None
+    table = np.stack([rng.choice(E, K, replace=False) for _ in range(tokens)]) if routing_name == "table" else None
+    routing = {"learned": lib.ROUTE_LEARNED, "table": lib.ROUTE_TABLE,
+               "softmax": lib.ROUTE_SOFTMAX}[routing_name]
+    _check_layer(ops, lib, oracle, wl, experts, shared, sem, routing_name, routing, x, SCORE_SIGMOID,
+                 bias, table, route_scale=1.5 if sem == "deepseek" else 1.0,
+                 routed_limit=0.3 if sem == "deepseek" else 0.0,
+                 shared_limit=0.2 if sem == "deepseek" else 0.0)
+

@@ -23,6 +23,8 @@
 #include "iq_codebooks.h"
 #include "vl_kernels.h"
 #include "vl_layout.h"
+#include "vl_moe.h"
+#include "vl_moe_dev.h"
 #include "vl_stream.h"
 
 namespace vl {
@@ -377,24 +379,28 @@ constexpr int kPiecesInFlight = 2;
 
 constexpr uint32_t kRowsPerBlock = 4;
 
-// kRowsPerBlock rows per 256-thread block; thread i takes pieces i, i + 256, ... of each of the
-// block's rows, so that the activations it loads for a piece serve all of them, and issues the
-// loads of kPiecesInFlight pieces of every row before it decodes the first.
-// NT = token slots (tokens <= NT).
+// Per-block LDS of the row products: each wave's sums, then the block's.
+template <int NT>
+struct RowsLds {
+    float part[4][kRowsPerBlock][NT];
+    float sum[kRowsPerBlock][NT];
+    uint32_t bad[4];
+};
+
+// The products of nrows (<= kRowsPerBlock) rows of W, starting at rp with row stride rb, with the
+// activation rows xs[0 .. ntok-1]; the result lands in lds.sum[row][t] (valid on return for
+// every thread), and whether any activation was non-finite is returned. Thread i takes pieces i,
+// i + 256, ... of each row, so that the activations it loads for a piece serve all the rows, and
+// issues the loads of kPiecesInFlight pieces of every row before it decodes the first. Each wave
+// adds its lanes; the four waves' sums are added in wave order.
 template <uint32_t FMT, int NT>
-__global__ void __launch_bounds__(256) k_gguf_matvec(vl_tiled_layout L, const uint8_t* __restrict__ W,
-                                                     const float* __restrict__ x, uint32_t tokens,
-                                                     float* __restrict__ y, uint32_t* status) {
+__device__ __forceinline__ bool block_rows_dot(const uint8_t* rp, uint64_t rb, uint32_t nrows,
+                                               uint32_t cols, const float* const (&xs)[NT],
+                                               uint32_t ntok, RowsLds<NT>& lds) {
     constexpr uint32_t R = kRowsPerBlock;
-    __shared__ float part[4][R][NT];
-    __shared__ uint32_t bad[4];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t row0 = blockIdx.x * R;  // grid = ceil(rows / R)
-    const uint32_t nrows = L.rows - row0 < R ? L.rows - row0 : R;
-    const uint32_t cols = L.cols, ppr = (cols + 7u) / 8u;
+    const uint32_t ppr = (cols + 7u) / 8u;
     const bool whole = (cols & 7u) == 0u;
-    const uint64_t rb = row_bytes<FMT>(cols);
-    const uint8_t* rp = W + (uint64_t)row0 * rb;
     float acc[R][NT];
 #pragma unroll
     for (uint32_t rr = 0; rr < R; ++rr)
@@ -417,8 +423,8 @@ __global__ void __launch_bounds__(256) k_gguf_matvec(vl_tiled_layout L, const ui
             float xv[NT][8];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const float* xp = x + (uint64_t)t * cols + 8u * p;
-                if (t >= (int)tokens) {
+                const float* xp = xs[t] + 8u * p;
+                if (t >= (int)ntok) {
 #pragma unroll
                     for (int i = 0; i < 8; ++i) xv[t][i] = 0.0f;
                 } else if (whole) {
@@ -445,7 +451,6 @@ __global__ void __launch_bounds__(256) k_gguf_matvec(vl_tiled_layout L, const ui
             }
         }
     }
-    // Each wave adds its lanes, then thread 0 adds the four waves' sums in wave order.
 #pragma unroll
     for (uint32_t rr = 0; rr < R; ++rr)
 #pragma unroll
@@ -457,20 +462,100 @@ __global__ void __launch_bounds__(256) k_gguf_matvec(vl_tiled_layout L, const ui
 #pragma unroll
         for (uint32_t rr = 0; rr < R; ++rr)
 #pragma unroll
-            for (int t = 0; t < NT; ++t) part[wave][rr][t] = acc[rr][t];
-        bad[wave] = wave_bad ? 1u : 0u;
+            for (int t = 0; t < NT; ++t) lds.part[wave][rr][t] = acc[rr][t];
+        lds.bad[wave] = wave_bad ? 1u : 0u;
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t bits = (bad[0] | bad[1] | bad[2] | bad[3]) ? kStatusNonFiniteInput : 0u;
+    if (tid < R * NT) {
+        const uint32_t rr = tid / NT, t = tid % NT;
+        lds.sum[rr][t] = ((lds.part[0][rr][t] + lds.part[1][rr][t]) + lds.part[2][rr][t]) + lds.part[3][rr][t];
+    }
+    const bool any_bad = (lds.bad[0] | lds.bad[1] | lds.bad[2] | lds.bad[3]) != 0u;
+    __syncthreads();
+    return any_bad;
+}
+
+// kRowsPerBlock rows per 256-thread block (block_rows_dot). NT = token slots (tokens <= NT).
+template <uint32_t FMT, int NT>
+__global__ void __launch_bounds__(256) k_gguf_matvec(vl_tiled_layout L, const uint8_t* __restrict__ W,
+                                                     const float* __restrict__ x, uint32_t tokens,
+                                                     float* __restrict__ y, uint32_t* status) {
+    __shared__ RowsLds<NT> lds;
+    const uint32_t row0 = blockIdx.x * kRowsPerBlock;  // grid = ceil(rows / kRowsPerBlock)
+    const uint32_t nrows = L.rows - row0 < kRowsPerBlock ? L.rows - row0 : kRowsPerBlock;
+    const uint64_t rb = row_bytes<FMT>(L.cols);
+    const float* xs[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) xs[t] = x + (uint64_t)t * L.cols;
+    const bool bad_x = block_rows_dot<FMT, NT>(W + (uint64_t)row0 * rb, rb, nrows, L.cols, xs, tokens, lds);
+    if (threadIdx.x == 0) {
+        uint32_t bits = bad_x ? kStatusNonFiniteInput : 0u;
         for (uint32_t rr = 0; rr < nrows; ++rr)
             for (uint32_t t = 0; t < tokens && t < (uint32_t)NT; ++t) {
-                const float v = ((part[0][rr][t] + part[1][rr][t]) + part[2][rr][t]) + part[3][rr][t];
+                const float v = lds.sum[rr][t];
                 y[(uint64_t)t * L.rows + row0 + rr] = v;
                 if (!__builtin_isfinite(v)) bits |= kStatusNonFiniteOutput;
             }
         if (bits) or_bits(status, bits);
     }
+}
+
+// MoE layer stages for GGUF-layout experts, on the grouped layer's plan (the active groups of up
+// to kMoeMaxTokens tokens of one expert, their weight pointers and the combine entries), with
+// the grouped layer's h [group][slot][inter] and per-slot down outputs [group][slot][width] that
+// k_moe_combine adds. Block (bx, a): rows 4 bx .. 4 bx + 3 of group a; groups past the plan's
+// count leave at once.
+template <uint32_t FMT>
+__global__ void __launch_bounds__(256) k_gguf_moe_gateup(const MoeShape s, const MoeInputs in,
+                                                         const MoeWorkspace w) {
+    constexpr int NT = kMoeMaxTokens;
+    __shared__ RowsLds<NT> lg, lu;
+    const uint32_t a = blockIdx.y;
+    if (a >= *gp(&ws_ptr<const MoeHeader>(w, w.off_header)->n_active)) return;  // whole block
+    const ActiveExpert* ae = ws_ptr<const ActiveExpert>(w, w.off_active) + a;
+    const MoeExpert ex = ws_ptr<const MoeExpert>(w, w.off_gweights)[a];
+    const uint32_t F = s.inter, H = s.width, ntok = *gp(&ae->ntok);
+    const uint32_t row0 = blockIdx.x * kRowsPerBlock;
+    const uint32_t nrows = F - row0 < kRowsPerBlock ? F - row0 : kRowsPerBlock;
+    const uint64_t rb = row_bytes<FMT>(H);
+    const float* xs[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) xs[t] = in.x + (uint64_t)(t < (int)ntok ? *gp(&ae->tok[t]) : 0u) * H;
+    block_rows_dot<FMT, NT>(ex.gate + (uint64_t)row0 * rb, rb, nrows, H, xs, ntok, lg);
+    block_rows_dot<FMT, NT>(ex.up + (uint64_t)row0 * rb, rb, nrows, H, xs, ntok, lu);
+    const uint32_t tid = threadIdx.x, rr = tid / NT, t = tid % NT;
+    bool bad = false;
+    if (tid < kRowsPerBlock * NT && rr < nrows && t < ntok) {
+        const float g = lg.sum[rr][t], u = lu.sum[rr][t];
+        const float h = swiglu(s.semantics, g, u, *gp(&ae->limit), *gp(&ae->apply_w) != 0u, *gp(&ae->route_w[t]));
+        bad = !__builtin_isfinite(g) || !__builtin_isfinite(u) || !__builtin_isfinite(h);
+        *gp(ws_ptr<float>(w, w.off_h) + ((uint64_t)a * NT + t) * F + row0 + rr) = h;
+    }
+    if (__any(bad) && (tid & 63u) == 0)
+        or_bits(&ws_ptr<MoeHeader>(w, w.off_header)->status, kStatusNonFiniteOutput);
+}
+
+template <uint32_t FMT>
+__global__ void __launch_bounds__(256) k_gguf_moe_down(const MoeShape s, const MoeInputs in,
+                                                       const MoeWorkspace w) {
+    constexpr int NT = kMoeMaxTokens;
+    __shared__ RowsLds<NT> ld;
+    const uint32_t a = blockIdx.y;
+    if (a >= *gp(&ws_ptr<const MoeHeader>(w, w.off_header)->n_active)) return;  // whole block
+    const ActiveExpert* ae = ws_ptr<const ActiveExpert>(w, w.off_active) + a;
+    const MoeExpert ex = ws_ptr<const MoeExpert>(w, w.off_gweights)[a];
+    const uint32_t F = s.inter, H = s.width, ntok = *gp(&ae->ntok);
+    const uint32_t row0 = blockIdx.x * kRowsPerBlock;
+    const uint32_t nrows = H - row0 < kRowsPerBlock ? H - row0 : kRowsPerBlock;
+    const uint64_t rb = row_bytes<FMT>(F);
+    const float* h = ws_ptr<const float>(w, w.off_h);
+    const float* xs[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) xs[t] = h + ((uint64_t)a * NT + t) * F;
+    block_rows_dot<FMT, NT>(ex.down + (uint64_t)row0 * rb, rb, nrows, F, xs, ntok, ld);
+    const uint32_t tid = threadIdx.x, rr = tid / NT, t = tid % NT;
+    if (tid < kRowsPerBlock * NT && rr < nrows && t < ntok)
+        *gp(ws_ptr<float>(w, w.off_ypart) + ((uint64_t)a * NT + t) * H + row0 + rr) = ld.sum[rr][t];
 }
 
 template <uint32_t FMT>
@@ -499,7 +584,49 @@ hipError_t matvec_fmt(const vl_tiled_layout& L, const uint8_t* w, const float* x
     }
 }
 
+template <uint32_t FMT>
+hipError_t moe_gateup_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w, hipStream_t st) {
+    hipLaunchKernelGGL(k_gguf_moe_gateup<FMT>, dim3((s.inter + kRowsPerBlock - 1u) / kRowsPerBlock, w.max_active),
+                       dim3(256), 0, st, s, in, w);
+    return hipGetLastError();
+}
+
+template <uint32_t FMT>
+hipError_t moe_down_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w, hipStream_t st) {
+    hipLaunchKernelGGL(k_gguf_moe_down<FMT>, dim3((s.width + kRowsPerBlock - 1u) / kRowsPerBlock, w.max_active),
+                       dim3(256), 0, st, s, in, w);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_gguf_moe_gateup(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
+                                  hipStream_t stream) {
+    switch (s.gate_type) {
+        case VL_TYPE_Q4_K: return moe_gateup_fmt<VL_TYPE_Q4_K>(s, in, w, stream);
+        case VL_TYPE_Q5_K: return moe_gateup_fmt<VL_TYPE_Q5_K>(s, in, w, stream);
+        case VL_TYPE_Q6_K: return moe_gateup_fmt<VL_TYPE_Q6_K>(s, in, w, stream);
+        case VL_TYPE_IQ2_S: return moe_gateup_fmt<VL_TYPE_IQ2_S>(s, in, w, stream);
+        case VL_TYPE_MXFP4: return moe_gateup_fmt<VL_TYPE_MXFP4>(s, in, w, stream);
+        case VL_TYPE_BF16: return moe_gateup_fmt<VL_TYPE_BF16>(s, in, w, stream);
+        case VL_TYPE_F32: return moe_gateup_fmt<VL_TYPE_F32>(s, in, w, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gguf_moe_down(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
+                                hipStream_t stream) {
+    switch (s.down_type) {
+        case VL_TYPE_Q4_K: return moe_down_fmt<VL_TYPE_Q4_K>(s, in, w, stream);
+        case VL_TYPE_Q5_K: return moe_down_fmt<VL_TYPE_Q5_K>(s, in, w, stream);
+        case VL_TYPE_Q6_K: return moe_down_fmt<VL_TYPE_Q6_K>(s, in, w, stream);
+        case VL_TYPE_IQ2_S: return moe_down_fmt<VL_TYPE_IQ2_S>(s, in, w, stream);
+        case VL_TYPE_MXFP4: return moe_down_fmt<VL_TYPE_MXFP4>(s, in, w, stream);
+        case VL_TYPE_BF16: return moe_down_fmt<VL_TYPE_BF16>(s, in, w, stream);
+        case VL_TYPE_F32: return moe_down_fmt<VL_TYPE_F32>(s, in, w, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
 
 hipError_t launch_gguf_copy_rows(const vl_tiled_layout& L, const uint8_t* gguf_row0, uint8_t* dst,
                                  uint32_t row0, uint32_t row1, hipStream_t stream) {

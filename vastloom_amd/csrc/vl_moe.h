@@ -110,6 +110,13 @@ hipError_t launch_moe(const MoeShape& s, const MoeInputs& in, const MoeWorkspace
 // callers that must know the selected experts before their weights are on the device.
 hipError_t launch_moe_route(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& ws, hipStream_t stream);
 
+// Gate/up and down stages of a grouped layer whose gate/up or down matrices are of a GGUF-layout
+// type (vl_gguf.hip): they read the plan, the active groups and their weight pointers, and write
+// h and the per-slot down outputs as the tiled grouped stages do.
+hipError_t launch_gguf_moe_gateup(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& ws,
+                                  hipStream_t stream);
+hipError_t launch_gguf_moe_down(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& ws,
+                                hipStream_t stream);
 // Bytes of the per-device workspace that vl_moe_layer_noalloc uses instead of a caller's buffer.
 constexpr uint64_t kStaticWorkspaceBytes = 64ull << 20;
 

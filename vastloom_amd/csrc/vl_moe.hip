@@ -50,7 +50,9 @@ bool moe_shape_ok(const MoeShape& s) {
     if (s.tokens > kMoeMaxTokens &&
         ((uint64_t)s.tokens * s.top_k > kMoeMaxGroupAssign || max_groups(s) > kMoeMaxGroups))
         return false;
-    if (!vl_type_tiled(s.gate_type) || !vl_type_tiled(s.down_type)) return false;
+    // GGUF-layout down matrices take any gate/up type; GGUF-layout gate/up matrices need a
+    // GGUF-layout down (the tiled down stage reads the h magnitudes the tiled gate/up forms).
+    if (!vl_type_tiled(s.gate_type) && vl_type_tiled(s.down_type)) return false;
     if (!vl_block_shape(s.gate_type, &be, &bb) || s.width % be || s.width % 256u) return false;
     if (!vl_block_shape(s.down_type, &be, &bb) || s.inter % be || s.inter % 32u) return false;
     if (s.semantics > kSemPlain || s.routing > kRouteGiven || s.score_fn > kScoreSigmoid) return false;
@@ -84,7 +86,8 @@ static uint32_t router_slices(const MoeShape& s, uint32_t blocks) {
 MoeWorkspace moe_workspace_layout(const MoeShape& s, uint32_t blocks, void* base) {
     MoeWorkspace w{};
     w.base = static_cast<uint8_t*>(base);
-    w.grouped = s.tokens > kMoeMaxTokens ? 1u : 0u;
+    // GGUF-layout matrices run on the grouped layer's plan at every token count.
+    w.grouped = s.tokens > kMoeMaxTokens || !vl_type_tiled(s.gate_type) || !vl_type_tiled(s.down_type) ? 1u : 0u;
     w.wide = w.grouped && wide_shape_ok(s) ? 1u : 0u;
     w.max_active = w.grouped ? (uint32_t)max_groups(s) : max_active(s);
     w.max_items = w.wide ? w.max_active : 0u;
@@ -2009,7 +2012,7 @@ static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, con
         case VL_TYPE_IQ3_XXS: e = launch_gateup_grouped<VL_TYPE_IQ3_XXS>(s, in, w, st); break;
         case VL_TYPE_IQ1_S: e = launch_gateup_grouped<VL_TYPE_IQ1_S>(s, in, w, st); break;
         case VL_TYPE_Q8_0: e = launch_gateup_grouped<VL_TYPE_Q8_0>(s, in, w, st); break;
-        default: return hipErrorInvalidValue;
+        default: e = launch_gguf_moe_gateup(s, in, w, st); break;
     }
     if (e != hipSuccess) return e;
     mark(kStageDown);
@@ -2018,7 +2021,7 @@ static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, con
         case VL_TYPE_IQ3_XXS: e = launch_down_grouped<VL_TYPE_IQ3_XXS>(s, in, w, st); break;
         case VL_TYPE_IQ1_S: e = launch_down_grouped<VL_TYPE_IQ1_S>(s, in, w, st); break;
         case VL_TYPE_Q8_0: e = launch_down_grouped<VL_TYPE_Q8_0>(s, in, w, st); break;
-        default: return hipErrorInvalidValue;
+        default: e = launch_gguf_moe_down(s, in, w, st); break;
     }
     if (e != hipSuccess) return e;
     const uint64_t outs = (uint64_t)s.tokens * s.width;

@@ -47,7 +47,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--workload", default="iq2_moe",
-                   choices=["q8_expert", "q8_moe", "iq2_moe", "mixed_moe", "grouped_moe"])
+                   choices=["q8_expert", "q8_moe", "iq2_moe", "mixed_moe", "grouped_moe",
+                            "kquant_moe"])
     p.add_argument("--layers", type=int, default=None,
                    help="layer instances rotated between steps (defeats caching of weights); "
                         "default 6, or 2 for the grouped workload")
@@ -100,12 +101,23 @@ def wide_path(wl) -> bool:
             and wl.intermediate % 256 == 0)
 
 
+TILED_TYPES = (8, 16, 18, 19)  # Q8_0, IQ2_XXS, IQ3_XXS, IQ1_S
+
+
+def gguf_layout(wl) -> bool:
+    """Whether the layer has GGUF-layout matrices (it then runs on the grouped plan)."""
+    return wl.gate_type not in TILED_TYPES or wl.down_type not in TILED_TYPES
+
+
 def gateup_kernel(wl) -> str:
     """The gate/up kernel a layer of this workload runs (single-token layers of the learned,
     softmax and given routings take the single-token kernels, except IQ3_XXS; 2-8 tokens the
-    token-slot stream kernels; more tokens the grouped path: the fp16 kernels for IQ2_XXS, the
-    int8 ones otherwise)."""
-    if wl.tokens > 8:
+    token-slot stream kernels; more tokens, or GGUF-layout matrices, the grouped path: the fp16
+    kernels for IQ2_XXS, the int8 ones for the other tiled types, k_gguf_moe_gateup for a
+    GGUF-layout gate/up)."""
+    if wl.gate_type not in TILED_TYPES:
+        return "k_gguf_moe_gateup"
+    if wl.tokens > 8 or gguf_layout(wl):
         return "k_wide_gateup" if wide_path(wl) else "k_moe_gateup_grouped"
     if wl.tokens == 1 and wl.routing != "zipf_table" and 18 not in (wl.gate_type, wl.down_type):
         return "k_tok_gateup"
@@ -511,6 +523,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": f"{TYPE(wl.gate_type).lower()}/{TYPE(wl.down_type).lower()} weights, "
                  + ("f16xf16->f32 MFMA (exact fp16 weights, hi/lo fp16 activations)" if wide_path(wl)
+                    else "f32 FMA on the decoded codes, block scales factored out"
+                    if wl.gate_type not in TILED_TYPES
                     else "i8xi8->i32 MFMA, f32 accumulate"),
         "data": f"synthetic (seeded PCG64; uniform random {TYPE(wl.gate_type)}/{TYPE(wl.down_type)} "
                 f"payload bytes, |N(0,1)|*{wl.scale_factor} fp16 scales, N(0,0.02) router, N(0,1) tokens)",

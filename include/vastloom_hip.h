@@ -40,9 +40,10 @@ typedef enum vl_status {
 } vl_status;
 
 /* GGUF storage type ids (include/vastloom/inference/ggml_quantization.hpp:34-45). Q8_0 and the
- * three IQ types are rearranged ("tiled") when they become resident and are the types the MoE
- * layer entry points take; Q4_K, Q5_K, Q6_K, IQ2_S, MXFP4, BF16 and F32 stay in their GGUF bytes
- * and have device dequantize and matvec through the same matrix entry points. */
+ * three IQ types are rearranged ("tiled") when they become resident; Q4_K, Q5_K, Q6_K, IQ2_S,
+ * MXFP4, BF16 and F32 stay in their GGUF bytes. Every one of them has device dequantize and
+ * matvec through the matrix entry points. The MoE layer entry points take any of them for gate/up
+ * and down, except a GGUF-layout gate/up with a tiled down (refused as invalid_argument). */
 #define VL_GGML_F32 0u
 #define VL_GGML_Q8_0 8u
 #define VL_GGML_Q4_K 12u

@@ -393,10 +393,11 @@ struct RowsLds {
 // i + 256, ... of each row, so that the activations it loads for a piece serve all the rows, and
 // issues the loads of kPiecesInFlight pieces of every row before it decodes the first. Each wave
 // adds its lanes; the four waves' sums are added in wave order.
-template <uint32_t FMT, int NT>
+template <uint32_t FMT, int NT, int NTS>
 __device__ __forceinline__ bool block_rows_dot(const uint8_t* rp, uint64_t rb, uint32_t nrows,
-                                               uint32_t cols, const float* const (&xs)[NT],
-                                               uint32_t ntok, RowsLds<NT>& lds) {
+                                               uint32_t cols, const float* const (&xs)[NTS],
+                                               uint32_t ntok, RowsLds<NTS>& lds) {
+    static_assert(NT <= NTS, "token slots beyond the LDS rows");
     constexpr uint32_t R = kRowsPerBlock;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t ppr = (cols + 7u) / 8u;
@@ -487,7 +488,7 @@ __global__ void __launch_bounds__(256) k_gguf_matvec(vl_tiled_layout L, const ui
     const float* xs[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) xs[t] = x + (uint64_t)t * L.cols;
-    const bool bad_x = block_rows_dot<FMT, NT>(W + (uint64_t)row0 * rb, rb, nrows, L.cols, xs, tokens, lds);
+    const bool bad_x = block_rows_dot<FMT, NT, NT>(W + (uint64_t)row0 * rb, rb, nrows, L.cols, xs, tokens, lds);
     if (threadIdx.x == 0) {
         uint32_t bits = bad_x ? kStatusNonFiniteInput : 0u;
         for (uint32_t rr = 0; rr < nrows; ++rr)
@@ -498,6 +499,19 @@ __global__ void __launch_bounds__(256) k_gguf_matvec(vl_tiled_layout L, const ui
             }
         if (bits) or_bits(status, bits);
     }
+}
+
+// block_rows_dot with as many token slots as the group has tokens (1, 2, 4 or 8): a group's
+// token count is uniform over the block.
+template <uint32_t FMT>
+__device__ __forceinline__ void rows_dot_slots(const uint8_t* rp, uint64_t rb, uint32_t nrows, uint32_t cols,
+                                               const float* const (&xs)[kMoeMaxTokens], uint32_t ntok,
+                                               RowsLds<kMoeMaxTokens>& lds) {
+    constexpr int S = kMoeMaxTokens;
+    if (ntok <= 1) block_rows_dot<FMT, 1, S>(rp, rb, nrows, cols, xs, ntok, lds);
+    else if (ntok <= 2) block_rows_dot<FMT, 2, S>(rp, rb, nrows, cols, xs, ntok, lds);
+    else if (ntok <= 4) block_rows_dot<FMT, 4, S>(rp, rb, nrows, cols, xs, ntok, lds);
+    else block_rows_dot<FMT, 8, S>(rp, rb, nrows, cols, xs, ntok, lds);
 }
 
 // MoE layer stages for GGUF-layout experts, on the grouped layer's plan (the active groups of up
@@ -521,8 +535,8 @@ __global__ void __launch_bounds__(256) k_gguf_moe_gateup(const MoeShape s, const
     const float* xs[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) xs[t] = in.x + (uint64_t)(t < (int)ntok ? *gp(&ae->tok[t]) : 0u) * H;
-    block_rows_dot<FMT, NT>(ex.gate + (uint64_t)row0 * rb, rb, nrows, H, xs, ntok, lg);
-    block_rows_dot<FMT, NT>(ex.up + (uint64_t)row0 * rb, rb, nrows, H, xs, ntok, lu);
+    rows_dot_slots<FMT>(ex.gate + (uint64_t)row0 * rb, rb, nrows, H, xs, ntok, lg);
+    rows_dot_slots<FMT>(ex.up + (uint64_t)row0 * rb, rb, nrows, H, xs, ntok, lu);
     const uint32_t tid = threadIdx.x, rr = tid / NT, t = tid % NT;
     bool bad = false;
     if (tid < kRowsPerBlock * NT && rr < nrows && t < ntok) {
@@ -552,7 +566,7 @@ __global__ void __launch_bounds__(256) k_gguf_moe_down(const MoeShape s, const M
     const float* xs[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) xs[t] = h + ((uint64_t)a * NT + t) * F;
-    block_rows_dot<FMT, NT>(ex.down + (uint64_t)row0 * rb, rb, nrows, F, xs, ntok, ld);
+    rows_dot_slots<FMT>(ex.down + (uint64_t)row0 * rb, rb, nrows, F, xs, ntok, ld);
     const uint32_t tid = threadIdx.x, rr = tid / NT, t = tid % NT;
     if (tid < kRowsPerBlock * NT && rr < nrows && t < ntok)
         *gp(ws_ptr<float>(w, w.off_ypart) + ((uint64_t)a * NT + t) * H + row0 + rr) = ld.sum[rr][t];

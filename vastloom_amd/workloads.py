@@ -26,6 +26,7 @@ routed experts):
                  router, top-8, one token                                                    seed 2
   mixed_moe      as iq2_moe with IQ1_S gate/up and IQ3_XXS down, five tokens                 seed 3
   grouped_moe    as iq2_moe, 512 tokens, table routing drawn from Zipf(1.1) over experts     seed 4
+  kquant_moe     as iq2_moe with Q4_K gate/up and Q6_K down (GGUF-layout types), one token   seed 5
 """
 
 from __future__ import annotations
@@ -205,10 +206,13 @@ def workload(name: str) -> MoeWorkload:
     if name == "mixed_moe":
         return MoeWorkload(name, 3, 7168, 2048, 256, 8, 5, IQ1_S, IQ3_XXS, 0.01, "deepseek",
                            score_fn=1, has_shared=True)
+    if name == "kquant_moe":
+        return MoeWorkload(name, 5, 7168, 2048, 256, 8, 1, Q4_K, Q6_K, 0.01, "deepseek",
+                           score_fn=1, has_shared=True)
     if name == "grouped_moe":
         return MoeWorkload(name, 4, 7168, 2048, 256, 8, 512, IQ2_XXS, IQ2_XXS, 0.01,
                            "deepseek", score_fn=1, has_shared=True, routing="zipf_table")
     raise KeyError(name)
 
 
-WORKLOADS = ("q8_expert", "q8_moe", "iq2_moe", "mixed_moe", "grouped_moe")
+WORKLOADS = ("q8_expert", "q8_moe", "iq2_moe", "mixed_moe", "grouped_moe", "kquant_moe")

@@ -71,10 +71,21 @@ __device__ __forceinline__ uint32_t byte_of(uint2 v, int i) {
 }
 __device__ __forceinline__ float bits_float(uint32_t b) { return __uint_as_float(b); }
 
-// Byte i (0..11) of a Q4_K/Q5_K scale field held as three little-endian words.
-__device__ __forceinline__ uint32_t scale_byte(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t i) {
-    const uint32_t w = i < 4u ? s0 : i < 8u ? s1 : s2;
-    return (w >> (8u * (i & 3u))) & 0xffu;
+// The 6-bit scale and minimum of sub-block j of a Q4_K/Q5_K superblock from its 12 scale bytes
+// held as three little-endian words b (bytes 0-3), c (4-7), d (8-11): for j < 4 the low six bits
+// of byte j (scale) and byte j + 4 (minimum); for j >= 4 the nibbles of byte j + 4 with the top
+// two bits of bytes j - 4 (scale) and j (minimum) above them (ggml_quantization.cpp:435-455).
+__device__ __forceinline__ void k_scale_min(uint32_t b, uint32_t c, uint32_t d, uint32_t j,
+                                            uint32_t& sc, uint32_t& mn) {
+    const uint32_t sh = 8u * (j & 3u);
+    const uint32_t lb = b >> sh, lc = c >> sh, ld = d >> sh;
+    if (j < 4u) {
+        sc = lb & 63u;
+        mn = lc & 63u;
+    } else {
+        sc = (ld & 15u) | ((lb >> 2) & 0x30u);
+        mn = ((ld >> 4) & 15u) | ((lc >> 2) & 0x30u);
+    }
 }
 
 // The raw bytes one piece needs, loaded before any of them is used.
@@ -222,14 +233,7 @@ __device__ __forceinline__ void decode_piece(const RawPiece& r, uint32_t p, floa
         const float d = half_bits_to_float(r.a), dmin = half_bits_to_float(r.a >> 16);
         // Sub-block j's 6-bit scale and minimum from the 12 packed bytes (words b, c, d).
         uint32_t sc, mn;
-        if (j < 4u) {
-            sc = scale_byte(r.b, r.c, r.d, j) & 63u;
-            mn = scale_byte(r.b, r.c, r.d, j + 4u) & 63u;
-        } else {
-            const uint32_t x = scale_byte(r.b, r.c, r.d, j + 4u);
-            sc = (x & 15u) | (scale_byte(r.b, r.c, r.d, j - 4u) >> 6) << 4;
-            mn = (x >> 4) | (scale_byte(r.b, r.c, r.d, j) >> 6) << 4;
-        }
+        k_scale_min(r.b, r.c, r.d, j, sc, mn);
         const float dj = d * (float)sc, mj = dmin * (float)mn;
         const uint32_t shift = 4u * (j & 1u);
 #pragma unroll
@@ -342,14 +346,7 @@ __device__ __forceinline__ void piece_dot(const RawPiece& r, uint32_t p, const f
             const uint32_t j = (p & 31u) >> 2;
             const float d = half_bits_to_float(r.a), dmin = half_bits_to_float(r.a >> 16);
             uint32_t sc, mn;
-            if (j < 4u) {
-                sc = scale_byte(r.b, r.c, r.d, j) & 63u;
-                mn = scale_byte(r.b, r.c, r.d, j + 4u) & 63u;
-            } else {
-                const uint32_t x = scale_byte(r.b, r.c, r.d, j + 4u);
-                sc = (x & 15u) | (scale_byte(r.b, r.c, r.d, j - 4u) >> 6) << 4;
-                mn = (x >> 4) | (scale_byte(r.b, r.c, r.d, j) >> 6) << 4;
-            }
+            k_scale_min(r.b, r.c, r.d, j, sc, mn);
             const uint32_t sh = 4u * (j & 1u);
             uint32_t lo = (r.q.x >> sh) & 0x0f0f0f0fu, hi = (r.q.y >> sh) & 0x0f0f0f0fu;
             if constexpr (FMT == VL_TYPE_Q5_K) {
@@ -393,7 +390,7 @@ struct RowsLds {
 // i + 256, ... of each row, so that the activations it loads for a piece serve all the rows, and
 // issues the loads of kPiecesInFlight pieces of every row before it decodes the first. Each wave
 // adds its lanes; the four waves' sums are added in wave order.
-template <uint32_t FMT, int NT, int NTS>
+template <uint32_t FMT, int NT, int NTS, bool CHECK_X = true>
 __device__ __forceinline__ bool block_rows_dot(const uint8_t* rp, uint64_t rb, uint32_t nrows,
                                                uint32_t cols, const float* const (&xs)[NTS],
                                                uint32_t ntok, RowsLds<NTS>& lds) {
@@ -437,8 +434,10 @@ __device__ __forceinline__ bool block_rows_dot(const uint8_t* rp, uint64_t rb, u
 #pragma unroll
                     for (int i = 0; i < 8; ++i) xv[t][i] = 8u * p + i < cols ? xp[i] : 0.0f;
                 }
+                if constexpr (CHECK_X) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) bad_x |= !__builtin_isfinite(xv[t][i]);
+                    for (int i = 0; i < 8; ++i) bad_x |= !__builtin_isfinite(xv[t][i]);
+                }
             }
             float sx[NT];
 #pragma unroll
@@ -502,16 +501,17 @@ __global__ void __launch_bounds__(256) k_gguf_matvec(vl_tiled_layout L, const ui
 }
 
 // block_rows_dot with as many token slots as the group has tokens (1, 2, 4 or 8): a group's
-// token count is uniform over the block.
+// token count is uniform over the block. The layer's plan has already checked the activations
+// (a non-finite one refuses the layer), and h is checked where it is formed.
 template <uint32_t FMT>
 __device__ __forceinline__ void rows_dot_slots(const uint8_t* rp, uint64_t rb, uint32_t nrows, uint32_t cols,
                                                const float* const (&xs)[kMoeMaxTokens], uint32_t ntok,
                                                RowsLds<kMoeMaxTokens>& lds) {
     constexpr int S = kMoeMaxTokens;
-    if (ntok <= 1) block_rows_dot<FMT, 1, S>(rp, rb, nrows, cols, xs, ntok, lds);
-    else if (ntok <= 2) block_rows_dot<FMT, 2, S>(rp, rb, nrows, cols, xs, ntok, lds);
-    else if (ntok <= 4) block_rows_dot<FMT, 4, S>(rp, rb, nrows, cols, xs, ntok, lds);
-    else block_rows_dot<FMT, 8, S>(rp, rb, nrows, cols, xs, ntok, lds);
+    if (ntok <= 1) block_rows_dot<FMT, 1, S, false>(rp, rb, nrows, cols, xs, ntok, lds);
+    else if (ntok <= 2) block_rows_dot<FMT, 2, S, false>(rp, rb, nrows, cols, xs, ntok, lds);
+    else if (ntok <= 4) block_rows_dot<FMT, 4, S, false>(rp, rb, nrows, cols, xs, ntok, lds);
+    else block_rows_dot<FMT, 8, S, false>(rp, rb, nrows, cols, xs, ntok, lds);
 }
 
 // MoE layer stages for GGUF-layout experts, on the grouped layer's plan (the active groups of up

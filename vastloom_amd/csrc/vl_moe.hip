@@ -322,7 +322,17 @@ __global__ void __launch_bounds__(256) k_moe_logits_finish(const MoeShape s, con
     if (i >= n) return;
     const double* part = ws_ptr<const double>(w, w.off_lgpart);
     double sum = part[i];
-    for (uint32_t z = 1; z < w.lg_slices; ++z) sum += part[(uint64_t)z * n + i];
+    // Slices in order; the loads of 32 slices go out before the first of them is added.
+    constexpr uint32_t kBatch = 32;
+    uint32_t z = 1;
+    for (; z + kBatch <= w.lg_slices; z += kBatch) {
+        double v[kBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) v[k] = part[(uint64_t)(z + k) * n + i];
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) sum += v[k];
+    }
+    for (; z < w.lg_slices; ++z) sum += part[(uint64_t)z * n + i];
     router_logit_store(s, in, w, (uint32_t)(i % s.experts), (uint32_t)(i / s.experts), sum);
 }
 

@@ -105,12 +105,13 @@ template <> struct Fmt<VL_TYPE_MXFP4> { static constexpr uint32_t be = 32, bb = 
 template <> struct Fmt<VL_TYPE_BF16> { static constexpr uint32_t be = 1, bb = 2; };
 template <> struct Fmt<VL_TYPE_F32> { static constexpr uint32_t be = 1, bb = 4; };
 
-// Loads piece p of a row (row = the row's first byte). A BF16 or F32 piece past the row's last
-// column reads nothing for the missing columns.
+// Loads piece p of a row (row = the row's first byte). Offsets within the row are 32-bit (the
+// launchers refuse rows of 4 GiB or more). A BF16 or F32 piece past the row's last column reads
+// nothing for the missing columns.
 template <uint32_t FMT>
 __device__ __forceinline__ void load_piece(const uint8_t* row, uint32_t p, uint32_t cols, RawPiece& r) {
     if constexpr (FMT == VL_TYPE_F32) {
-        const uint8_t* e = row + 32ull * p;
+        const uint8_t* e = row + 32u * p;
         if ((cols & 7u) == 0u) {  // row bytes % 32 == 0: two 16-byte loads
             const u32x4 v0 = ld_u128(e), v1 = ld_u128(e + 16);
             r.a = v0.x; r.b = v0.y; r.c = v0.z; r.d = v0.w;
@@ -126,7 +127,7 @@ __device__ __forceinline__ void load_piece(const uint8_t* row, uint32_t p, uint3
             r.h = make_uint2(w[6], w[7]);
         }
     } else if constexpr (FMT == VL_TYPE_BF16) {
-        const uint8_t* e = row + 16ull * p;
+        const uint8_t* e = row + 16u * p;
         if ((cols & 7u) == 0u) {  // rows of whole pieces: one 16-byte load (row bytes % 16 == 0)
             const u32x4 v = ld_u128(e);
             r.a = v.x; r.b = v.y; r.c = v.z; r.d = v.w;
@@ -141,7 +142,7 @@ __device__ __forceinline__ void load_piece(const uint8_t* row, uint32_t p, uint3
         // Piece q of a block: low nibbles (q < 2) or high nibbles (q >= 2) of code bytes
         // 1 + 8 (q & 1) .. +7. Blocks are 17 bytes, so every byte is loaded on its own.
         const uint32_t q = p & 3u;
-        const uint8_t* blk = row + 17ull * (p >> 2);
+        const uint8_t* blk = row + 17u * (p >> 2);
         const uint8_t* c = blk + 1u + 8u * (q & 1u);
         r.a = ld_u8(blk);
         r.q.x = ld_u8(c) | ld_u8(c + 1) << 8 | ld_u8(c + 2) << 16 | ld_u8(c + 3) << 24;
@@ -151,7 +152,7 @@ __device__ __forceinline__ void load_piece(const uint8_t* row, uint32_t p, uint3
         // sign byte, the group's high-index byte and scale byte, and the block's d (82-byte
         // blocks: d is 2-byte aligned, the rest are single bytes).
         const uint32_t q = p & 31u, g = q >> 2, sb = q & 3u;
-        const uint8_t* blk = row + 82ull * (p >> 5);
+        const uint8_t* blk = row + 82u * (p >> 5);
         r.a = ld_u16(blk);
         r.b = ld_u8(blk + 2u + 4u * g + sb);
         r.c = ld_u8(blk + 34u + 4u * g + sb);
@@ -159,9 +160,10 @@ __device__ __forceinline__ void load_piece(const uint8_t* row, uint32_t p, uint3
     } else if constexpr (FMT == VL_TYPE_Q6_K) {
         // Blocks are 210 bytes: 2-byte aligned loads only. Piece q = 16h + 4k + l0/8.
         const uint32_t q = p & 31u, h = q >> 4, k = (q >> 2) & 3u, l0 = (q & 3u) * 8u;
-        const uint8_t* blk = row + 210ull * (p >> 5);
-        const uint8_t* lo = blk + 64u * h + 32u * (k & 1u) + l0;
-        const uint8_t* hi = blk + 128u + 32u * h + l0;
+        const uint32_t b0 = 210u * (p >> 5);
+        const uint8_t* blk = row + b0;
+        const uint8_t* lo = row + (b0 + 64u * h + 32u * (k & 1u) + l0);
+        const uint8_t* hi = row + (b0 + 128u + 32u * h + l0);
         r.q.x = ld_u16(lo) | ld_u16(lo + 2) << 16;
         r.q.y = ld_u16(lo + 4) | ld_u16(lo + 6) << 16;
         r.h.x = ld_u16(hi) | ld_u16(hi + 2) << 16;
@@ -170,14 +172,14 @@ __device__ __forceinline__ void load_piece(const uint8_t* row, uint32_t p, uint3
         r.b = ld_u8(blk + 192u + 8u * h + (l0 >> 4) + 2u * k);
     } else {  // Q4_K, Q5_K: 144- and 176-byte blocks keep 16-byte alignment
         const uint32_t q = p & 31u, j = q >> 2, l0 = (q & 3u) * 8u;
-        const uint8_t* blk = row + (uint64_t)Fmt<FMT>::bb * (p >> 5);
-        const u32x4 head = ld_u128(blk);  // d, dmin and the 12 scale bytes
+        const uint32_t b0 = Fmt<FMT>::bb * (p >> 5);
+        const u32x4 head = ld_u128(row + b0);  // d, dmin and the 12 scale bytes
         r.a = head.x; r.b = head.y; r.c = head.z; r.d = head.w;
         if constexpr (FMT == VL_TYPE_Q5_K) {
-            r.h = ld_u64(blk + 16u + l0);
-            r.q = ld_u64(blk + 48u + 32u * (j >> 1) + l0);
+            r.h = ld_u64(row + (b0 + 16u + l0));
+            r.q = ld_u64(row + (b0 + 48u + 32u * (j >> 1) + l0));
         } else {
-            r.q = ld_u64(blk + 16u + 32u * (j >> 1) + l0);
+            r.q = ld_u64(row + (b0 + 16u + 32u * (j >> 1) + l0));
         }
     }
 }
@@ -273,6 +275,9 @@ __global__ void __launch_bounds__(256) k_gguf_dequant(vl_tiled_layout L, const u
 
 // Four unsigned bytes of a word as floats (v_cvt_f32_ubyte0..3).
 __device__ __forceinline__ void bytes_float(uint32_t v, float* f) {
+    // Opaque to the compiler, so that the masks and shifts that formed v are not folded into a
+    // bit-field extract per byte: each byte then converts with one v_cvt_f32_ubyteN.
+    asm("" : "+v"(v));
     f[0] = (float)(v & 0xffu);
     f[1] = (float)((v >> 8) & 0xffu);
     f[2] = (float)((v >> 16) & 0xffu);
@@ -572,8 +577,15 @@ __global__ void __launch_bounds__(256) k_gguf_moe_down(const MoeShape s, const M
         *gp(ws_ptr<float>(w, w.off_ypart) + ((uint64_t)a * NT + t) * H + row0 + rr) = ld.sum[rr][t];
 }
 
+// Whether rows of `cols` columns of this type fit the kernels' 32-bit offsets.
+template <uint32_t FMT>
+bool rows_fit(uint32_t cols) {
+    return (uint64_t)(cols / Fmt<FMT>::be) * Fmt<FMT>::bb + 64u <= 0xffffffffull;
+}
+
 template <uint32_t FMT>
 hipError_t dequant_fmt(const vl_tiled_layout& L, const uint8_t* w, float* out, hipStream_t st) {
+    if (!rows_fit<FMT>(L.cols)) return hipErrorInvalidValue;
     const uint64_t n = (uint64_t)L.rows * ((L.cols + 7u) / 8u);
     hipLaunchKernelGGL(k_gguf_dequant<FMT>, dim3((uint32_t)((n + 255u) / 256u)), dim3(256), 0, st, L, w, out);
     return hipGetLastError();
@@ -590,6 +602,7 @@ hipError_t matvec_nt(const vl_tiled_layout& L, const uint8_t* w, const float* x,
 template <uint32_t FMT>
 hipError_t matvec_fmt(const vl_tiled_layout& L, const uint8_t* w, const float* x, uint32_t tokens,
                       float* y, uint32_t* status, hipStream_t st) {
+    if (!rows_fit<FMT>(L.cols)) return hipErrorInvalidValue;
     switch (limb_slots(tokens)) {
         case 1: return matvec_nt<FMT, 1>(L, w, x, tokens, y, status, st);
         case 2: return matvec_nt<FMT, 2>(L, w, x, tokens, y, status, st);
@@ -600,6 +613,7 @@ hipError_t matvec_fmt(const vl_tiled_layout& L, const uint8_t* w, const float* x
 
 template <uint32_t FMT>
 hipError_t moe_gateup_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w, hipStream_t st) {
+    if (!rows_fit<FMT>(s.width)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_gguf_moe_gateup<FMT>, dim3((s.inter + kRowsPerBlock - 1u) / kRowsPerBlock, w.max_active),
                        dim3(256), 0, st, s, in, w);
     return hipGetLastError();
@@ -607,6 +621,7 @@ hipError_t moe_gateup_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorks
 
 template <uint32_t FMT>
 hipError_t moe_down_fmt(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w, hipStream_t st) {
+    if (!rows_fit<FMT>(s.inter)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_gguf_moe_down<FMT>, dim3((s.width + kRowsPerBlock - 1u) / kRowsPerBlock, w.max_active),
                        dim3(256), 0, st, s, in, w);
     return hipGetLastError();

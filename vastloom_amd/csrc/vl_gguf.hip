@@ -7,7 +7,8 @@
 // These matrices are read as they are stored, row-major with each row's blocks contiguous, so
 // making one resident is a device copy. A "piece" is eight consecutive weights of a row; a block
 // holds a whole number of pieces (32 for the 256-weight K-quants, 4 for MXFP4), so a piece never
-// crosses a block. A 256-thread block takes four rows: thread i decodes the pieces i, i + 256,
+// crosses a block (the row products take 16-weight pieces of the K-quants when they carry one or
+// two token slots). A 256-thread block takes four rows: thread i decodes the pieces i, i + 256,
 // ... of each, two pieces per row at a time with all their loads issued before the first is
 // decoded, and accumulates w * x in float per row and token (the activations of a piece are
 // loaded once for the four rows; block and sub-block factors multiply the piece's sum of
@@ -381,6 +382,103 @@ constexpr int kPiecesInFlight = 2;
 
 constexpr uint32_t kRowsPerBlock = 4;
 
+// Weights per piece in the row products: 16 for the K-quants with at most two token slots, so
+// that one header load and one scale unpacking serve 16 weights of a sub-block; 8 otherwise.
+template <uint32_t FMT, int NT>
+constexpr int piece_width() {
+    return (FMT == VL_TYPE_Q4_K || FMT == VL_TYPE_Q5_K || FMT == VL_TYPE_Q6_K) && NT <= 2 ? 16 : 8;
+}
+
+// The raw bytes of a 16-weight K-quant piece. Q4_K/Q5_K: the block header and the 16 quant (and
+// high-bit) bytes of half a sub-block, all 16-byte aligned (144- and 176-byte blocks). Q6_K: the
+// 16 low-nibble and 16 high-bit bytes of the piece, its scale byte and d (210-byte blocks: 2-byte
+// loads).
+struct RawWide {
+    uint32_t a, b, c, d;
+    u32x4 q, h;
+};
+
+template <uint32_t FMT>
+__device__ __forceinline__ void load_wide(const uint8_t* row, uint32_t p, RawWide& r) {
+    if constexpr (FMT == VL_TYPE_Q6_K) {
+        // Piece q = 8h + 2k + l0/16 holds weights 128h + 32k + l0 .. +15 of its block.
+        const uint32_t q = p & 15u, h = q >> 3, k = (q >> 1) & 3u, l0 = (q & 1u) * 16u;
+        const uint32_t b0 = 210u * (p >> 4);
+        const uint8_t* lo = row + (b0 + 64u * h + 32u * (k & 1u) + l0);
+        const uint8_t* hi = row + (b0 + 128u + 32u * h + l0);
+        uint32_t lw[4], hw[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            lw[w] = ld_u16(lo + 4 * w) | ld_u16(lo + 4 * w + 2) << 16;
+            hw[w] = ld_u16(hi + 4 * w) | ld_u16(hi + 4 * w + 2) << 16;
+        }
+        r.q = u32x4{lw[0], lw[1], lw[2], lw[3]};
+        r.h = u32x4{hw[0], hw[1], hw[2], hw[3]};
+        r.a = ld_u16(row + (b0 + 208u));
+        r.b = ld_u8(row + (b0 + 192u + 8u * h + (l0 >> 4) + 2u * k));
+        return;
+    }
+    const uint32_t q = p & 15u, j = q >> 1, l0 = (q & 1u) * 16u;
+    const uint32_t b0 = Fmt<FMT>::bb * (p >> 4);
+    const u32x4 head = ld_u128(row + b0);
+    r.a = head.x; r.b = head.y; r.c = head.z; r.d = head.w;
+    if constexpr (FMT == VL_TYPE_Q5_K) {
+        r.h = ld_u128(row + (b0 + 16u + l0));
+        r.q = ld_u128(row + (b0 + 48u + 32u * (j >> 1) + l0));
+    } else {
+        r.q = ld_u128(row + (b0 + 16u + 32u * (j >> 1) + l0));
+    }
+}
+
+// acc[t] += d_j * sum q_i x[t][i] - m_j * sum x[t][i] over the 16 weights of piece p.
+template <uint32_t FMT, int NT>
+__device__ __forceinline__ void wide_dot(const RawWide& r, uint32_t p, const float (&xv)[NT][16],
+                                         const float (&sx)[NT], float (&acc)[NT]) {
+    if constexpr (FMT == VL_TYPE_Q6_K) {
+        // acc[t] += (d * scale) * (sum q_i x[t][i] - 32 sum x[t][i]), q_i the 6-bit codes.
+        const uint32_t k = ((p & 15u) >> 1) & 3u, sh = k < 2u ? 0u : 4u;
+        const uint32_t lw[4] = {r.q.x, r.q.y, r.q.z, r.q.w}, hw[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+        float q[16];
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            bytes_float(((lw[w] >> sh) & 0x0f0f0f0fu) | ((hw[w] >> (2u * k)) & 0x03030303u) << 4, q + 4 * w);
+        const float scale = half_bits_to_float(r.a) * (float)(int)(int8_t)(uint8_t)r.b;
+        const float offset = 32.0f * scale;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s = fmaf(q[i], xv[t][i], s);
+            acc[t] = fmaf(scale, s, fmaf(-offset, sx[t], acc[t]));
+        }
+        return;
+    }
+    const uint32_t j = (p & 15u) >> 1;
+    const float d = half_bits_to_float(r.a), dmin = half_bits_to_float(r.a >> 16);
+    uint32_t sc, mn;
+    k_scale_min(r.b, r.c, r.d, j, sc, mn);
+    const uint32_t sh = 4u * (j & 1u);
+    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    float q[16];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t v = (qw[w] >> sh) & 0x0f0f0f0fu;
+        if constexpr (FMT == VL_TYPE_Q5_K) {
+            const uint32_t hw = w == 0 ? r.h.x : w == 1 ? r.h.y : w == 2 ? r.h.z : r.h.w;
+            v |= ((hw >> j) & 0x01010101u) << 4;
+        }
+        bytes_float(v, q + 4 * w);
+    }
+    const float scale = d * (float)sc, offset = dmin * (float)mn;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s = fmaf(q[i], xv[t][i], s);
+        acc[t] = fmaf(scale, s, fmaf(-offset, sx[t], acc[t]));
+    }
+}
+
 // Per-block LDS of the row products: each wave's sums, then the block's.
 template <int NT>
 struct RowsLds {
@@ -410,6 +508,49 @@ __device__ __forceinline__ bool block_rows_dot(const uint8_t* rp, uint64_t rb, u
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[rr][t] = 0.0f;
     bool bad_x = false;
+    if constexpr (piece_width<FMT, NT>() == 16) {
+        const uint32_t ppw = cols / 16u;  // K-quant rows are whole 256-weight blocks
+        for (uint32_t base = tid; base < ppw; base += 256u * kPiecesInFlight) {
+            RawWide r[kPiecesInFlight][R];
+#pragma unroll
+            for (int u = 0; u < kPiecesInFlight; ++u) {
+                const uint32_t p = base + 256u * u;
+#pragma unroll
+                for (uint32_t rr = 0; rr < R; ++rr)
+                    if (p < ppw && rr < nrows) load_wide<FMT>(rp + rr * rb, p, r[u][rr]);
+            }
+#pragma unroll
+            for (int u = 0; u < kPiecesInFlight; ++u) {
+                const uint32_t p = base + 256u * u;
+                if (p >= ppw) break;
+                float xv[NT][16];
+                float sx[NT];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const float* xp = xs[t] + 16u * p;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const f32x4 v = t < (int)ntok ? *gp(reinterpret_cast<const f32x4*>(xp + 4 * k))
+                                                      : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                        xv[t][4 * k] = v.x; xv[t][4 * k + 1] = v.y; xv[t][4 * k + 2] = v.z; xv[t][4 * k + 3] = v.w;
+                    }
+                    if constexpr (CHECK_X) {
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) bad_x |= !__builtin_isfinite(xv[t][i]);
+                    }
+                    float h[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) h[i] = xv[t][2 * i] + xv[t][2 * i + 1];
+                    sx[t] = ((h[0] + h[1]) + (h[2] + h[3])) + ((h[4] + h[5]) + (h[6] + h[7]));
+                }
+#pragma unroll
+                for (uint32_t rr = 0; rr < R; ++rr) {
+                    if (rr >= nrows) break;
+                    wide_dot<FMT, NT>(r[u][rr], p, xv, sx, acc[rr]);
+                }
+            }
+        }
+    } else
     for (uint32_t base = tid; base < ppr; base += 256u * kPiecesInFlight) {
         RawPiece r[kPiecesInFlight][R];
 #pragma unroll

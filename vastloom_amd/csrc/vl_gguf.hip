@@ -320,21 +320,27 @@ __device__ __forceinline__ void piece_dot(const RawPiece& r, uint32_t p, const f
             acc[t] = fmaf(ls, d, acc[t]);
         }
     } else if constexpr (FMT == VL_TYPE_MXFP4) {
+        // Four codes per word, one per byte: v_perm_b32 picks each code's magnitude (0, 1, 2, 3,
+        // 4, 6, 8, 12 for codes & 7) out of an eight-byte table, and the code's sign bit flips
+        // the sign of the matching activation.
         const uint32_t e = r.a;
         const float s = bits_float(e < 2u ? 0x00200000u << e : (e - 1u) << 23);
         const uint32_t shift = 4u * ((p & 3u) >> 1);
+        const uint32_t c0 = (r.q.x >> shift) & 0x0f0f0f0fu, c1 = (r.q.y >> shift) & 0x0f0f0f0fu;
         float v[8];
+        bytes_float(__builtin_amdgcn_perm(0x0c080604u, 0x03020100u, c0 & 0x07070707u), v);
+        bytes_float(__builtin_amdgcn_perm(0x0c080604u, 0x03020100u, c1 & 0x07070707u), v + 4);
+        uint32_t neg[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t c = (byte_of(r.q, i) >> shift) & 15u, m = c & 7u;
-            const int mag = m < 4u ? (int)m : (int)((m & 1u ? 6u : 4u) << ((m - 4u) >> 1));
-            v[i] = (float)(c & 8u ? -mag : mag);
+        for (int i = 0; i < 4; ++i) {
+            neg[i] = (c0 << (28 - 8 * i)) & 0x80000000u;      // bit 3 of byte i -> bit 31
+            neg[i + 4] = (c1 << (28 - 8 * i)) & 0x80000000u;
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             float d = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) d = fmaf(v[i], xv[t][i], d);
+            for (int i = 0; i < 8; ++i) d = fmaf(v[i], __uint_as_float(__float_as_uint(xv[t][i]) ^ neg[i]), d);
             acc[t] = fmaf(s, d, acc[t]);
         }
     } else {
@@ -431,8 +437,8 @@ __device__ __forceinline__ void load_wide(const uint8_t* row, uint32_t p, RawWid
 }
 
 // acc[t] += d_j * sum q_i x[t][i] - m_j * sum x[t][i] over the 16 weights of piece p.
-template <uint32_t FMT, int NT>
-__device__ __forceinline__ void wide_dot(const RawWide& r, uint32_t p, const float (&xv)[NT][16],
+template <uint32_t FMT, int NT, int PW>
+__device__ __forceinline__ void wide_dot(const RawWide& r, uint32_t p, const float (&xv)[NT][PW],
                                          const float (&sx)[NT], float (&acc)[NT]) {
     if constexpr (FMT == VL_TYPE_Q6_K) {
         // acc[t] += (d * scale) * (sum q_i x[t][i] - 32 sum x[t][i]), q_i the 6-bit codes.
@@ -508,10 +514,11 @@ __device__ __forceinline__ bool block_rows_dot(const uint8_t* rp, uint64_t rb, u
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[rr][t] = 0.0f;
     bool bad_x = false;
-    if constexpr (piece_width<FMT, NT>() == 16) {
-        const uint32_t ppw = cols / 16u;  // K-quant rows are whole 256-weight blocks
+    constexpr int PW = piece_width<FMT, NT>();
+    if constexpr (PW > 8) {
+        const uint32_t ppw = cols / PW;  // K-quant rows are whole 256-weight blocks
         for (uint32_t base = tid; base < ppw; base += 256u * kPiecesInFlight) {
-            RawWide r[kPiecesInFlight][R];
+            RawWide r[kPiecesInFlight][R];  // PW-weight pieces
 #pragma unroll
             for (int u = 0; u < kPiecesInFlight; ++u) {
                 const uint32_t p = base + 256u * u;
@@ -523,30 +530,32 @@ __device__ __forceinline__ bool block_rows_dot(const uint8_t* rp, uint64_t rb, u
             for (int u = 0; u < kPiecesInFlight; ++u) {
                 const uint32_t p = base + 256u * u;
                 if (p >= ppw) break;
-                float xv[NT][16];
+                float xv[NT][PW];
                 float sx[NT];
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    const float* xp = xs[t] + 16u * p;
+                    const float* xp = xs[t] + (uint32_t)PW * p;
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
+                    for (int k = 0; k < PW / 4; ++k) {
                         const f32x4 v = t < (int)ntok ? *gp(reinterpret_cast<const f32x4*>(xp + 4 * k))
                                                       : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                         xv[t][4 * k] = v.x; xv[t][4 * k + 1] = v.y; xv[t][4 * k + 2] = v.z; xv[t][4 * k + 3] = v.w;
                     }
                     if constexpr (CHECK_X) {
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) bad_x |= !__builtin_isfinite(xv[t][i]);
+                        for (int i = 0; i < PW; ++i) bad_x |= !__builtin_isfinite(xv[t][i]);
                     }
-                    float h[8];
+                    float h[PW / 2];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) h[i] = xv[t][2 * i] + xv[t][2 * i + 1];
-                    sx[t] = ((h[0] + h[1]) + (h[2] + h[3])) + ((h[4] + h[5]) + (h[6] + h[7]));
+                    for (int i = 0; i < PW / 2; ++i) h[i] = xv[t][2 * i] + xv[t][2 * i + 1];
+                    sx[t] = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < PW / 2; ++i) sx[t] += h[i];
                 }
 #pragma unroll
                 for (uint32_t rr = 0; rr < R; ++rr) {
                     if (rr >= nrows) break;
-                    wide_dot<FMT, NT>(r[u][rr], p, xv, sx, acc[rr]);
+                    wide_dot<FMT, NT, PW>(r[u][rr], p, xv, sx, acc[rr]);
                 }
             }
         }

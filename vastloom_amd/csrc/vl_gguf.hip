@@ -310,13 +310,15 @@ __device__ __forceinline__ void piece_dot(const RawPiece& r, uint32_t p, const f
         float v[8];
         bytes_float((uint32_t)grid, v);
         bytes_float((uint32_t)(grid >> 32), v + 4);
+        // Sign bit i of the sign byte flips the sign of activation i.
+        uint32_t neg[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = (r.c >> i) & 1u ? -v[i] : v[i];
+        for (int i = 0; i < 8; ++i) neg[i] = (r.c << (31 - i)) & 0x80000000u;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             float d = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) d = fmaf(v[i], xv[t][i], d);
+            for (int i = 0; i < 8; ++i) d = fmaf(v[i], __uint_as_float(__float_as_uint(xv[t][i]) ^ neg[i]), d);
             acc[t] = fmaf(ls, d, acc[t]);
         }
     } else if constexpr (FMT == VL_TYPE_MXFP4) {

@@ -336,6 +336,33 @@ __global__ void __launch_bounds__(256) k_moe_logits_finish(const MoeShape s, con
     router_logit_store(s, in, w, (uint32_t)(i % s.experts), (uint32_t)(i / s.experts), sum);
 }
 
+// Grouped layers with many column slices (few tokens): one wave per logit. Lane l adds slices
+// l, l + 64, ... in order and the wave adds its 64 sums in a fixed butterfly order (lane 0's
+// result is kept), rounded to f32, with its score and selection key.
+__global__ void __launch_bounds__(256) k_moe_logits_finish_wave(const MoeShape s, const MoeInputs in,
+                                                                const MoeWorkspace w) {
+    const uint64_t n = (uint64_t)s.tokens * s.experts, i = (uint64_t)blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (i >= n) return;  // whole waves
+    const uint32_t lane = threadIdx.x & 63u;
+    const double* part = ws_ptr<const double>(w, w.off_lgpart);
+    double sum = 0.0;
+    for (uint32_t z = lane; z < w.lg_slices; z += 64u) sum += part[(uint64_t)z * n + i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (lane == 0) router_logit_store(s, in, w, (uint32_t)(i % s.experts), (uint32_t)(i / s.experts), sum);
+}
+
+// The router product's finishing launch: a wave per logit when there are 64 or more slices.
+static hipError_t launch_logits_finish(const MoeShape& s, const MoeInputs& in, const MoeWorkspace& w,
+                                       hipStream_t st) {
+    const uint64_t n = (uint64_t)s.tokens * s.experts;
+    if (w.lg_slices >= 64u)
+        hipLaunchKernelGGL(k_moe_logits_finish_wave, dim3((uint32_t)((n + 3u) / 4u)), dim3(256), 0, st, s, in, w);
+    else
+        hipLaunchKernelGGL(k_moe_logits_finish, dim3((uint32_t)((n + 255u) / 256u)), dim3(256), 0, st, s, in, w);
+    return hipGetLastError();
+}
+
 // Blocks b < R (R = experts, or 0 for caller-given routes): expert row b's logits for the tokens
 // of group g (tokens 8g .. 8g + 7). Blocks R + c: the limbs of column block c of the group's
 // tokens, in blocks of their own so that no routing block waits for them. Block (0, 0) zeroes the
@@ -1995,9 +2022,7 @@ static hipError_t launch_moe_grouped(const MoeShape& s, const MoeInputs& in, con
                            dim3((s.experts + kLgE - 1u) / kLgE, (s.tokens + kLgT - 1u) / kLgT, w.lg_slices),
                            dim3(256), 0, st, s, in, w);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        const uint64_t n = (uint64_t)s.tokens * s.experts;
-        hipLaunchKernelGGL(k_moe_logits_finish, dim3((uint32_t)((n + 255u) / 256u)), dim3(256), 0, st, s, in, w);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if ((e = launch_logits_finish(s, in, w, st)) != hipSuccess) return e;
     }
     hipLaunchKernelGGL(k_moe_route_many, dim3((s.tokens + kStreamWaves - 1u) / kStreamWaves),
                        dim3(kStreamThreads), 0, st, s, in, w);
@@ -2060,8 +2085,7 @@ hipError_t launch_moe_route(const MoeShape& s, const MoeInputs& in, const MoeWor
                            dim3((s.experts + kLgE - 1u) / kLgE, (s.tokens + kLgT - 1u) / kLgT, w.lg_slices),
                            dim3(256), 0, st, s, in, w);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        const uint64_t n = (uint64_t)s.tokens * s.experts;
-        hipLaunchKernelGGL(k_moe_logits_finish, dim3((uint32_t)((n + 255u) / 256u)), dim3(256), 0, st, s, in, w);
+        if ((e = launch_logits_finish(s, in, w, st)) != hipSuccess) return e;
     } else {
         hipLaunchKernelGGL(k_moe_router, dim3(s.experts + w.xblocks), dim3(256), 0, st, s, in, w);
     }
